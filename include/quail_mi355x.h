@@ -1,0 +1,167 @@
+/*
+ * quail_mi355x.h - C ABI of libquail_mi355x.so, the gfx950 (MI355X) kernels
+ * of Quail's packed-prompt prefill pass for Qwen3 FP8 models.
+ *
+ * Each entry point replaces one call on the reference's hot path; the
+ * comment above it cites the reference interface (paths relative to the
+ * fsdatalab/quail repository) whose result it reproduces.
+ *
+ * Conventions
+ *   - Pointers are device pointers; sizes and strides are int64 and count
+ *     elements of the pointed-to type (bytes for e4m3 data).
+ *   - Work is enqueued on `stream` and never synchronized; the caller keeps
+ *     every buffer alive until the stream has passed the call.
+ *   - bf16 is passed as raw 16-bit words; e4m3 as OCP e4m3fn bytes (max 448).
+ *   - FP8 activation scales are "column-major": the scale of token t and
+ *     128-column group g is at scales[g * s_ld + t] (attention.py:534-537).
+ *   - Return value: 0 on success; -1 for an argument error, with the
+ *     message in qx_last_error(); a positive hipError_t if the launch failed.
+ *   - The library allocates no memory and keeps no state between calls.
+ */
+#ifndef QUAIL_MI355X_H
+#define QUAIL_MI355X_H
+
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Library version (1). */
+int qx_version(void);
+
+/* Text of the last argument error on the calling thread. */
+const char* qx_last_error(void);
+
+/* 1 if the current HIP device is gfx950, 0 if not, <0 on a HIP error. */
+int qx_device_is_gfx950(void);
+
+/*
+ * FP8 block-scaled GEMM, bf16 output:
+ *   C[m,n] = sum_kb sA[kb*sa_ld + m] * sW[(n/128)*(K/128) + kb] * sum_{k in kb} A[m,k] W[n,k]
+ * Replaces Engine.gemm -> DeepGEMM fp8_gemm_nt((A, sA), (W, sW), C)
+ * (quail/backends/quail/executor/attention.py:479-490); weight scales are the
+ * checkpoint's weight_scale_inv (attention.py:471-477).
+ * K and N multiples of 128 (N of 256 for configs 0 and 1). config selects
+ * the tile shape (0: 128x256, 1: 256x256, 2: 128x128 tokens x weights).
+ */
+int qx_gemm_fp8_blockscaled(const void* A, const float* sA, const void* W, const float* sW,
+                            void* C, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldc,
+                            int64_t sa_ld, int config, hipStream_t stream);
+
+/*
+ * res <- bf16(x + res); y = (x + res) * rsqrt(mean((x+res)^2) + eps) * w in
+ * fp32; per-token 128-group e4m3 quant of y with scale max(amax,1e-10)/448.
+ * Replaces the Triton add_rms_norm_quant (attention.py:796-829) called from
+ * Engine.custom_norm_quant (attention.py:1098-1111).
+ */
+int qx_add_rmsnorm_quant(const void* x, int64_t x_ld, void* res, int64_t res_ld, const void* w,
+                         void* q, int64_t q_ld, float* scales, int64_t s_ld, int64_t n, int64_t H,
+                         float eps, hipStream_t stream);
+
+/*
+ * y = bf16(bf16(x * rstd) * w), then per-token 128-group e4m3 quant.
+ * Replaces Engine.norm_quant without a residual: vLLM rms_norm then
+ * per_token_group_quant_fp8 (attention.py:1237-1240, 539-556, 517-532).
+ */
+int qx_rmsnorm_quant(const void* x, int64_t x_ld, const void* w, void* q, int64_t q_ld,
+                     float* scales, int64_t s_ld, int64_t n, int64_t H, float eps,
+                     hipStream_t stream);
+
+/*
+ * res[i] = table[ids[i]] (bf16), then qx_rmsnorm_quant of that row: the
+ * embedding gather of Qwen3Pipeline.forward_chunk (qwen3.py:123) fused with
+ * layer 0's norm_quant (qwen3.py:47-49).
+ */
+int qx_embed_rmsnorm_quant(const void* table, int64_t t_ld, const int64_t* ids, void* res,
+                           int64_t res_ld, const void* w, void* q, int64_t q_ld, float* scales,
+                           int64_t s_ld, int64_t n, int64_t H, float eps, hipStream_t stream);
+
+/*
+ * vLLM fused_add_rms_norm (attention.py:558-562): z = bf16(h + r);
+ * res_out <- z; out = bf16(bf16(z * rstd) * w). With rows != NULL, output
+ * row i reads input row rows[i] (the final_indices gather of qwen3.py:130-134).
+ * out may alias h and res_out may alias r only when rows == NULL.
+ */
+int qx_add_rmsnorm(const void* h, int64_t h_ld, const void* r, int64_t r_ld, const int64_t* rows,
+                   const void* w, void* out, int64_t out_ld, void* res_out, int64_t res_out_ld,
+                   int64_t n, int64_t H, float eps, hipStream_t stream);
+
+/*
+ * Per-head RMSNorm of q (HQ heads) and k (HK heads) of the fused qkv rows,
+ * then neox RoPE from cos_sin[positions[i]] = [cos D/2 | sin D/2], fp32
+ * math, bf16 outputs. Replaces the Triton qk_norm_rope (attention.py:833-879)
+ * called from Engine.custom_qk_norm_rope (attention.py:1113-1128).
+ * cs_is_f32 selects an fp32 cache; otherwise it is bf16.
+ */
+int qx_qk_norm_rope(const void* qkv, int64_t qkv_ld, void* q_out, int64_t q_ld, void* k_out,
+                    int64_t k_ld, const void* cos_sin, int cs_is_f32, const int64_t* positions,
+                    const void* q_w, const void* k_w, int64_t n, int64_t HQ, int64_t HK,
+                    int64_t D, float eps, hipStream_t stream);
+
+/*
+ * y = g * sigmoid(g) * u over rows [g (I) | u (I)], fp32; per-token
+ * 128-group e4m3 quant. Replaces the Triton silu_mul_quant
+ * (attention.py:771-793) called from Engine.custom_silu_quant (:1084-1096).
+ */
+int qx_silu_mul_quant(const void* gate_up, int64_t gu_ld, void* q, int64_t q_ld, float* scales,
+                      int64_t s_ld, int64_t n, int64_t I, hipStream_t stream);
+
+/*
+ * Per-token 128-group e4m3 quant of bf16 rows. Replaces Engine.quant ->
+ * vLLM per_token_group_quant_fp8 (attention.py:517-532).
+ */
+int qx_group_quant(const void* x, int64_t x_ld, void* q, int64_t q_ld, float* scales,
+                   int64_t s_ld, int64_t n, int64_t K, hipStream_t stream);
+
+/*
+ * k_pool[dst[i]] = k[src[i]], v_pool[dst[i]] = v[src[i]] for rows of
+ * row_elems bf16; dst[i] < 0 writes nothing. Source rows have strides k_ld
+ * and v_ld (v may be the strided v slice of qkv). Replaces the Triton
+ * kv_row_scatter (attention.py:885-897) of Engine.kv_row_scatter /
+ * write_kv (attention.py:1165-1195), including its pool-to-pool tail copy.
+ */
+int qx_kv_scatter(const void* k, int64_t k_ld, const void* v, int64_t v_ld, void* k_pool,
+                  void* v_pool, const int64_t* src, const int64_t* dst, int64_t count,
+                  int64_t row_elems, hipStream_t stream);
+
+/* out[i] = table[ids[i]] (bf16 rows). Replaces vLLM embed_tokens (qwen3.py:123). */
+int qx_embed(const void* table, int64_t t_ld, const int64_t* ids, void* out, int64_t o_ld,
+             int64_t n, int64_t H, hipStream_t stream);
+
+/*
+ * Varlen GQA attention reading K/V through a block table: sequence s has
+ * query rows [cu_q[s], cu_q[s+1]) and keys [0, used[s]) at pool rows
+ * table[s*table_ld + j/page]*page + j%page; causal masking aligned
+ * bottom-right. Replaces Engine.attention_unified -> _paged ->
+ * flash_attn_varlen_func(..., block_table, seqused_k, causal)
+ * (attention.py:1477-1573, 1368-1393, 1280-1306). With out_fp8 it also
+ * performs Engine.quant of the bf16 result (attention.py:1274-1275): e4m3
+ * rows plus scales[h*s_ld + row] (one group per head, D == 128).
+ */
+int qx_paged_attention(const void* q, int64_t q_ld, const void* k_pool, const void* v_pool,
+                       const int* cu_q, const int* used, const int* table, int64_t table_ld,
+                       int64_t seqs, int64_t max_q, int64_t HQ, int64_t HK, int64_t D,
+                       int64_t page, float scale, int causal, void* out_bf16, void* out_fp8,
+                       int64_t o_ld, float* scales, int64_t s_ld, hipStream_t stream);
+
+/*
+ * Last-token answer head over the retained head rows (t <= 16):
+ * logits = normed . rows^T; mode 0 rounds logits to bf16 (AnswerRows.logits,
+ * AsyncLabelLogprobs normalize=False: readout.py:44-48, 188-191), mode 1
+ * keeps fp32 (AsyncScores: readout.py:331-336). With cls (1 yes, 0 no,
+ * -1 neither per row) it writes bits = max(yes) > max(no) (AI.IF),
+ * yes_no pairs, and score = sigmoid((yes - no) / temperature) (AI.SCORE).
+ * Any output pointer may be NULL.
+ */
+int qx_answer_head(const void* normed, int64_t n_ld, const void* rows, int64_t r_ld, int64_t t,
+                   int64_t n, int64_t H, int mode, const int* cls, float temperature,
+                   float* logits, uint8_t* bits, float* yes_no, float* score,
+                   hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* QUAIL_MI355X_H */

@@ -1,0 +1,212 @@
+"""Paged KV arena on the GPU: per-layer K and V pools in 16-token pages.
+
+The surface the packer and the attention path use, as the reference KVArena
+(quail/backends/quail/executor/arena.py:1-24, 35-147, 347-437, 522-563,
+644-648, 839-887) defines it for full-attention models: alloc / activate /
+alloc_temporary / free_key / pin / retain, residency queries, capacity_rows,
+layer_kv / paged_kv and block tables. Sliding-window pools and recurrent
+state slots (other model families) are not part of this engine.
+
+HBM layout: one allocation split [k0, v0, k1, v1, ...]; each pool is
+(num_pages * page_tokens, num_kv_heads, head_dim) bf16, so page p holds pool
+rows p*T .. p*T + T - 1 and a KV row is num_kv_heads * head_dim contiguous
+bf16 (2 KiB for Qwen3-4B). At 16 tokens a page is 32 KiB per layer and pool.
+"""
+
+import numpy as np
+import torch
+
+from quail_amd.pages import PageArena
+
+
+class KVArena:
+    def __init__(self, num_layers: int, num_pages: int, page_tokens: int, num_kv_heads: int,
+                 d_head: int, dtype=torch.bfloat16, device="cuda"):
+        self.torch = torch
+        self.dtype = dtype
+        self.device = device
+        self.num_layers = num_layers
+        self.kv_shape = (num_kv_heads, d_head)
+        self.sliding_layers = frozenset()
+        self.has_sliding = False
+        self.num_state_slots = 0
+        self._build(num_pages, page_tokens)
+        self.evicted_keys = 0
+        self.evicted_pages = 0
+        self.evicted_prefix_tokens = 0
+
+    def _build(self, num_pages, page_tokens):
+        heads, dim = self.kv_shape
+        self.accounting = PageArena(num_pages, page_tokens)
+        rows = num_pages * page_tokens
+        size = rows * heads * dim
+        storage = torch.empty(2 * self.num_layers * size, dtype=self.dtype, device=self.device)
+        parts = storage.split([size] * (2 * self.num_layers))
+        self.k = [p.view(rows, heads, dim) for p in parts[0::2]]
+        self.v = [p.view(rows, heads, dim) for p in parts[1::2]]
+        self._capacity_rows = {}
+        self._holds = {}
+        self._deferred = set()
+
+    # ---- sizes -------------------------------------------------------------
+
+    @property
+    def page_tokens(self) -> int:
+        return self.accounting.page_tokens
+
+    @property
+    def num_pages(self) -> int:
+        return self.accounting.num_pages
+
+    @property
+    def free_pages(self) -> int:
+        return self.accounting.free_pages
+
+    @property
+    def retained_pages(self) -> int:
+        return self.accounting.retained_pages
+
+    def pages_needed(self, tokens: int) -> int:
+        return self.accounting.pages_needed(tokens)
+
+    def page_cost(self, tokens: int, sliding_tokens: int = 0) -> int:
+        return self.accounting.pages_needed(tokens)
+
+    # ---- residency ---------------------------------------------------------
+
+    def is_resident(self, key) -> bool:
+        return key in self.accounting.owned
+
+    def resident_keys(self):
+        return list(self.accounting.owned)
+
+    def owned_pages(self, key) -> list:
+        """The page ids the key's block table reads: borrowed, then its own."""
+        return self.accounting.table_pages(key)
+
+    def tokens(self, key) -> int:
+        return self.accounting.tokens[key]
+
+    def _refresh_rows(self, key):
+        pages = np.asarray(self.accounting.table_pages(key), dtype=np.int64)
+        t = self.page_tokens
+        self._capacity_rows[key] = (pages[:, None] * t + np.arange(t, dtype=np.int64)).reshape(-1)
+
+    def capacity_rows(self, key) -> np.ndarray:
+        """Pool row of every row in the key's pages, in logical order (host int64)."""
+        return self._capacity_rows[key]
+
+    # ---- allocation ----------------------------------------------------------
+
+    def _borrow_plan(self, borrow):
+        if borrow is None:
+            return []
+        parent, shared = borrow
+        return self.accounting.shared_pages(parent, shared)
+
+    def can_borrow(self, parent, shared: int) -> bool:
+        acct = self.accounting
+        return parent in acct.owned and shared <= acct.tokens[parent]
+
+    def alloc(self, key, tokens: int, capacity_tokens=None, base_tokens=None, borrow=None):
+        """Pages for a fresh key, or None when the free list is short.
+        borrow = (parent key, shared tokens): the key reads the parent's
+        first pages as its own leading pages."""
+        pages = self.accounting.alloc(key, tokens, capacity_tokens,
+                                      borrowed=self._borrow_plan(borrow))
+        if pages is None:
+            return None
+        self._refresh_rows(key)
+        return pages
+
+    def _evict_for_pages(self, need: int) -> None:
+        acct = self.accounting
+        while need > acct.free_pages:
+            victim = acct.pop_retained_victim(keep=frozenset(self._holds))
+            if victim is None:
+                return
+            key, pages, tokens = victim
+            self.evicted_keys += 1
+            self.evicted_prefix_tokens += tokens
+            self.evicted_pages += acct.free_key(key)
+            self._capacity_rows.pop(key, None)
+
+    def activate(self, key, tokens: int, capacity_tokens=None, base_tokens=None, borrow=None):
+        """Make a prefix active (pinned), evicting retained KV when needed."""
+        acct = self.accounting
+        capacity = tokens if capacity_tokens is None else capacity_tokens
+        if key in acct.owned:
+            acct.pin(key)
+            need = max(0, acct.pages_needed(capacity) - len(acct.table_pages(key)))
+            self._evict_for_pages(need)
+            if need > acct.free_pages:
+                return None
+            acct.grow(key, capacity)
+            acct.tokens[key] = tokens
+            self._refresh_rows(key)
+            return acct.owned[key]
+        borrowed = self._borrow_plan(borrow)
+        self._evict_for_pages(acct.pages_needed(capacity) - len(borrowed))
+        pages = self.alloc(key, tokens, capacity, base_tokens, borrow=borrow)
+        if pages is not None:
+            acct.pin(key)
+        return pages
+
+    def alloc_temporary(self, tokens: int, sliding_tokens=None):
+        key = object()
+        pages = self.alloc(key, tokens, base_tokens=0)
+        return None if pages is None else (key, pages)
+
+    def free_key(self, key) -> int:
+        """Free a key's pages; a key with queued borrowers waits for them."""
+        if self._holds.get(key):
+            self._deferred.add(key)
+            return 0
+        self._capacity_rows.pop(key, None)
+        return self.accounting.free_key(key)
+
+    def pin(self, key) -> None:
+        self.accounting.pin(key)
+
+    def retain(self, key, priority=None) -> None:
+        self.accounting.retain(key, priority)
+
+    def hold(self, key, borrowers: int) -> None:
+        if borrowers:
+            self._holds[key] = self._holds.get(key, 0) + borrowers
+
+    def release(self, key) -> None:
+        if key not in self._holds:
+            return
+        self._holds[key] -= 1
+        if not self._holds[key]:
+            del self._holds[key]
+            if key in self._deferred:
+                self._deferred.discard(key)
+                self.free_key(key)
+
+    # ---- tensors read by attention ---------------------------------------------
+
+    def layer_kv(self, layer: int):
+        """Flat K and V pools of one layer: (rows, num_kv_heads, head_dim)."""
+        return self.k[layer], self.v[layer]
+
+    def paged_kv(self, layer: int):
+        heads, dim = self.kv_shape
+        shape = (-1, self.page_tokens, heads, dim)
+        return self.k[layer].view(shape), self.v[layer].view(shape)
+
+    def block_table_rows(self, pages, pad_to=None) -> np.ndarray:
+        """(len(pages), width) int32 table, each row zero-padded on the right."""
+        width = max(len(p) for p in pages)
+        if pad_to:
+            width = max(width, pad_to)
+        table = np.zeros((len(pages), width), dtype=np.int32)
+        for row, p in enumerate(pages):
+            table[row, :len(p)] = p
+        return table
+
+    def block_table(self, keys, pad_to=None):
+        table = self.block_table_rows([self.owned_pages(k) for k in keys], pad_to)
+        used = np.asarray([self.accounting.tokens[k] for k in keys], dtype=np.int32)
+        return table, used

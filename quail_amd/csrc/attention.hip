@@ -1,0 +1,307 @@
+// Paged varlen causal GQA attention over the KV arena, with the o_proj input
+// quantization fused into the epilogue. Replaces the FlashAttention varlen
+// call of quail/backends/quail/executor/attention.py:1280-1306 (reached from
+// attention_unified :1558-1563 through _paged :1368-1393) followed by the
+// per-token group quant of :1274-1275.
+//
+// Semantics (FA varlen with block_table and seqused_k):
+//   sequence s owns query rows [cu_q[s], cu_q[s+1]) and reads keys [0, used[s])
+//   through table[s] (page ids, `page` tokens per page). With causal masking
+//   the alignment is bottom-right: query i (0-based in s) of a sequence with
+//   q_len rows sees keys < used[s] - q_len + i + 1. Scale 1/sqrt(D) by default.
+//   GQA: query head h reads KV head h / (HQ / HK).
+//   Pools: k_pool, v_pool are (pages * page, HK, D) bf16.
+//
+// Output: bf16 (n, HQ*D), or with D == 128 the e4m3 o_proj input (n, HQ*D)
+// plus fp32 scales at scales[h * s_ld + row] (one 128-group = one head),
+// computed from the bf16-rounded attention output exactly as the reference's
+// separate quant kernel would see it.
+//
+// Kernel layout (CDNA4): a workgroup = one 32-row query tile of one sequence
+// x NW query heads that share a KV head (one wave per head). KV is consumed
+// in 64-key tiles staged in LDS (K row-major, V transposed). Each wave forms
+// S^T = K Q^T with v_mfma_f32_32x32x16_bf16 so that a lane owns one query
+// column; the online softmax is then lane-local (plus one cross-half
+// shuffle), P^T feeds the PV MFMA directly as its B operand, and O^T keeps
+// one query per lane, so rescaling needs no shuffles. P enters the PV MFMA as
+// a bf16 hi/lo pair, so the output carries fp32-level accuracy.
+#include "qx_common.h"
+#include "qx_status.h"
+
+namespace qx {
+namespace {
+
+constexpr int kBQ = 32;   // query rows per wave
+constexpr int kBK = 64;   // keys per KV tile
+
+// position of key k (0..15) inside its 16-key group of the transposed V tile:
+// the 8 keys one MFMA lane-half consumes become contiguous
+__device__ __forceinline__ int vt_pos(int k) { return ((k >> 2) & 1) * 8 + (k >> 3) * 4 + (k & 3); }
+
+template <int D, int NW, bool QUANT>
+__global__ __launch_bounds__(NW * 64) void paged_attention_kernel(
+    const uint16_t* __restrict__ q, int64_t q_ld, const uint16_t* __restrict__ kp,
+    const uint16_t* __restrict__ vp, const int* __restrict__ cu_q, const int* __restrict__ used,
+    const int* __restrict__ table, int64_t table_ld, int HQ, int HK, int page, float scale_log2,
+    int causal, uint16_t* __restrict__ out16, uint8_t* __restrict__ out8, int64_t o_ld,
+    float* __restrict__ scales, int64_t s_ld) {
+  constexpr int NT = NW * 64;
+  constexpr int ND16 = D / 16;   // MFMA k-steps over the head dim
+  constexpr int NDS = D / 32;    // 32-row d tiles of O^T
+  constexpr int KCH = D / 8;     // 16-byte chunks per K row
+  constexpr int K_BYTES = kBK * D * 2;
+  __shared__ __attribute__((aligned(16))) uint8_t k_lds[K_BYTES];
+  __shared__ __attribute__((aligned(16))) uint8_t vt_lds[D * kBK * 2];
+
+  const int s = blockIdx.y;
+  const int qt = gridDim.x - 1 - blockIdx.x;  // heavy (late) tiles first
+  const int q0 = cu_q[s];
+  const int q_len = cu_q[s + 1] - q0;
+  if (qt * kBQ >= q_len) return;
+  const int G = HQ / HK;
+  const int groups_per_kv = G / NW;
+  const int kvh = blockIdx.z / groups_per_kv;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int head = kvh * G + (blockIdx.z % groups_per_kv) * NW + wave;
+  const int half = lane >> 5;
+  const int col = lane & 31;
+
+  const int used_s = used[s];
+  const int off = causal ? used_s - q_len : 0;
+  const int r = qt * kBQ + col;  // this lane's query row within the sequence
+  const bool r_ok = r < q_len;
+  const int last_row = min(qt * kBQ + kBQ, q_len) - 1;
+  const int kv_end = causal ? min(used_s, off + last_row + 1) : used_s;
+  const int* trow = table + (int64_t)s * table_ld;
+
+  // Q^T fragments (B operand): lane holds query `col`, d = c*16 + half*8 .. +8
+  v8s qf[ND16];
+  {
+    const int rr = r_ok ? r : q_len - 1;
+    const uint16_t* qrow = q + (int64_t)(q0 + rr) * q_ld + head * D;
+#pragma unroll
+    for (int c = 0; c < ND16; ++c) qf[c] = *reinterpret_cast<const v8s*>(qrow + c * 16 + half * 8);
+  }
+
+  v16f o[NDS];
+#pragma unroll
+  for (int d = 0; d < NDS; ++d)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) o[d][e] = 0.f;
+  float m_run = -INFINITY, l_run = 0.f;
+  const int64_t kv_row = (int64_t)HK * D;  // elements per pool row
+
+  for (int t0 = 0; t0 < kv_end; t0 += kBK) {
+    // ---- stage K (row-major, chunk-swizzled) and V^T into LDS ----------
+    for (int u = tid; u < kBK * KCH; u += NT) {
+      const int key = u / KCH, c = u % KCH;
+      int kidx = t0 + key;
+      kidx = kidx < kv_end ? kidx : kv_end - 1;
+      const int64_t prow = (int64_t)trow[kidx / page] * page + (kidx % page);
+      const uint4 val = *reinterpret_cast<const uint4*>(kp + prow * kv_row + kvh * D + c * 8);
+      *reinterpret_cast<uint4*>(k_lds + key * (D * 2) + ((c ^ (key & 7)) * 16)) = val;
+    }
+    for (int u = tid; u < (kBK / 2) * KCH; u += NT) {
+      const int kp2 = u / KCH, dc = u % KCH;
+      const int key = kp2 * 2;
+      int k0 = t0 + key, k1 = k0 + 1;
+      k0 = k0 < kv_end ? k0 : kv_end - 1;
+      k1 = k1 < kv_end ? k1 : kv_end - 1;
+      const int64_t p0 = (int64_t)trow[k0 / page] * page + (k0 % page);
+      const int64_t p1 = (int64_t)trow[k1 / page] * page + (k1 % page);
+      const uint4 a = *reinterpret_cast<const uint4*>(vp + p0 * kv_row + kvh * D + dc * 8);
+      const uint4 b = *reinterpret_cast<const uint4*>(vp + p1 * kv_row + kvh * D + dc * 8);
+      const uint32_t aw[4] = {a.x, a.y, a.z, a.w}, bw[4] = {b.x, b.y, b.z, b.w};
+      const int pos = (key >> 4) * 16 + vt_pos(key & 15);  // even; pos+1 holds key+1
+      const int chunk = pos >> 3, within = (pos & 7) * 2;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int d = dc * 8 + e;
+        const uint32_t lo = (e & 1) ? (aw[e >> 1] >> 16) : (aw[e >> 1] & 0xffffu);
+        const uint32_t hi = (e & 1) ? (bw[e >> 1] >> 16) : (bw[e >> 1] & 0xffffu);
+        *reinterpret_cast<uint32_t*>(vt_lds + d * (kBK * 2) + ((chunk ^ (d & 7)) * 16) + within) =
+            lo | (hi << 16);
+      }
+    }
+    __syncthreads();
+
+    // ---- S^T = K Q^T for two 32-key subtiles ---------------------------
+    v16f sacc[2];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      v16f a = {};
+      const int key = ks * 32 + col;
+#pragma unroll
+      for (int c = 0; c < ND16; ++c) {
+        const int lc = 2 * c + half;
+        const v8s kf = *reinterpret_cast<const v8s*>(k_lds + key * (D * 2) + ((lc ^ (key & 7)) * 16));
+        a = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, kf),
+                                                    __builtin_bit_cast(v8bf, qf[c]), a, 0, 0, 0);
+      }
+      sacc[ks] = a;
+    }
+
+    // ---- mask, online softmax (lane = one query; partner lane^32) -------
+    const int lim = causal ? min(off + r + 1, used_s) : used_s;  // keys < lim are visible
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int kidx = t0 + ks * 32 + (i >> 2) * 8 + half * 4 + (i & 3);
+        float v = sacc[ks][i] * scale_log2;
+        v = (kidx < lim && r_ok) ? v : -INFINITY;
+        sacc[ks][i] = v;
+        tmax = fmaxf(tmax, v);
+      }
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+    const float m_new = fmaxf(m_run, tmax);
+    const float m_use = m_new == -INFINITY ? 0.f : m_new;
+    const float alpha = exp2f(m_run - m_use);
+    // P is split into bf16 hi + lo parts (P = hi + lo to ~16 mantissa bits),
+    // so the PV product keeps fp32-level accuracy on bf16 MFMAs.
+    float psum = 0.f;
+    v8s pf[4], pl[4];
+#pragma unroll
+    for (int kc = 0; kc < 4; ++kc) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float pv = exp2f(sacc[kc >> 1][(kc & 1) * 8 + j] - m_use);
+        psum += pv;
+        const uint16_t hi = f32_to_bf16(pv);
+        pf[kc][j] = (short)hi;
+        pl[kc][j] = (short)f32_to_bf16(pv - bf16_to_f32(hi));
+      }
+    }
+    psum += __shfl_xor(psum, 32, 64);
+    l_run = l_run * alpha + psum;
+    m_run = m_new;
+#pragma unroll
+    for (int d = 0; d < NDS; ++d)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) o[d][e] *= alpha;
+
+    // ---- O^T += V^T P^T --------------------------------------------------
+#pragma unroll
+    for (int d = 0; d < NDS; ++d) {
+      const int dr = d * 32 + col;
+#pragma unroll
+      for (int kc = 0; kc < 4; ++kc) {
+        const int lc = 2 * kc + half;
+        const v8s vf = *reinterpret_cast<const v8s*>(vt_lds + dr * (kBK * 2) + ((lc ^ (dr & 7)) * 16));
+        o[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, vf),
+                                                       __builtin_bit_cast(v8bf, pf[kc]), o[d], 0, 0, 0);
+        o[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, vf),
+                                                       __builtin_bit_cast(v8bf, pl[kc]), o[d], 0, 0, 0);
+      }
+    }
+    __syncthreads();
+  }
+
+  // ---- epilogue: lane holds query `col`, d = dt*32 + (i/4)*8 + half*4 + i%4
+  const float inv = l_run > 0.f ? 1.0f / l_run : 0.f;
+  const int64_t row = q0 + r;
+  if (QUANT) {
+    float amax = 0.f;
+#pragma unroll
+    for (int d = 0; d < NDS; ++d)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const float v = round_bf16(o[d][e] * inv);
+        o[d][e] = v;
+        amax = fmaxf(amax, fabsf(v));
+      }
+    amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
+    const float sc = fp8_scale(amax);
+    if (r_ok) {
+      uint8_t* orow = out8 + row * o_ld + head * D;
+#pragma unroll
+      for (int d = 0; d < NDS; ++d)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int dd = d * 32 + g * 8 + half * 4;
+          *reinterpret_cast<uint32_t*>(orow + dd) =
+              pack4_fp8(o[d][g * 4] / sc, o[d][g * 4 + 1] / sc, o[d][g * 4 + 2] / sc, o[d][g * 4 + 3] / sc);
+        }
+      if (half == 0) scales[(int64_t)head * s_ld + row] = sc;
+    }
+  } else if (r_ok) {
+    uint16_t* orow = out16 + row * o_ld + head * D;
+#pragma unroll
+    for (int d = 0; d < NDS; ++d)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int dd = d * 32 + g * 8 + half * 4;
+        *reinterpret_cast<uint2*>(orow + dd) =
+            make_uint2(pack2_bf16(o[d][g * 4] * inv, o[d][g * 4 + 1] * inv),
+                       pack2_bf16(o[d][g * 4 + 2] * inv, o[d][g * 4 + 3] * inv));
+      }
+  }
+}
+
+template <int D, int NW>
+int launch_attn(const void* q, int64_t q_ld, const void* kp, const void* vp, const int* cu_q,
+                const int* used, const int* table, int64_t table_ld, int seqs, int max_q, int HQ,
+                int HK, int page, float scale, int causal, void* out16, void* out8, int64_t o_ld,
+                float* scales, int64_t s_ld, hipStream_t stream) {
+  const int G = HQ / HK;
+  dim3 grid((max_q + kBQ - 1) / kBQ, seqs, HK * (G / NW));
+  const float scale_log2 = scale * 1.4426950408889634f;
+  if (out8) {
+    hipLaunchKernelGGL((paged_attention_kernel<D, NW, true>), grid, dim3(NW * 64), 0, stream,
+                       (const uint16_t*)q, q_ld, (const uint16_t*)kp, (const uint16_t*)vp, cu_q,
+                       used, table, table_ld, HQ, HK, page, scale_log2, causal, nullptr,
+                       (uint8_t*)out8, o_ld, scales, s_ld);
+  } else {
+    hipLaunchKernelGGL((paged_attention_kernel<D, NW, false>), grid, dim3(NW * 64), 0, stream,
+                       (const uint16_t*)q, q_ld, (const uint16_t*)kp, (const uint16_t*)vp, cu_q,
+                       used, table, table_ld, HQ, HK, page, scale_log2, causal,
+                       (uint16_t*)out16, nullptr, o_ld, nullptr, 0);
+  }
+  QX_LAUNCH_STATUS();
+}
+
+}  // namespace
+}  // namespace qx
+
+extern "C" {
+
+// out_fp8 != NULL: write the e4m3 o_proj input and its scales (D must be
+// 128); otherwise write bf16 to out_bf16. o_ld is in elements of the output.
+int qx_paged_attention(const void* q, int64_t q_ld, const void* k_pool, const void* v_pool,
+                       const int* cu_q, const int* used, const int* table, int64_t table_ld,
+                       int64_t seqs, int64_t max_q, int64_t HQ, int64_t HK, int64_t D,
+                       int64_t page, float scale, int causal, void* out_bf16, void* out_fp8,
+                       int64_t o_ld, float* scales, int64_t s_ld, hipStream_t stream) {
+  QX_CHECK(q && k_pool && v_pool && cu_q && used && table, "attention: null pointer");
+  QX_CHECK(out_bf16 || out_fp8, "attention: no output");
+  QX_CHECK(D == 64 || D == 128, "attention: head_dim %lld", (long long)D);
+  QX_CHECK(HQ > 0 && HK > 0 && HQ % HK == 0, "attention: heads %lld/%lld", (long long)HQ,
+           (long long)HK);
+  QX_CHECK(page > 0, "attention: page");
+  QX_CHECK(q_ld % 8 == 0 && o_ld % 4 == 0, "attention: strides");
+  QX_CHECK(!out_fp8 || (D == 128 && scales), "attention: fused quant needs D=128 and scales");
+  QX_CHECK(seqs < 65536, "attention: %lld sequences exceed the grid", (long long)seqs);
+  if (seqs == 0 || max_q == 0) return QX_OK;
+  const int G = (int)(HQ / HK);
+  const int nw = G % 4 == 0 ? 4 : (G % 2 == 0 ? 2 : 1);
+  const int args_seqs = (int)seqs, args_mq = (int)max_q;
+#define QX_ATTN(DD, NW_)                                                                     \
+  return qx::launch_attn<DD, NW_>(q, q_ld, k_pool, v_pool, cu_q, used, table, table_ld,      \
+                                  args_seqs, args_mq, (int)HQ, (int)HK, (int)page, scale,    \
+                                  causal, out_bf16, out_fp8, o_ld, scales, s_ld, stream)
+  if (D == 128) {
+    if (nw == 4) QX_ATTN(128, 4);
+    if (nw == 2) QX_ATTN(128, 2);
+    QX_ATTN(128, 1);
+  } else {
+    if (nw == 4) QX_ATTN(64, 4);
+    if (nw == 2) QX_ATTN(64, 2);
+    QX_ATTN(64, 1);
+  }
+#undef QX_ATTN
+}
+
+}  // extern "C"

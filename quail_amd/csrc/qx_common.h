@@ -1,0 +1,96 @@
+// Device helpers shared by the gfx950 kernels of libquail_mi355x.
+//
+// Number formats follow the reference's arithmetic:
+//   * bf16 is stored as uint16_t and rounded from fp32 to nearest even, as
+//     torch's `.to(torch.bfloat16)` and Triton's `.to(tl.bfloat16)` do.
+//   * FP8 is OCP e4m3fn (max 448), the format of Qwen3 FP8 checkpoints
+//     (quail/specs/qwen3.py:16). Values are clamped to +-448 before the
+//     hardware round-to-nearest-even conversion, which is the reference's
+//     `clamp(x / s, -448, 448).to(e4m3)` (attention.py:782-786).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace qx {
+
+constexpr float kFp8Max = 448.0f;
+constexpr float kScaleFloor = 1e-10f;  // attention.py:781 `max(amax, 1e-10)`
+constexpr int kGroup = 128;            // per-token FP8 group (attention.py GROUP)
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef short v8s __attribute__((ext_vector_type(8)));
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) {
+  return __uint_as_float(static_cast<uint32_t>(h) << 16);
+}
+
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0;  // NaN stays NaN
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+// Round an fp32 value through bf16 and back (the reference stores bf16
+// intermediates between kernels).
+__device__ __forceinline__ float round_bf16(float f) {
+  return bf16_to_f32(f32_to_bf16(f));
+}
+
+// Four fp32 values -> four packed e4m3fn bytes (little-endian order), with
+// the clamp to +-448 applied first.
+__device__ __forceinline__ uint32_t pack4_fp8(float a, float b, float c, float d) {
+  a = fminf(fmaxf(a, -kFp8Max), kFp8Max);
+  b = fminf(fmaxf(b, -kFp8Max), kFp8Max);
+  c = fminf(fmaxf(c, -kFp8Max), kFp8Max);
+  d = fminf(fmaxf(d, -kFp8Max), kFp8Max);
+  int v = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+  v = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, v, true);
+  return static_cast<uint32_t>(v);
+}
+
+// Unpack two bf16 held in one 32-bit word.
+__device__ __forceinline__ float lo_bf16(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float hi_bf16(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+__device__ __forceinline__ uint32_t pack2_bf16(float lo, float hi) {
+  return static_cast<uint32_t>(f32_to_bf16(lo)) | (static_cast<uint32_t>(f32_to_bf16(hi)) << 16);
+}
+
+// Butterfly reductions across `width` consecutive lanes of a wave64.
+template <int width>
+__device__ __forceinline__ float group_max(float v) {
+#pragma unroll
+  for (int o = width / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+template <int width>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+  for (int o = width / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+// Per-group FP8 scale: max(amax, 1e-10) / 448 (attention.py:780-781).
+__device__ __forceinline__ float fp8_scale(float amax) {
+  return fmaxf(amax, kScaleFloor) / kFp8Max;
+}
+
+}  // namespace qx
+
+// Status codes of every extern "C" entry point.
+#define QX_OK 0
+#define QX_EINVAL (-1)
+
+// Record a launch error (if any) as the entry point's return value.
+#define QX_LAUNCH_STATUS()                          \
+  do {                                              \
+    hipError_t _e = hipGetLastError();              \
+    return _e == hipSuccess ? QX_OK : (int)_e;      \
+  } while (0)

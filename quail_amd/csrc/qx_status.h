@@ -1,0 +1,15 @@
+// Error text for the extern "C" entry points: each returns QX_OK (0),
+// QX_EINVAL (-1) after recording a message here, or a positive hipError_t.
+#pragma once
+
+namespace qx {
+void set_error(const char* fmt, ...);
+}
+
+#define QX_CHECK(cond, ...)        \
+  do {                             \
+    if (!(cond)) {                 \
+      qx::set_error(__VA_ARGS__);  \
+      return QX_EINVAL;            \
+    }                              \
+  } while (0)

@@ -1,0 +1,319 @@
+"""Engine: the kernel primitives of the prefill pass, on gfx950 HIP kernels.
+
+This mirrors the primitive surface of the reference Engine
+(quail/backends/quail/executor/attention.py:432-562, 1235-1275): norm_quant,
+gemm, qk_norm_rope, attention, activation_quant, quant, fused_add_rms_norm,
+write_kv and kv_row_scatter, with the same arguments, return values and
+in-place updates, so a pipeline written against the reference Engine runs
+unchanged. Every primitive launches hand-written kernels of
+libquail_mi355x.so through its C ABI on torch's current stream; tensors are
+torch-allocated (the library allocates nothing). There is no CPU or
+PyTorch fallback: without the native library the primitives raise.
+
+Layouts are the reference's: FP8 activations are e4m3fn (n, K) with
+"column-major" fp32 scales, a (K/128, n) tensor viewed as (n, K/128)
+(attention.py:534-537); weights are e4m3 (N, K) with weight_scale_inv
+(N/128, K/128).
+"""
+
+import os
+
+import torch
+
+from quail_amd import _lib
+
+GROUP = 128
+
+# GEMM tile configuration per (N, K): 0 = 128 tokens x 256 weights,
+# 1 = 256 x 256, 2 = 128 x 128 (see csrc/gemm_fp8.hip). Weight widths that
+# are not multiples of 256 use 2.
+GEMM_CONFIG_ENV = "QUAIL_GEMM_CONFIG"
+
+
+def _ptr(t):
+    return None if t is None else t.data_ptr()
+
+
+def _stream():
+    return torch.cuda.current_stream().cuda_stream
+
+
+def gemm_config(n: int, k: int, m: int) -> int:
+    forced = os.environ.get(GEMM_CONFIG_ENV)
+    if forced is not None:
+        return int(forced)
+    if n % 256:
+        return 2
+    return 0
+
+
+class Engine:
+    """Kernels, quantization and paged attention over the KV arena.
+
+    Args:
+        arena: KVArena the attention path reads and writes.
+        num_q_heads, num_kv_heads, head_dim: attention geometry.
+        rotary: the model's rotary module (its `cos_sin_cache`).
+        fp8: whether the linear weights are fp8 block-quantized; this engine
+            runs FP8 checkpoints only.
+        kernels: "quail" or "vllm" (accepted for interface parity; both
+            select the fused HIP kernels).
+    """
+
+    def __init__(self, arena, *, num_q_heads, num_kv_heads, head_dim, rotary, fp8=True,
+                 kernels="quail"):
+        if kernels not in ("quail", "vllm"):
+            raise ValueError(f"kernels must be 'quail' or 'vllm', got {kernels!r}")
+        if not fp8:
+            raise ValueError("this engine runs FP8 block-quantized checkpoints only")
+        lib = _lib.load()
+        if lib.qx_device_is_gfx950() != 1:
+            raise RuntimeError("the quail_amd engine needs a gfx950 (MI350/MI355X) device")
+        self.kernels = kernels
+        self.torch = torch
+        self.arena = arena
+        self.rotary = rotary
+        self.num_q_heads = num_q_heads
+        self.num_kv_heads = num_kv_heads
+        self.head_dim = head_dim
+        self.fp8 = torch.float8_e4m3fn
+        self.is_fp8 = True
+        self.use_ue8m0 = False
+
+    # ---- weights and quant --------------------------------------------
+
+    @staticmethod
+    def weight_scale(linear):
+        for name in ("weight_scale", "weight_scale_inv"):
+            scale = getattr(linear, name, None)
+            if scale is not None:
+                return scale
+        raise AttributeError(f"no weight scale on {type(linear).__name__}")
+
+    def _col_major_scales(self, num_tokens, width, device="cuda"):
+        return torch.empty((width // GROUP, num_tokens), dtype=torch.float32,
+                           device=device).permute(1, 0)
+
+    @staticmethod
+    def _scale_ld(scales):
+        # a (tokens, groups) view of (groups, tokens) storage: group stride
+        return scales.stride(1) if scales.dim() == 2 else scales.shape[0]
+
+    def gemm(self, q_input, input_scale, linear, out=None):
+        """bf16 q_input @ W^T with the FP8 block scales applied per 128 of K."""
+        w = linear.weight
+        sw = self.weight_scale(linear)
+        m, k = q_input.shape
+        n = w.shape[0]
+        if w.shape[1] != k:
+            raise ValueError(f"gemm: input width {k} vs weight {tuple(w.shape)}")
+        if input_scale.shape != (m, k // GROUP) or input_scale.stride(0) != 1:
+            raise ValueError("gemm: activation scales must be the (tokens, K/128) view of "
+                             "column-major storage")
+        if out is None:
+            out = torch.empty((m, n), dtype=torch.bfloat16, device=q_input.device)
+        _lib.call("qx_gemm_fp8_blockscaled", _ptr(q_input), _ptr(input_scale), _ptr(w),
+                  _ptr(sw), _ptr(out), m, n, k, q_input.stride(0), out.stride(0),
+                  self._scale_ld(input_scale), gemm_config(n, k, m), _stream())
+        return out
+
+    def quant(self, x, *, output=None):
+        """Per-token 128-group FP8 of bf16 rows: (e4m3 rows, col-major scales)."""
+        n, k = x.shape
+        if output is not None:
+            q, scales = output
+        else:
+            q = torch.empty((n, k), dtype=self.fp8, device=x.device)
+            scales = self._col_major_scales(n, k, x.device)
+        _lib.call("qx_group_quant", _ptr(x), x.stride(0), _ptr(q), q.stride(0), _ptr(scales),
+                  self._scale_ld(scales), n, k, _stream())
+        return q, scales
+
+    def rms_norm(self, x, norm):
+        return self.norm_rows(x, norm.weight, norm.variance_epsilon)
+
+    def norm_rows(self, x, weight, eps):
+        """vLLM rms_norm of the last dimension: bf16(bf16(x * rstd) * w)."""
+        width = x.shape[-1]
+        rows = x.reshape(-1, width)
+        if not rows.is_contiguous():
+            rows = rows.contiguous()
+        out = torch.empty_like(rows)
+        # z = x + 0 leaves x; the residual copy goes to a scratch row set
+        zeros = torch.zeros_like(rows)
+        _lib.call("qx_add_rmsnorm", _ptr(rows), rows.stride(0), _ptr(zeros), zeros.stride(0),
+                  None, _ptr(weight), _ptr(out), out.stride(0), None, 0, rows.shape[0],
+                  width, float(eps), _stream())
+        return out.view(x.shape)
+
+    def fused_add_rms_norm(self, hidden, residual, norm):
+        """In place, as vLLM: residual <- bf16(hidden + residual);
+        hidden <- rms_norm(residual). Returns (hidden, residual)."""
+        n, h = hidden.shape
+        _lib.call("qx_add_rmsnorm", _ptr(hidden), hidden.stride(0), _ptr(residual),
+                  residual.stride(0), None, _ptr(norm.weight), _ptr(hidden), hidden.stride(0),
+                  _ptr(residual), residual.stride(0), n, h, float(norm.variance_epsilon),
+                  _stream())
+        return hidden, residual
+
+    def final_norm(self, hidden, residual, final_indices, norm):
+        """fused_add_rms_norm of the rows final_indices selects, gathered in
+        the same kernel (qwen3.py:130-134); returns the normed rows."""
+        rows = final_indices.shape[0]
+        h = hidden.shape[1]
+        out = torch.empty((rows, h), dtype=torch.bfloat16, device=hidden.device)
+        _lib.call("qx_add_rmsnorm", _ptr(hidden), hidden.stride(0), _ptr(residual),
+                  residual.stride(0), _ptr(final_indices), _ptr(norm.weight), _ptr(out),
+                  out.stride(0), None, 0, rows, h, float(norm.variance_epsilon), _stream())
+        return out
+
+    # ---- the primitives a forward loop calls ---------------------------
+
+    def norm_quant(self, hidden, norm, residual=None):
+        """RMS-normed, quantized GEMM input; adds the residual first when given."""
+        n, h = hidden.shape
+        q = torch.empty((n, h), dtype=self.fp8, device=hidden.device)
+        scales = self._col_major_scales(n, h, hidden.device)
+        eps = float(norm.variance_epsilon)
+        if residual is None:
+            _lib.call("qx_rmsnorm_quant", _ptr(hidden), hidden.stride(0), _ptr(norm.weight),
+                      _ptr(q), q.stride(0), _ptr(scales), self._scale_ld(scales), n, h, eps,
+                      _stream())
+        else:
+            _lib.call("qx_add_rmsnorm_quant", _ptr(hidden), hidden.stride(0), _ptr(residual),
+                      residual.stride(0), _ptr(norm.weight), _ptr(q), q.stride(0), _ptr(scales),
+                      self._scale_ld(scales), n, h, eps, _stream())
+        return q, scales
+
+    def embed_norm_quant(self, ids, embed_weight, norm):
+        """Embedding gather fused with layer 0's norm_quant: returns
+        (q, scales, residual) where residual holds the embedded rows."""
+        n = ids.shape[0]
+        h = embed_weight.shape[1]
+        residual = torch.empty((n, h), dtype=torch.bfloat16, device=ids.device)
+        q = torch.empty((n, h), dtype=self.fp8, device=ids.device)
+        scales = self._col_major_scales(n, h, ids.device)
+        _lib.call("qx_embed_rmsnorm_quant", _ptr(embed_weight), embed_weight.stride(0),
+                  _ptr(ids), _ptr(residual), residual.stride(0), _ptr(norm.weight), _ptr(q),
+                  q.stride(0), _ptr(scales), self._scale_ld(scales), n, h,
+                  float(norm.variance_epsilon), _stream())
+        return q, scales, residual
+
+    def activation_quant(self, gate_up):
+        """SiLU-gated product of the two gate_up halves, quantized."""
+        n, doubled = gate_up.shape
+        half = doubled // 2
+        q = torch.empty((n, half), dtype=self.fp8, device=gate_up.device)
+        scales = self._col_major_scales(n, half, gate_up.device)
+        _lib.call("qx_silu_mul_quant", _ptr(gate_up), gate_up.stride(0), _ptr(q), q.stride(0),
+                  _ptr(scales), self._scale_ld(scales), n, half, _stream())
+        return q, scales
+
+    def qk_norm_rope(self, qkv, positions, attn):
+        """Per-head normed and rotated q and k from the fused qkv output."""
+        n = qkv.shape[0]
+        hq, hk, d = self.num_q_heads, self.num_kv_heads, self.head_dim
+        q = torch.empty((n, hq * d), dtype=torch.bfloat16, device=qkv.device)
+        k = torch.empty((n, hk * d), dtype=torch.bfloat16, device=qkv.device)
+        cache = self.rotary.cos_sin_cache
+        if cache.dtype not in (torch.bfloat16, torch.float32):
+            raise ValueError(f"cos_sin_cache dtype {cache.dtype}")
+        if cache.shape[1] != d:
+            raise ValueError(f"cos_sin_cache width {cache.shape[1]} != head_dim {d}")
+        _lib.call("qx_qk_norm_rope", _ptr(qkv), qkv.stride(0), _ptr(q), q.stride(0), _ptr(k),
+                  k.stride(0), _ptr(cache), int(cache.dtype == torch.float32), _ptr(positions),
+                  _ptr(attn.q_norm.weight), _ptr(attn.k_norm.weight), n, hq, hk, d,
+                  float(attn.q_norm.variance_epsilon), _stream())
+        return q, k
+
+    def kv_row_scatter(self, k3, v3, src, dst, layer):
+        """Scatter KV rows into the layer's arena pages; dst < 0 is padding."""
+        count = src.shape[0]
+        row = self.num_kv_heads * self.head_dim
+        k_pool, v_pool = self.arena.layer_kv(layer)
+        k_ld = k3.stride(0)
+        v_ld = v3.stride(0)
+        _lib.call("qx_kv_scatter", _ptr(k3), k_ld, _ptr(v3), v_ld, _ptr(k_pool), _ptr(v_pool),
+                  _ptr(src), _ptr(dst), count, row, _stream())
+
+    def write_kv(self, k3, v3, meta, *, copy_tail=True):
+        """Write fresh rows and retained partial pages (attention.py:1175-1195)."""
+        if meta.get("kv_written", False):
+            return
+        layer = meta["layer"]
+        pool = meta["unified"]
+        if pool is None:
+            return
+        if pool["src"].numel():
+            self.kv_row_scatter(k3, v3, pool["src"], pool["dst"], layer)
+        if copy_tail and pool.get("tail_src") is not None:
+            k_pool, v_pool = self.arena.layer_kv(layer)
+            self.kv_row_scatter(k_pool, v_pool, pool["tail_src"], pool["tail_dst"], layer)
+
+    def attention(self, q, k, v, chunk, *, output=None):
+        """Attention over the chunk and the arena; the quantized o_proj input.
+
+        q, k and v are the flat per-row projections; v may be the strided
+        slice of qkv. Returns (e4m3 rows, col-major scales).
+        """
+        n = q.shape[0]
+        hq, hk, d = self.num_q_heads, self.num_kv_heads, self.head_dim
+        if chunk.attention_mode != "unified":
+            raise ValueError("this engine runs the unified attention path")
+        q3 = q.view(n, hq, d)
+        k3 = k.view(n, hk, d)
+        v3 = v.view(n, hk, d) if v.is_contiguous() else v
+        return self.attention_unified(q3, k3, v3, chunk.meta, output=output)
+
+    def attention_unified(self, q3, k3, v3, meta, *, softmax_scale=None, output=None):
+        """Write the chunk's KV to its pages, then one paged causal call with
+        the o_proj input quantization fused (attention.py:1477-1573)."""
+        n = q3.shape[0]
+        hq, hk, d = self.num_q_heads, self.num_kv_heads, self.head_dim
+        unified = meta["unified"]
+        if unified is None:
+            raise ValueError("this engine reads KV from arena pages; pack with pages")
+        self.write_kv(k3, v3, meta)
+        layer = meta["layer"]
+        k_pool, v_pool = self.arena.layer_kv(layer)
+        scale = d ** -0.5 if softmax_scale is None else softmax_scale
+        table = unified["table"]
+        if output is not None:
+            o_q, o_s = output
+        else:
+            o_q = torch.empty((n, hq * d), dtype=self.fp8, device=q3.device)
+            o_s = self._col_major_scales(n, hq * d, q3.device)
+        seqs = unified["used"].shape[0]
+        q_ld = q3.stride(0)
+        if d == GROUP:
+            _lib.call("qx_paged_attention", _ptr(q3), q_ld, _ptr(k_pool), _ptr(v_pool),
+                      _ptr(unified["cu_q"]), _ptr(unified["used"]), _ptr(table),
+                      table.stride(0), seqs, int(unified["max_q"]), hq, hk, d,
+                      self.arena.page_tokens, float(scale), int(unified.get("causal", True)),
+                      None, _ptr(o_q), o_q.stride(0), _ptr(o_s), self._scale_ld(o_s), _stream())
+        else:
+            # a 128-column FP8 group spans several heads: bf16 out, then quant
+            o = torch.empty((n, hq * d), dtype=torch.bfloat16, device=q3.device)
+            _lib.call("qx_paged_attention", _ptr(q3), q_ld, _ptr(k_pool), _ptr(v_pool),
+                      _ptr(unified["cu_q"]), _ptr(unified["used"]), _ptr(table),
+                      table.stride(0), seqs, int(unified["max_q"]), hq, hk, d,
+                      self.arena.page_tokens, float(scale), int(unified.get("causal", True)),
+                      _ptr(o), None, o.stride(0), None, 0, _stream())
+            self.quant(o, output=(o_q, o_s))
+        meta["layer"] += 1
+        return o_q, o_s
+
+    def attention_bf16(self, q3, meta, layer):
+        """The unquantized attention rows of one layer (for tests)."""
+        n = q3.shape[0]
+        hq, hk, d = self.num_q_heads, self.num_kv_heads, self.head_dim
+        unified = meta["unified"]
+        k_pool, v_pool = self.arena.layer_kv(layer)
+        o = torch.empty((n, hq * d), dtype=torch.bfloat16, device=q3.device)
+        table = unified["table"]
+        _lib.call("qx_paged_attention", _ptr(q3), q3.stride(0), _ptr(k_pool), _ptr(v_pool),
+                  _ptr(unified["cu_q"]), _ptr(unified["used"]), _ptr(table), table.stride(0),
+                  unified["used"].shape[0], int(unified["max_q"]), hq, hk, d,
+                  self.arena.page_tokens, float(d ** -0.5), int(unified.get("causal", True)),
+                  _ptr(o), None, o.stride(0), None, 0, _stream())
+        return o

@@ -1,0 +1,109 @@
+"""Qwen3 forward pass over the gfx950 Engine.
+
+The same layer order and contract as the reference pipeline
+(quail/backends/quail/executor/models/qwen3.py:15-135 and the ModelPipeline
+contract of models/base.py:36-84): input RMSNorm, fused QKV projection,
+per-head Q/K RMSNorm with rotary, paged attention, output projection,
+post-attention RMSNorm, gate_up projection, SiLU-gated product, down
+projection; the final norm runs on `chunk.final_indices` only.
+
+Two launches are fused relative to the reference's sequence, with identical
+results: the embedding gather with layer 0's norm_quant, and the final-row
+gather with the final fused_add_rms_norm.
+"""
+
+from quail_amd.engine import Engine
+
+
+class Qwen3Pipeline:
+    """Forward passes for Qwen3 FP8 checkpoints (see quail_amd.model)."""
+
+    # ModelPipeline contract attributes (models/base.py:58-84)
+    warm_tokens = (64, 128, 256, 512, 1024, 2048)
+    needs_pages = True
+    mask = "causal"
+    masks = ("causal",)
+    tree_attention = False
+    gemm_warmup = True
+
+    def __init__(self, model, arena, *, spec=None, kernels="quail", engine_class=Engine):
+        self.layers = model.model.layers
+        self.embed = model.model.embed_tokens
+        self.final_norm = model.model.norm
+        attn = self.layers[0].self_attn
+        self.engine = engine_class(
+            arena, num_q_heads=attn.num_heads, num_kv_heads=attn.num_kv_heads,
+            head_dim=attn.head_dim, rotary=attn.rotary_emb,
+            fp8=attn.qkv_proj.weight.dtype.is_floating_point and
+            attn.qkv_proj.weight.element_size() == 1, kernels=kernels)
+        # element offsets inside the kernels are int64; the reference's
+        # 32-bit bound (qwen3.py:31-36) is kept so packs stay comparable
+        widest = max(max(layer.self_attn.qkv_proj.weight.shape[0],
+                         layer.mlp.gate_up_proj.weight.shape[0]) for layer in self.layers)
+        self.max_chunk_tokens = (2**31 - 1) // widest
+        self.spec = spec
+
+    def _check_bounds(self, chunk):
+        """Token ids index the embedding and positions the rotary cache; the
+        kernels gather without bounds checks, so reject bad packs here."""
+        ids = getattr(chunk, "host_ids", None)
+        if ids is not None and len(ids):
+            vocab = self.embed.weight.shape[0]
+            if int(ids.min()) < 0 or int(ids.max()) >= vocab:
+                raise ValueError(f"token id outside the {vocab}-row embedding")
+        pos = getattr(chunk, "host_positions", None)
+        if pos is not None and len(pos):
+            rows = self.engine.rotary.cos_sin_cache.shape[0]
+            if int(pos.min()) < 0 or int(pos.max()) >= rows:
+                raise ValueError(f"position outside the {rows}-row rotary cache")
+
+    def linears(self):
+        layer = self.layers[0]
+        return (layer.self_attn.qkv_proj, layer.self_attn.o_proj,
+                layer.mlp.gate_up_proj, layer.mlp.down_proj)
+
+    def before_attention(self, hidden, residual, positions, layer):
+        """Normalize and project rows into rotary Q, K, V and the residual."""
+        engine = self.engine
+        attn = layer.self_attn
+        if residual is None:
+            residual = hidden
+            q_in, q_scale = engine.norm_quant(hidden, layer.input_layernorm)
+        else:
+            q_in, q_scale = engine.norm_quant(hidden, layer.input_layernorm, residual)
+        return self._project_qkv(q_in, q_scale, positions, attn) + (residual,)
+
+    def _project_qkv(self, q_in, q_scale, positions, attn):
+        engine = self.engine
+        qkv = engine.gemm(q_in, q_scale, attn.qkv_proj)
+        q, k = engine.qk_norm_rope(qkv, positions, attn)
+        v = qkv[:, (engine.num_q_heads + engine.num_kv_heads) * engine.head_dim:]
+        return q, k, v
+
+    def after_attention(self, o_in, o_scale, residual, layer):
+        """Project attention rows and apply the residual MLP."""
+        engine = self.engine
+        hidden = engine.gemm(o_in, o_scale, layer.self_attn.o_proj)
+        g_in, g_scale = engine.norm_quant(hidden, layer.post_attention_layernorm, residual)
+        gate_up = engine.gemm(g_in, g_scale, layer.mlp.gate_up_proj)
+        d_in, d_scale = engine.activation_quant(gate_up)
+        return engine.gemm(d_in, d_scale, layer.mlp.down_proj)
+
+    def forward_chunk(self, chunk):
+        """Return the final-normed hidden state of chunk.final_indices."""
+        engine = self.engine
+        self._check_bounds(chunk)
+        chunk.meta["layer"] = 0
+        first = self.layers[0]
+        q_in, q_scale, residual = engine.embed_norm_quant(
+            chunk.input_ids, self.embed.weight, first.input_layernorm)
+        hidden = None
+        for index, layer in enumerate(self.layers):
+            if index == 0:
+                q, k, v = self._project_qkv(q_in, q_scale, chunk.positions, layer.self_attn)
+            else:
+                q, k, v, residual = self.before_attention(hidden, residual, chunk.positions,
+                                                          layer)
+            o_in, o_scale = engine.attention(q, k, v, chunk)
+            hidden = self.after_attention(o_in, o_scale, residual, layer)
+        return engine.final_norm(hidden, residual, chunk.final_indices, self.final_norm)

@@ -1,0 +1,336 @@
+"""Each gfx950 kernel against the oracle's restatement of the reference op.
+
+Integer/byte work (scatter, embedding gather) must be bit-exact. Floating
+point kernels are compared with tolerances written per test:
+  * FP8 outputs: scales within 1e-6 relative and >= 99.9% of e4m3 codes
+    identical, the rest one code step away (a 1-ulp fp32 difference can
+    move a value across an e4m3 rounding boundary);
+  * bf16 outputs: within 1 bf16 ulp (2^-8 relative) of the oracle for
+    >= 99.9% of elements, and rtol 1e-2 for all;
+  * attention: rtol/atol 2e-2 against exact fp32 brute force, the
+    reference's own bound (tests/gpu/test_decode_evaluator.py:175-238).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import fp8 as ofp8
+from oracle import qwen3_ref as ref
+from quail_amd import _lib
+from quail_amd.engine import Engine
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+def _engine(hq=4, hk=2, d=64, arena=None, cache=None):
+    rotary = type("R", (), {})()
+    rotary.cos_sin_cache = cache
+    return Engine(arena, num_q_heads=hq, num_kv_heads=hk, head_dim=d, rotary=rotary)
+
+
+def _gen(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+def _fp8_close(q_gpu, s_gpu, q_ref, s_ref, min_equal=0.999):
+    s_gpu = s_gpu.float().cpu()
+    s_ref = s_ref.float().cpu()
+    torch.testing.assert_close(s_gpu, s_ref, rtol=1e-6, atol=0)
+    a = q_gpu.cpu().view(torch.uint8).numpy().astype(np.int32)
+    b = q_ref.cpu().view(torch.uint8).numpy().astype(np.int32)
+    equal = (a == b).mean()
+    assert equal >= min_equal, f"only {equal:.5f} of e4m3 codes equal"
+    # the rest are neighbouring codes (same sign, magnitude code +-1)
+    diff = a != b
+    if diff.any():
+        assert np.all(np.abs((a[diff] & 0x7F) - (b[diff] & 0x7F)) <= 1)
+
+
+def _bf16_close(x, y, min_ulp1=0.999, rtol=1e-2, atol=None):
+    x = x.float().cpu()
+    y = y.float().cpu()
+    scale = y.abs().max().item() + 1e-30
+    atol = 1e-3 * scale if atol is None else atol
+    torch.testing.assert_close(x, y, rtol=rtol, atol=atol)
+    _, exp = torch.frexp(y)
+    ulp = torch.ldexp(torch.ones_like(y), exp - 8)       # one bf16 ulp of y
+    close = ((x - y).abs() <= ulp.clamp_min(atol * 1e-2)).float().mean().item()
+    assert close >= min_ulp1, f"only {close:.5f} within 1 bf16 ulp"
+
+
+def test_library_is_native_and_gfx950():
+    lib = _lib.load()
+    assert lib.qx_device_is_gfx950() == 1
+    assert torch.cuda.get_device_properties(0).gcnArchName.startswith("gfx950")
+
+
+# ---- FP8 block-scaled GEMM ---------------------------------------------------
+
+def _gemm_case(m, n, k, seed, device="cpu"):
+    g = _gen(seed)
+    a = torch.randn(m, k, generator=g)
+    q, s = ofp8.group_quant(a)
+    w = torch.randn(n, k, generator=g) * 0.02
+    wq, ws = ofp8.quantize_weight_blocks(w)
+    return q, s, wq, ws
+
+
+def _run_gemm(q, s, wq, ws, config=None, monkeypatch=None):
+    eng = _engine()
+    m, k = q.shape
+    scales = torch.empty((k // 128, m), dtype=torch.float32, device=DEV)
+    scales.copy_(s.T)
+    lin = type("L", (), {})()
+    lin.weight = wq.to(DEV)
+    lin.weight_scale_inv = ws.to(DEV)
+    return eng.gemm(q.to(DEV), scales.permute(1, 0), lin)
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 256, 128), (100, 512, 256), (257, 768, 384),
+                                   (64, 128, 256), (333, 1536, 256)])
+def test_gemm_small_shapes_match_dequantized_matmul(m, n, k):
+    q, s, wq, ws = _gemm_case(m, n, k, seed=m + n + k)
+    out = _run_gemm(q, s, wq, ws)
+    want = ref.gemm(q, s, ref.RefLinear(wq, ws))
+    _bf16_close(out, want)
+
+
+@pytest.mark.parametrize("config", [0, 1, 2])
+def test_gemm_tile_configs_agree(config, monkeypatch):
+    q, s, wq, ws = _gemm_case(300, 512, 512, seed=9)
+    monkeypatch.setenv("QUAIL_GEMM_CONFIG", str(config))
+    out = _run_gemm(q, s, wq, ws)
+    want = ref.gemm(q, s, ref.RefLinear(wq, ws))
+    _bf16_close(out, want)
+
+
+@pytest.mark.parametrize("k,n", [(2560, 6144), (4096, 2560), (2560, 19456), (9728, 2560)])
+def test_gemm_qwen3_4b_shapes_at_8192_tokens(k, n):
+    """The GEMM-alone config: M=8192 at the four Qwen3-4B projection shapes,
+    against the fp32 matmul of the dequantized operands (computed on the GPU
+    in fp32 for time)."""
+    m = 8192
+    g = torch.Generator(device=DEV).manual_seed(k + n)
+    a = torch.randn(m, k, generator=g, device=DEV)
+    q, s = ofp8.group_quant(a)
+    w = torch.randn(n, k, generator=g, device=DEV) * 0.02
+    wq, ws = ofp8.quantize_weight_blocks(w)
+    out = _run_gemm(q, s, wq, ws)
+    want = (ofp8.dequant_rows(q, s) @ ofp8.dequant_weight(wq, ws).T).to(torch.bfloat16)
+    _bf16_close(out, want, min_ulp1=0.995)
+
+
+def test_gemm_rejects_bad_shapes():
+    eng = _engine()
+    q = torch.zeros((4, 200), dtype=torch.float8_e4m3fn, device=DEV)
+    lin = type("L", (), {})()
+    lin.weight = torch.zeros((256, 200), dtype=torch.float8_e4m3fn, device=DEV)
+    lin.weight_scale_inv = torch.ones((2, 2), device=DEV)
+    scales = torch.ones((1, 4), device=DEV).permute(1, 0)
+    with pytest.raises(_lib.QxError, match="multiple of 128"):
+        eng.gemm(q, scales, lin)
+    with pytest.raises(ValueError, match="column-major"):
+        eng.gemm(q, torch.ones((4, 1), device=DEV), lin)
+
+
+# ---- norms and quant ------------------------------------------------------------
+
+@pytest.mark.parametrize("n,h", [(1, 256), (37, 2560), (130, 5120), (5, 4096)])
+def test_add_rmsnorm_quant(n, h):
+    g = _gen(n + h)
+    x = (torch.randn(n, h, generator=g) * 3).to(torch.bfloat16)
+    res = (torch.randn(n, h, generator=g) * 2).to(torch.bfloat16)
+    w = (1 + 0.1 * torch.randn(h, generator=g)).to(torch.bfloat16)
+    eng = _engine()
+    res_d = res.to(DEV).clone()
+    norm = type("N", (), {"weight": w.to(DEV), "variance_epsilon": 1e-6})()
+    q, s = eng.norm_quant(x.to(DEV), norm, res_d)
+    q_ref, s_ref, res_ref = ref.add_rms_norm_quant(x, res, w, 1e-6)
+    assert torch.equal(res_d.cpu(), res_ref)
+    _fp8_close(q, s, q_ref, s_ref)
+
+
+@pytest.mark.parametrize("n,h", [(3, 256), (64, 2560)])
+def test_rmsnorm_quant_and_embed_fused(n, h):
+    g = _gen(7 * n + h)
+    x = (torch.randn(n, h, generator=g)).to(torch.bfloat16)
+    w = (1 + 0.1 * torch.randn(h, generator=g)).to(torch.bfloat16)
+    norm = type("N", (), {"weight": w.to(DEV), "variance_epsilon": 1e-6})()
+    eng = _engine()
+    q, s = eng.norm_quant(x.to(DEV), norm)
+    q_ref, s_ref = ref.norm_quant_first(x, w, 1e-6)
+    _fp8_close(q, s, q_ref, s_ref)
+    table = (torch.randn(300, h, generator=g) * 0.02).to(torch.bfloat16)
+    ids = torch.randint(0, 300, (n,), generator=g)
+    q2, s2, res = eng.embed_norm_quant(ids.to(DEV), table.to(DEV), norm)
+    assert torch.equal(res.cpu(), table[ids])
+    q2_ref, s2_ref = ref.norm_quant_first(table[ids], w, 1e-6)
+    _fp8_close(q2, s2, q2_ref, s2_ref)
+
+
+def test_fused_add_rms_norm_in_place_and_gathered():
+    g = _gen(5)
+    n, h = 50, 2560
+    hid = torch.randn(n, h, generator=g).to(torch.bfloat16)
+    res = torch.randn(n, h, generator=g).to(torch.bfloat16)
+    w = (1 + 0.1 * torch.randn(h, generator=g)).to(torch.bfloat16)
+    norm = type("N", (), {"weight": w.to(DEV), "variance_epsilon": 1e-6})()
+    eng = _engine()
+    rows = torch.tensor([49, 0, 7, 7, 13])
+    out = eng.final_norm(hid.to(DEV), res.to(DEV), rows.to(DEV), norm)
+    want, _ = ref.fused_add_rms_norm(hid[rows], res[rows], w, 1e-6)
+    _bf16_close(out, want, min_ulp1=0.998)
+    hd, rd = hid.to(DEV), res.to(DEV)
+    eng.fused_add_rms_norm(hd, rd, norm)
+    want_all, z = ref.fused_add_rms_norm(hid, res, w, 1e-6)
+    assert torch.equal(rd.cpu(), z)
+    _bf16_close(hd, want_all, min_ulp1=0.998)
+
+
+@pytest.mark.parametrize("n,i", [(3, 768), (40, 9728), (7, 12288)])
+def test_silu_mul_quant(n, i):
+    g = _gen(n * i)
+    gu = (torch.randn(n, 2 * i, generator=g) * 2).to(torch.bfloat16)
+    eng = _engine()
+    q, s = eng.activation_quant(gu.to(DEV))
+    q_ref, s_ref = ref.silu_mul_quant(gu)
+    _fp8_close(q, s, q_ref, s_ref, min_equal=0.998)
+
+
+def test_group_quant_matches_and_zero_group_floor():
+    g = _gen(11)
+    x = torch.randn(9, 4096, generator=g).to(torch.bfloat16)
+    x[3, 256:384] = 0
+    eng = _engine()
+    q, s = eng.quant(x.to(DEV))
+    q_ref, s_ref = ofp8.group_quant(x.float())
+    _fp8_close(q, s, q_ref, s_ref, min_equal=1.0)
+    assert s[3, 2].item() == np.float32(1e-10) / np.float32(448)
+
+
+# ---- qk norm + rope -----------------------------------------------------------------
+
+@pytest.mark.parametrize("hq,hk,d", [(4, 2, 64), (32, 8, 128), (64, 8, 128)])
+@pytest.mark.parametrize("cache_dtype", [torch.bfloat16, torch.float32])
+def test_qk_norm_rope(hq, hk, d, cache_dtype):
+    n = 77
+    g = _gen(hq * d)
+    qkv = torch.randn(n, (hq + 2 * hk) * d, generator=g).to(torch.bfloat16)
+    pos = torch.randint(0, 4000, (n,), generator=g)
+    pos[0] = 0
+    cache = ref.rope_cache(d, 4096, 1e6).to(cache_dtype)
+    qw = (1 + 0.1 * torch.randn(d, generator=g)).to(torch.bfloat16)
+    kw = (1 + 0.1 * torch.randn(d, generator=g)).to(torch.bfloat16)
+    attn = type("A", (), {})()
+    attn.q_norm = type("N", (), {"weight": qw.to(DEV), "variance_epsilon": 1e-6})()
+    attn.k_norm = type("N", (), {"weight": kw.to(DEV), "variance_epsilon": 1e-6})()
+    eng = _engine(hq, hk, d, cache=cache.to(DEV))
+    q, k = eng.qk_norm_rope(qkv.to(DEV), pos.to(DEV), attn)
+    q_ref, k_ref = ref.qk_norm_rope(qkv, pos, cache, qw, kw, hq, hk, d, 1e-6)
+    _bf16_close(q, q_ref, min_ulp1=0.998)
+    _bf16_close(k, k_ref, min_ulp1=0.998)
+
+
+# ---- KV scatter and paged attention ---------------------------------------------------
+
+class _Arena:
+    def __init__(self, kp, vp, page):
+        self.kp, self.vp, self.page_tokens = kp, vp, page
+
+    def layer_kv(self, layer):
+        return self.kp, self.vp
+
+
+def test_kv_scatter_is_bit_exact_and_skips_negative_rows():
+    g = _gen(2)
+    n, hk, d = 50, 8, 128
+    qkv = torch.randn(n, 48 * 128, generator=g).to(torch.bfloat16).to(DEV)
+    k = torch.randn(n, hk * d, generator=g).to(torch.bfloat16).to(DEV)
+    v = qkv[:, 40 * 128:]                         # strided v slice of qkv
+    kp = torch.zeros(256, hk, d, dtype=torch.bfloat16, device=DEV)
+    vp = torch.zeros_like(kp)
+    src = torch.arange(n, device=DEV)
+    dst = torch.randperm(256, generator=g)[:n].to(DEV)
+    dst[5] = -1
+    eng = _engine(32, hk, d, arena=_Arena(kp, vp, 16))
+    eng.kv_row_scatter(k, v, src, dst, 0)
+    ok = dst >= 0
+    assert torch.equal(kp[dst[ok]], k.view(n, hk, d)[ok])
+    assert torch.equal(vp[dst[ok]], v.reshape(n, hk, d)[ok])
+    written = torch.zeros(256, dtype=torch.bool, device=DEV)
+    written[dst[ok]] = True
+    assert torch.all(kp[~written] == 0)
+
+
+def _paged_case(seed, hq, hk, d, page, seqs, pool_pages):
+    g = _gen(seed)
+    rng = np.random.default_rng(seed)
+    q_lens = rng.integers(1, 150, seqs)
+    q_lens[0] = 1
+    extra = rng.integers(0, 100, seqs)
+    used = q_lens + extra
+    cu = np.concatenate([[0], np.cumsum(q_lens)]).astype(np.int32)
+    n = int(cu[-1])
+    width = int(max(-(-used // page)))
+    perm = rng.permutation(pool_pages)
+    table = np.zeros((seqs, width), dtype=np.int32)
+    at = 0
+    for s in range(seqs):
+        need = -(-int(used[s]) // page)
+        table[s, :need] = perm[at:at + need]
+        at += need
+    kp = torch.randn(pool_pages * page, hk, d, generator=g).to(torch.bfloat16)
+    vp = torch.randn(pool_pages * page, hk, d, generator=g).to(torch.bfloat16)
+    q = torch.randn(n, hq, d, generator=g).to(torch.bfloat16)
+    return q, kp, vp, cu, used.astype(np.int32), table
+
+
+@pytest.mark.parametrize("hq,hk,d", [(4, 2, 64), (32, 8, 128), (64, 8, 128), (8, 8, 128)])
+def test_paged_attention_matches_exact_fp32(hq, hk, d):
+    page = 16
+    q, kp, vp, cu, used, table = _paged_case(hq + d, hq, hk, d, page, 6, 160)
+    want = ref.paged_attention(q, kp, vp, cu, used, table, page)
+    eng = _engine(hq, hk, d, arena=_Arena(kp.to(DEV), vp.to(DEV), page))
+    meta = dict(unified=dict(cu_q=torch.tensor(cu, device=DEV),
+                             used=torch.tensor(used, device=DEV),
+                             table=torch.tensor(table, device=DEV),
+                             max_q=int(np.diff(cu).max()), causal=True))
+    got = eng.attention_bf16(q.to(DEV), meta, 0)
+    torch.testing.assert_close(got.float().cpu().view_as(want), want.float(), rtol=2e-2, atol=2e-2)
+    if d == 128:
+        # the fused o_proj quant equals quantizing the bf16 rows
+        meta["layer"] = 0
+        meta["unified"]["src"] = torch.empty(0, dtype=torch.long, device=DEV)
+        o_q, o_s = eng.attention_unified(q.to(DEV), None, None, meta)
+        q_ref, s_ref = ofp8.group_quant(got.float().cpu())
+        _fp8_close(o_q, o_s, q_ref, s_ref, min_equal=1.0)
+
+
+def test_answer_head_modes():
+    g = _gen(13)
+    n, h, t = 33, 2560, 6
+    normed = torch.randn(n, h, generator=g).to(torch.bfloat16)
+    rows = (torch.randn(t, h, generator=g) * 0.02).to(torch.bfloat16)
+    cls = torch.tensor([1, 0, 1, -1, 0, 0], dtype=torch.int32)
+    from quail_amd.readout import AnswerRows
+    ar = AnswerRows.__new__(AnswerRows)
+    ar.weights = rows.to(DEV)
+    ar.classes = cls.to(DEV)
+    for mode in (0, 1):
+        logits = torch.empty(n, t, device=DEV)
+        bits = torch.empty(n, dtype=torch.uint8, device=DEV)
+        yn = torch.empty(n, 2, device=DEV)
+        score = torch.empty(n, device=DEV)
+        ar.head(normed.to(DEV), mode=mode, logits=logits, bits=bits, yes_no=yn, score=score)
+        want = ref.label_logits(normed, rows, mode)
+        if mode == 0:
+            _bf16_close(logits, want, min_ulp1=0.99)
+        else:
+            torch.testing.assert_close(logits.cpu(), want, rtol=1e-4, atol=1e-4)
+        yes, no, b, sc = ref.answer(normed, rows, cls.tolist(), mode)
+        agree = (bits.cpu() == b).float().mean().item()
+        assert agree >= 0.97
+        torch.testing.assert_close(score.cpu(), sc, rtol=1e-2, atol=1e-2)
