@@ -79,6 +79,9 @@ class Engine:
         self.fp8 = torch.float8_e4m3fn
         self.is_fp8 = True
         self.use_ue8m0 = False
+        # a list to receive (M, N, K, start event, end event) per GEMM launch,
+        # recorded on the launch stream; None (the default) records nothing
+        self.gemm_timer = None
 
     # ---- weights and quant --------------------------------------------
 
@@ -112,9 +115,16 @@ class Engine:
                              "column-major storage")
         if out is None:
             out = torch.empty((m, n), dtype=torch.bfloat16, device=q_input.device)
+        timer = self.gemm_timer
+        if timer is not None:
+            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            start.record()
         _lib.call("qx_gemm_fp8_blockscaled", _ptr(q_input), _ptr(input_scale), _ptr(w),
                   _ptr(sw), _ptr(out), m, n, k, q_input.stride(0), out.stride(0),
                   self._scale_ld(input_scale), gemm_config(n, k, m), _stream())
+        if timer is not None:
+            end.record()
+            timer.append((m, n, k, start, end))
         return out
 
     def quant(self, x, *, output=None):

@@ -133,7 +133,7 @@ def test_gemm_rejects_bad_shapes():
     with pytest.raises(_lib.QxError, match="multiple of 128"):
         eng.gemm(q, scales, lin)
     with pytest.raises(ValueError, match="column-major"):
-        eng.gemm(q, torch.ones((4, 1), device=DEV), lin)
+        eng.gemm(q, torch.ones((4, 2), device=DEV)[:, :1], lin)
 
 
 # ---- norms and quant ------------------------------------------------------------
