@@ -43,8 +43,10 @@ int qx_device_is_gfx950(void);
  * Replaces Engine.gemm -> DeepGEMM fp8_gemm_nt((A, sA), (W, sW), C)
  * (quail/backends/quail/executor/attention.py:479-490); weight scales are the
  * checkpoint's weight_scale_inv (attention.py:471-477).
- * K and N multiples of 128 (N of 256 for configs 0 and 1). config selects
- * the tile shape (0: 128x256, 1: 256x256, 2: 128x128 tokens x weights).
+ * K and N multiples of 128 (N of 256 for configs 0, 1 and 3). config selects
+ * the tile shape, tokens x weights: 0: 256x256 (8 waves), 1: 256x256,
+ * 2: 128x128, 3: 128x256, 4-6: 256x128 (3, 2, 4 K stages); all give the
+ * same result.
  */
 int qx_gemm_fp8_blockscaled(const void* A, const float* sA, const void* W, const float* sW,
                             void* C, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldc,
@@ -136,15 +138,17 @@ int qx_embed(const void* table, int64_t t_ld, const int64_t* ids, void* out, int
  * table[s*table_ld + j/page]*page + j%page; causal masking aligned
  * bottom-right. Replaces Engine.attention_unified -> _paged ->
  * flash_attn_varlen_func(..., block_table, seqused_k, causal)
- * (attention.py:1477-1573, 1368-1393, 1280-1306). With out_fp8 it also
+ * (attention.py:1477-1573, 1368-1393, 1280-1306); max_q and max_used are
+ * FA's max_seqlen_q / max_seqlen_k (max_used <= 2048 * page). With out_fp8 it also
  * performs Engine.quant of the bf16 result (attention.py:1274-1275): e4m3
  * rows plus scales[h*s_ld + row] (one group per head, D == 128).
  */
 int qx_paged_attention(const void* q, int64_t q_ld, const void* k_pool, const void* v_pool,
                        const int* cu_q, const int* used, const int* table, int64_t table_ld,
-                       int64_t seqs, int64_t max_q, int64_t HQ, int64_t HK, int64_t D,
-                       int64_t page, float scale, int causal, void* out_bf16, void* out_fp8,
-                       int64_t o_ld, float* scales, int64_t s_ld, hipStream_t stream);
+                       int64_t seqs, int64_t max_q, int64_t max_used, int64_t HQ, int64_t HK,
+                       int64_t D, int64_t page, float scale, int causal, void* out_bf16,
+                       void* out_fp8, int64_t o_ld, float* scales, int64_t s_ld,
+                       hipStream_t stream);
 
 /*
  * Last-token answer head over the retained head rows (t <= 16):

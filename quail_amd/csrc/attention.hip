@@ -17,64 +17,96 @@
 // computed from the bf16-rounded attention output exactly as the reference's
 // separate quant kernel would see it.
 //
-// Kernel layout (CDNA4): a workgroup = one 32-row query tile of one sequence
-// x NW query heads that share a KV head (one wave per head). KV is consumed
-// in 64-key tiles staged in LDS (K row-major, V transposed). Each wave forms
-// S^T = K Q^T with v_mfma_f32_32x32x16_bf16 so that a lane owns one query
-// column; the online softmax is then lane-local (plus one cross-half
-// shuffle), P^T feeds the PV MFMA directly as its B operand, and O^T keeps
-// one query per lane, so rescaling needs no shuffles. P enters the PV MFMA as
-// a bf16 hi/lo pair, so the output carries fp32-level accuracy.
+// Kernel layout (CDNA4). A workgroup is QSUB 32-row query tiles of one
+// sequence x HPB query heads sharing one KV head: one wave per (tile, head),
+// so every K/V tile staged in LDS serves HPB * QSUB * 32 query rows. KV is
+// consumed in 64-key tiles, double buffered: while a tile is computed, the
+// next tile's K rows travel HBM -> LDS directly (global_load_lds) and its V
+// rows are fetched into registers, to be written transposed into the other
+// LDS buffer once the compute is done; one barrier per tile. The sequence's
+// page-table row is staged in LDS once.
+//
+// Each wave forms S^T = K Q^T with v_mfma_f32_32x32x16_bf16 so that a lane
+// owns one query column; the online softmax is then lane-local (plus one
+// cross-half shuffle), P^T feeds the PV MFMA directly as its B operand, and
+// O^T keeps one query per lane, so rescaling needs no shuffles. P enters the
+// PV MFMA as a bf16 hi/lo pair, so the output carries fp32-level accuracy.
 #include "qx_common.h"
 #include "qx_status.h"
 
 namespace qx {
 namespace {
 
-constexpr int kBQ = 32;   // query rows per wave
-constexpr int kBK = 64;   // keys per KV tile
+typedef __attribute__((address_space(3))) void lds_void;
+
+constexpr int kBK = 64;          // keys per KV tile
+constexpr int kMaxPages = 2048;  // page-table entries staged in LDS per sequence
 
 // position of key k (0..15) inside its 16-key group of the transposed V tile:
 // the 8 keys one MFMA lane-half consumes become contiguous
 __device__ __forceinline__ int vt_pos(int k) { return ((k >> 2) & 1) * 8 + (k >> 3) * 4 + (k & 3); }
 
-template <int D, int NW, bool QUANT>
-__global__ __launch_bounds__(NW * 64) void paged_attention_kernel(
+// 16-B chunk swizzle of a K row (2*D bytes): the 16 rows of one ds_read_b128
+// phase map to 16 distinct 16-B bank groups of the 64-bank LDS
+template <int D>
+__device__ __forceinline__ int kswz(int key) { return D == 128 ? (key & 15) : ((key >> 1) & 7); }
+
+template <int D, int HPB, int QSUB, bool QUANT>
+__global__ __launch_bounds__(HPB * QSUB * 64) void paged_attention_kernel(
     const uint16_t* __restrict__ q, int64_t q_ld, const uint16_t* __restrict__ kp,
     const uint16_t* __restrict__ vp, const int* __restrict__ cu_q, const int* __restrict__ used,
-    const int* __restrict__ table, int64_t table_ld, int HQ, int HK, int page, float scale_log2,
-    int causal, uint16_t* __restrict__ out16, uint8_t* __restrict__ out8, int64_t o_ld,
-    float* __restrict__ scales, int64_t s_ld) {
+    const int* __restrict__ table, int64_t table_ld, int max_used, int HQ, int HK, int page,
+    float scale_log2, int causal, uint16_t* __restrict__ out16, uint8_t* __restrict__ out8,
+    int64_t o_ld, float* __restrict__ scales, int64_t s_ld) {
+  constexpr int NW = HPB * QSUB;
   constexpr int NT = NW * 64;
+  constexpr int BQ = 32 * QSUB;  // query rows per workgroup
   constexpr int ND16 = D / 16;   // MFMA k-steps over the head dim
   constexpr int NDS = D / 32;    // 32-row d tiles of O^T
   constexpr int KCH = D / 8;     // 16-byte chunks per K row
-  constexpr int K_BYTES = kBK * D * 2;
-  __shared__ __attribute__((aligned(16))) uint8_t k_lds[K_BYTES];
-  __shared__ __attribute__((aligned(16))) uint8_t vt_lds[D * kBK * 2];
+  constexpr int KROW = D * 2;    // bytes per K row
+  constexpr int K_BYTES = kBK * KROW;
+  constexpr int VT_BYTES = D * kBK * 2;
+  constexpr int KEYS_PER_SLAB = 1024 / KROW;            // keys per direct-load instruction
+  constexpr int K_SLABS = kBK / KEYS_PER_SLAB / NW;     // per wave per tile
+  constexpr int V_TOTAL = (kBK / 2) * KCH;              // key pairs x 8-d chunks per tile
+  constexpr int V_UNITS = (V_TOTAL + NT - 1) / NT;      // per thread
+  static_assert(K_SLABS >= 1 && K_SLABS * KEYS_PER_SLAB * NW == kBK, "K slabs");
+  __shared__ __attribute__((aligned(1024))) uint8_t k_lds[2][K_BYTES];
+  __shared__ __attribute__((aligned(16))) uint8_t vt_lds[2][VT_BYTES];
+  __shared__ int pages_lds[kMaxPages];
 
   const int s = blockIdx.y;
   const int qt = gridDim.x - 1 - blockIdx.x;  // heavy (late) tiles first
   const int q0 = cu_q[s];
   const int q_len = cu_q[s + 1] - q0;
-  if (qt * kBQ >= q_len) return;
+  if (qt * BQ >= q_len) return;  // uniform over the workgroup
   const int G = HQ / HK;
-  const int groups_per_kv = G / NW;
+  const int groups_per_kv = G / HPB;
   const int kvh = blockIdx.z / groups_per_kv;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int head = kvh * G + (blockIdx.z % groups_per_kv) * NW + wave;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int head = kvh * G + (blockIdx.z % groups_per_kv) * HPB + (wave % HPB);
+  const int qsub = wave / HPB;
   const int half = lane >> 5;
   const int col = lane & 31;
 
-  const int used_s = used[s];
+  const int used_s = min(used[s], max_used);
   const int off = causal ? used_s - q_len : 0;
-  const int r = qt * kBQ + col;  // this lane's query row within the sequence
+  const int r = qt * BQ + qsub * 32 + col;  // this lane's query row within the sequence
   const bool r_ok = r < q_len;
-  const int last_row = min(qt * kBQ + kBQ, q_len) - 1;
-  const int kv_end = causal ? min(used_s, off + last_row + 1) : used_s;
+  const int block_last = min(qt * BQ + BQ, q_len) - 1;
+  const int kv_end = max(0, causal ? min(used_s, off + block_last + 1) : used_s);
+  // keys this wave can see at all (its last valid row)
+  const int wave_last = min(qt * BQ + qsub * 32 + 31, q_len - 1);
+  const int wave_end = causal ? min(used_s, off + wave_last + 1) : used_s;
+  const int ntiles = (kv_end + kBK - 1) / kBK;
+
+  // stage the page-table row
   const int* trow = table + (int64_t)s * table_ld;
+  const int npages = (kv_end + page - 1) / page;
+  for (int i = tid; i < npages; i += NT) pages_lds[i] = trow[i];
 
   // Q^T fragments (B operand): lane holds query `col`, d = c*16 + half*8 .. +8
   v8s qf[ND16];
@@ -84,6 +116,65 @@ __global__ __launch_bounds__(NW * 64) void paged_attention_kernel(
 #pragma unroll
     for (int c = 0; c < ND16; ++c) qf[c] = *reinterpret_cast<const v8s*>(qrow + c * 16 + half * 8);
   }
+  const int64_t kv_row = (int64_t)HK * D;  // elements per pool row
+  const uint16_t* kbase = kp + kvh * D;
+  const uint16_t* vbase = vp + kvh * D;
+  __builtin_amdgcn_s_waitcnt(0);
+  lds_barrier();  // pages_lds visible
+
+  auto pool_row = [&](int kidx) -> int64_t {
+    kidx = kidx < kv_end ? kidx : kv_end - 1;  // tail keys re-read the last key (masked)
+    return (int64_t)pages_lds[kidx / page] * page + (kidx % page);
+  };
+  // K rows of tile t straight into LDS: lane i of a slab writes bytes
+  // [16i, 16i+16): key i / KCH of the slab, physical chunk i % KCH
+  auto issue_k = [&](int t, int buf) {
+#pragma unroll
+    for (int j = 0; j < K_SLABS; ++j) {
+      const int slab = wave * K_SLABS + j;
+      const int key = slab * KEYS_PER_SLAB + lane / KCH;
+      const int p = lane % KCH;
+      const int c = p ^ kswz<D>(key);
+      const uint16_t* src = kbase + pool_row(t * kBK + key) * kv_row + c * 8;
+      __builtin_amdgcn_global_load_lds((const void*)src,
+                                       (lds_void*)(&k_lds[buf][0] + slab * 1024), 16, 0, 0);
+    }
+  };
+  uint4 vreg[V_UNITS][2];
+  auto fetch_v = [&](int t) {
+#pragma unroll
+    for (int u = 0; u < V_UNITS; ++u) {
+      const int unit = tid + u * NT;
+      if (unit < V_TOTAL) {
+        const int key = (unit / KCH) * 2, dc = unit % KCH;
+        vreg[u][0] =
+            *reinterpret_cast<const uint4*>(vbase + pool_row(t * kBK + key) * kv_row + dc * 8);
+        vreg[u][1] =
+            *reinterpret_cast<const uint4*>(vbase + pool_row(t * kBK + key + 1) * kv_row + dc * 8);
+      }
+    }
+  };
+  auto store_vt = [&](int buf) {
+#pragma unroll
+    for (int u = 0; u < V_UNITS; ++u) {
+      const int unit = tid + u * NT;
+      if (unit < V_TOTAL) {
+        const int key = (unit / KCH) * 2, dc = unit % KCH;
+        const uint32_t aw[4] = {vreg[u][0].x, vreg[u][0].y, vreg[u][0].z, vreg[u][0].w};
+        const uint32_t bw[4] = {vreg[u][1].x, vreg[u][1].y, vreg[u][1].z, vreg[u][1].w};
+        const int pos = (key >> 4) * 16 + vt_pos(key & 15);  // even; pos+1 holds key+1
+        const int chunk = pos >> 3, within = (pos & 7) * 2;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int d = dc * 8 + e;
+          const uint32_t lo = (e & 1) ? (aw[e >> 1] >> 16) : (aw[e >> 1] & 0xffffu);
+          const uint32_t hi = (e & 1) ? (bw[e >> 1] >> 16) : (bw[e >> 1] & 0xffffu);
+          *reinterpret_cast<uint32_t*>(&vt_lds[buf][0] + d * (kBK * 2) +
+                                       ((chunk ^ ((d >> 1) & 7)) * 16) + within) = lo | (hi << 16);
+        }
+      }
+    }
+  };
 
   v16f o[NDS];
 #pragma unroll
@@ -91,113 +182,100 @@ __global__ __launch_bounds__(NW * 64) void paged_attention_kernel(
 #pragma unroll
     for (int e = 0; e < 16; ++e) o[d][e] = 0.f;
   float m_run = -INFINITY, l_run = 0.f;
-  const int64_t kv_row = (int64_t)HK * D;  // elements per pool row
+  const int lim = causal ? min(off + r + 1, used_s) : used_s;  // keys < lim are visible
 
-  for (int t0 = 0; t0 < kv_end; t0 += kBK) {
-    // ---- stage K (row-major, chunk-swizzled) and V^T into LDS ----------
-    for (int u = tid; u < kBK * KCH; u += NT) {
-      const int key = u / KCH, c = u % KCH;
-      int kidx = t0 + key;
-      kidx = kidx < kv_end ? kidx : kv_end - 1;
-      const int64_t prow = (int64_t)trow[kidx / page] * page + (kidx % page);
-      const uint4 val = *reinterpret_cast<const uint4*>(kp + prow * kv_row + kvh * D + c * 8);
-      *reinterpret_cast<uint4*>(k_lds + key * (D * 2) + ((c ^ (key & 7)) * 16)) = val;
-    }
-    for (int u = tid; u < (kBK / 2) * KCH; u += NT) {
-      const int kp2 = u / KCH, dc = u % KCH;
-      const int key = kp2 * 2;
-      int k0 = t0 + key, k1 = k0 + 1;
-      k0 = k0 < kv_end ? k0 : kv_end - 1;
-      k1 = k1 < kv_end ? k1 : kv_end - 1;
-      const int64_t p0 = (int64_t)trow[k0 / page] * page + (k0 % page);
-      const int64_t p1 = (int64_t)trow[k1 / page] * page + (k1 % page);
-      const uint4 a = *reinterpret_cast<const uint4*>(vp + p0 * kv_row + kvh * D + dc * 8);
-      const uint4 b = *reinterpret_cast<const uint4*>(vp + p1 * kv_row + kvh * D + dc * 8);
-      const uint32_t aw[4] = {a.x, a.y, a.z, a.w}, bw[4] = {b.x, b.y, b.z, b.w};
-      const int pos = (key >> 4) * 16 + vt_pos(key & 15);  // even; pos+1 holds key+1
-      const int chunk = pos >> 3, within = (pos & 7) * 2;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int d = dc * 8 + e;
-        const uint32_t lo = (e & 1) ? (aw[e >> 1] >> 16) : (aw[e >> 1] & 0xffffu);
-        const uint32_t hi = (e & 1) ? (bw[e >> 1] >> 16) : (bw[e >> 1] & 0xffffu);
-        *reinterpret_cast<uint32_t*>(vt_lds + d * (kBK * 2) + ((chunk ^ (d & 7)) * 16) + within) =
-            lo | (hi << 16);
-      }
-    }
-    __syncthreads();
+  if (ntiles > 0) {
+    // prologue: tile 0 into buffer 0
+    issue_k(0, 0);
+    fetch_v(0);
+    store_vt(0);
+    __builtin_amdgcn_s_waitcnt(0);
+    lds_barrier();
+  }
 
-    // ---- S^T = K Q^T for two 32-key subtiles ---------------------------
-    v16f sacc[2];
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      v16f a = {};
-      const int key = ks * 32 + col;
-#pragma unroll
-      for (int c = 0; c < ND16; ++c) {
-        const int lc = 2 * c + half;
-        const v8s kf = *reinterpret_cast<const v8s*>(k_lds + key * (D * 2) + ((lc ^ (key & 7)) * 16));
-        a = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, kf),
-                                                    __builtin_bit_cast(v8bf, qf[c]), a, 0, 0, 0);
-      }
-      sacc[ks] = a;
+  for (int t = 0; t < ntiles; ++t) {
+    const int buf = t & 1;
+    const bool more = t + 1 < ntiles;
+    if (more) {
+      issue_k(t + 1, buf ^ 1);
+      fetch_v(t + 1);
     }
-
-    // ---- mask, online softmax (lane = one query; partner lane^32) -------
-    const int lim = causal ? min(off + r + 1, used_s) : used_s;  // keys < lim are visible
-    float tmax = -INFINITY;
+    const int t0 = t * kBK;
+    if (t0 < wave_end) {  // wave-uniform: a tile wholly past this wave's rows is skipped
+      // ---- S^T = K Q^T for two 32-key subtiles -------------------------
+      const uint8_t* kl = &k_lds[buf][0];
+      v16f sacc[2];
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks)
+      for (int ks = 0; ks < 2; ++ks) {
+        v16f a = {};
+        const int key = ks * 32 + col;
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int kidx = t0 + ks * 32 + (i >> 2) * 8 + half * 4 + (i & 3);
-        float v = sacc[ks][i] * scale_log2;
-        v = (kidx < lim && r_ok) ? v : -INFINITY;
-        sacc[ks][i] = v;
-        tmax = fmaxf(tmax, v);
+        for (int c = 0; c < ND16; ++c) {
+          const int lc = 2 * c + half;
+          const v8s kf = *reinterpret_cast<const v8s*>(kl + key * KROW + ((lc ^ kswz<D>(key)) * 16));
+          a = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, kf),
+                                                      __builtin_bit_cast(v8bf, qf[c]), a, 0, 0, 0);
+        }
+        sacc[ks] = a;
       }
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-    const float m_new = fmaxf(m_run, tmax);
-    const float m_use = m_new == -INFINITY ? 0.f : m_new;
-    const float alpha = exp2f(m_run - m_use);
-    // P is split into bf16 hi + lo parts (P = hi + lo to ~16 mantissa bits),
-    // so the PV product keeps fp32-level accuracy on bf16 MFMAs.
-    float psum = 0.f;
-    v8s pf[4], pl[4];
+      // ---- mask, online softmax (lane = one query; partner lane^32) -----
+      float tmax = -INFINITY;
 #pragma unroll
-    for (int kc = 0; kc < 4; ++kc) {
+      for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const float pv = exp2f(sacc[kc >> 1][(kc & 1) * 8 + j] - m_use);
-        psum += pv;
-        const uint16_t hi = f32_to_bf16(pv);
-        pf[kc][j] = (short)hi;
-        pl[kc][j] = (short)f32_to_bf16(pv - bf16_to_f32(hi));
-      }
-    }
-    psum += __shfl_xor(psum, 32, 64);
-    l_run = l_run * alpha + psum;
-    m_run = m_new;
-#pragma unroll
-    for (int d = 0; d < NDS; ++d)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) o[d][e] *= alpha;
-
-    // ---- O^T += V^T P^T --------------------------------------------------
-#pragma unroll
-    for (int d = 0; d < NDS; ++d) {
-      const int dr = d * 32 + col;
+        for (int i = 0; i < 16; ++i) {
+          const int kidx = t0 + ks * 32 + (i >> 2) * 8 + half * 4 + (i & 3);
+          float v = sacc[ks][i] * scale_log2;
+          v = (kidx < lim && r_ok) ? v : -INFINITY;
+          sacc[ks][i] = v;
+          tmax = fmaxf(tmax, v);
+        }
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+      const float m_new = fmaxf(m_run, tmax);
+      const float m_use = m_new == -INFINITY ? 0.f : m_new;
+      const float alpha = exp2f(m_run - m_use);
+      float psum = 0.f;
+      v8s pf[4], pl[4];
 #pragma unroll
       for (int kc = 0; kc < 4; ++kc) {
-        const int lc = 2 * kc + half;
-        const v8s vf = *reinterpret_cast<const v8s*>(vt_lds + dr * (kBK * 2) + ((lc ^ (dr & 7)) * 16));
-        o[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, vf),
-                                                       __builtin_bit_cast(v8bf, pf[kc]), o[d], 0, 0, 0);
-        o[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, vf),
-                                                       __builtin_bit_cast(v8bf, pl[kc]), o[d], 0, 0, 0);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float pv = exp2f(sacc[kc >> 1][(kc & 1) * 8 + j] - m_use);
+          psum += pv;
+          const uint16_t hi = f32_to_bf16(pv);
+          pf[kc][j] = (short)hi;
+          pl[kc][j] = (short)f32_to_bf16(pv - bf16_to_f32(hi));
+        }
+      }
+      psum += __shfl_xor(psum, 32, 64);
+      l_run = l_run * alpha + psum;
+      m_run = m_new;
+#pragma unroll
+      for (int d = 0; d < NDS; ++d)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) o[d][e] *= alpha;
+      // ---- O^T += V^T P^T -------------------------------------------------
+      const uint8_t* vl = &vt_lds[buf][0];
+#pragma unroll
+      for (int d = 0; d < NDS; ++d) {
+        const int dr = d * 32 + col;
+#pragma unroll
+        for (int kc = 0; kc < 4; ++kc) {
+          const int lc = 2 * kc + half;
+          const v8s vf =
+              *reinterpret_cast<const v8s*>(vl + dr * (kBK * 2) + ((lc ^ ((dr >> 1) & 7)) * 16));
+          o[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, vf),
+                                                         __builtin_bit_cast(v8bf, pf[kc]), o[d], 0,
+                                                         0, 0);
+          o[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, vf),
+                                                         __builtin_bit_cast(v8bf, pl[kc]), o[d], 0,
+                                                         0, 0);
+        }
       }
     }
-    __syncthreads();
+    if (more) store_vt(buf ^ 1);
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's K rows landed in LDS
+    lds_barrier();
   }
 
   // ---- epilogue: lane holds query `col`, d = dt*32 + (i/4)*8 + half*4 + i%4
@@ -241,24 +319,25 @@ __global__ __launch_bounds__(NW * 64) void paged_attention_kernel(
   }
 }
 
-template <int D, int NW>
+template <int D, int HPB, int QSUB>
 int launch_attn(const void* q, int64_t q_ld, const void* kp, const void* vp, const int* cu_q,
-                const int* used, const int* table, int64_t table_ld, int seqs, int max_q, int HQ,
-                int HK, int page, float scale, int causal, void* out16, void* out8, int64_t o_ld,
-                float* scales, int64_t s_ld, hipStream_t stream) {
+                const int* used, const int* table, int64_t table_ld, int seqs, int max_q,
+                int max_used, int HQ, int HK, int page, float scale, int causal, void* out16,
+                void* out8, int64_t o_ld, float* scales, int64_t s_ld, hipStream_t stream) {
   const int G = HQ / HK;
-  dim3 grid((max_q + kBQ - 1) / kBQ, seqs, HK * (G / NW));
+  constexpr int BQ = 32 * QSUB;
+  dim3 grid((max_q + BQ - 1) / BQ, seqs, HK * (G / HPB));
   const float scale_log2 = scale * 1.4426950408889634f;
   if (out8) {
-    hipLaunchKernelGGL((paged_attention_kernel<D, NW, true>), grid, dim3(NW * 64), 0, stream,
-                       (const uint16_t*)q, q_ld, (const uint16_t*)kp, (const uint16_t*)vp, cu_q,
-                       used, table, table_ld, HQ, HK, page, scale_log2, causal, nullptr,
-                       (uint8_t*)out8, o_ld, scales, s_ld);
+    hipLaunchKernelGGL((paged_attention_kernel<D, HPB, QSUB, true>), grid, dim3(HPB * QSUB * 64),
+                       0, stream, (const uint16_t*)q, q_ld, (const uint16_t*)kp,
+                       (const uint16_t*)vp, cu_q, used, table, table_ld, max_used, HQ, HK, page,
+                       scale_log2, causal, nullptr, (uint8_t*)out8, o_ld, scales, s_ld);
   } else {
-    hipLaunchKernelGGL((paged_attention_kernel<D, NW, false>), grid, dim3(NW * 64), 0, stream,
-                       (const uint16_t*)q, q_ld, (const uint16_t*)kp, (const uint16_t*)vp, cu_q,
-                       used, table, table_ld, HQ, HK, page, scale_log2, causal,
-                       (uint16_t*)out16, nullptr, o_ld, nullptr, 0);
+    hipLaunchKernelGGL((paged_attention_kernel<D, HPB, QSUB, false>), grid, dim3(HPB * QSUB * 64),
+                       0, stream, (const uint16_t*)q, q_ld, (const uint16_t*)kp,
+                       (const uint16_t*)vp, cu_q, used, table, table_ld, max_used, HQ, HK, page,
+                       scale_log2, causal, (uint16_t*)out16, nullptr, o_ld, nullptr, 0);
   }
   QX_LAUNCH_STATUS();
 }
@@ -270,36 +349,42 @@ extern "C" {
 
 // out_fp8 != NULL: write the e4m3 o_proj input and its scales (D must be
 // 128); otherwise write bf16 to out_bf16. o_ld is in elements of the output.
+// max_used bounds every used[s] (FA's max_seqlen_k) and must be at most
+// 2048 * page (the page-table row each workgroup stages in LDS).
 int qx_paged_attention(const void* q, int64_t q_ld, const void* k_pool, const void* v_pool,
                        const int* cu_q, const int* used, const int* table, int64_t table_ld,
-                       int64_t seqs, int64_t max_q, int64_t HQ, int64_t HK, int64_t D,
-                       int64_t page, float scale, int causal, void* out_bf16, void* out_fp8,
-                       int64_t o_ld, float* scales, int64_t s_ld, hipStream_t stream) {
+                       int64_t seqs, int64_t max_q, int64_t max_used, int64_t HQ, int64_t HK,
+                       int64_t D, int64_t page, float scale, int causal, void* out_bf16,
+                       void* out_fp8, int64_t o_ld, float* scales, int64_t s_ld,
+                       hipStream_t stream) {
   QX_CHECK(q && k_pool && v_pool && cu_q && used && table, "attention: null pointer");
   QX_CHECK(out_bf16 || out_fp8, "attention: no output");
   QX_CHECK(D == 64 || D == 128, "attention: head_dim %lld", (long long)D);
   QX_CHECK(HQ > 0 && HK > 0 && HQ % HK == 0, "attention: heads %lld/%lld", (long long)HQ,
            (long long)HK);
   QX_CHECK(page > 0, "attention: page");
+  QX_CHECK(max_used >= 0 && max_used <= (int64_t)qx::kMaxPages * page,
+           "attention: max_used %lld exceeds %d pages", (long long)max_used, qx::kMaxPages);
   QX_CHECK(q_ld % 8 == 0 && o_ld % 4 == 0, "attention: strides");
   QX_CHECK(!out_fp8 || (D == 128 && scales), "attention: fused quant needs D=128 and scales");
   QX_CHECK(seqs < 65536, "attention: %lld sequences exceed the grid", (long long)seqs);
   if (seqs == 0 || max_q == 0) return QX_OK;
   const int G = (int)(HQ / HK);
-  const int nw = G % 4 == 0 ? 4 : (G % 2 == 0 ? 2 : 1);
-  const int args_seqs = (int)seqs, args_mq = (int)max_q;
-#define QX_ATTN(DD, NW_)                                                                     \
-  return qx::launch_attn<DD, NW_>(q, q_ld, k_pool, v_pool, cu_q, used, table, table_ld,      \
-                                  args_seqs, args_mq, (int)HQ, (int)HK, (int)page, scale,    \
-                                  causal, out_bf16, out_fp8, o_ld, scales, s_ld, stream)
+  const int hpb = G % 4 == 0 ? 4 : (G % 2 == 0 ? 2 : 1);
+  const int args_seqs = (int)seqs, args_mq = (int)max_q, args_mu = (int)max_used;
+#define QX_ATTN(DD, HPB_, QS_)                                                                  \
+  return qx::launch_attn<DD, HPB_, QS_>(q, q_ld, k_pool, v_pool, cu_q, used, table, table_ld,   \
+                                        args_seqs, args_mq, args_mu, (int)HQ, (int)HK,          \
+                                        (int)page, scale, causal, out_bf16, out_fp8, o_ld,      \
+                                        scales, s_ld, stream)
   if (D == 128) {
-    if (nw == 4) QX_ATTN(128, 4);
-    if (nw == 2) QX_ATTN(128, 2);
-    QX_ATTN(128, 1);
+    if (hpb == 4) QX_ATTN(128, 4, 2);
+    if (hpb == 2) QX_ATTN(128, 2, 4);
+    QX_ATTN(128, 1, 8);
   } else {
-    if (nw == 4) QX_ATTN(64, 4);
-    if (nw == 2) QX_ATTN(64, 2);
-    QX_ATTN(64, 1);
+    if (hpb == 4) QX_ATTN(64, 4, 2);
+    if (hpb == 2) QX_ATTN(64, 2, 4);
+    QX_ATTN(64, 1, 8);
   }
 #undef QX_ATTN
 }

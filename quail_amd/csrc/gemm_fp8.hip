@@ -11,18 +11,23 @@
 //   C  : M x N bf16, row-major, leading dimension ldc (elements)
 //
 // Design (MI355X / CDNA4):
-//   * one 128-wide K step is one scale group; per step each wave runs two
-//     v_mfma_f32_32x32x64_f8f6f4 per 32x32 output tile into a temporary and
-//     promotes it into the fp32 accumulator with the product of the two
-//     scales ("promotion": the scales change every 128 of K, so they cannot
-//     be applied once after the loop);
-//   * the MFMA "A" operand is the weight tile and "B" the token tile, so the
-//     32x32 output tile holds one token per lane column: the token scale
-//     sA[kb, m] is one value per lane per tile and the weight scale one
-//     value per wave;
-//   * operand tiles travel HBM -> LDS with global_load_lds_dwordx4 (no VGPR
-//     staging), double buffered; rows are 128 B with the 16-B chunk index
-//     XOR-swizzled by (row & 7), so fragment reads are bank-conflict free;
+//   * v_mfma_f32_32x32x64_f8f6f4 does the products; the MFMA "A" operand is
+//     the weight tile and "B" the token tile, so a 32x32 output tile holds
+//     one token per lane column: the token scale is one value per lane per
+//     tile and the weight scale one value per wave;
+//   * the scales change every 128 of K. Instead of promoting each 128-K
+//     partial from a temporary, the accumulator is kept in units of the
+//     current block's scale s = sA * sW: entering block kb it is multiplied
+//     by s_(kb-1) / s_kb and the MFMAs accumulate the raw FP8 products into
+//     it; the epilogue multiplies by the last block's scale. That is
+//     sum_kb s_kb P_kb as the reference defines it, with no temporaries and
+//     16 VALU multiplies per 32x32 tile per 128 of K. A block whose weight
+//     scale is 0 contributes nothing and is skipped;
+//   * operand tiles go HBM -> LDS with global_load_lds_dwordx4 (no VGPR
+//     staging) in 64-byte K slices through a STAGES-deep ring, so up to
+//     STAGES-1 slices are in flight while one is consumed. A slice row is
+//     64 B (4 chunks of 16 B), chunk-swizzled by ((row >> 2) & 3) so the 16
+//     rows of one ds_read_b128 phase cover all 64 LDS banks;
 //   * workgroups are remapped so each XCD (8 per MI355X, each with its own
 //     L2) runs a contiguous band of tiles that share operands.
 #include "qx_common.h"
@@ -33,36 +38,56 @@ namespace {
 
 typedef __attribute__((address_space(3))) void lds_void;
 
-template <int BM, int BN, int WAVES_N, int WAVES_M>
+constexpr int kSlice = 64;  // bytes of K per pipeline stage (one MFMA k-step)
+
+__device__ __forceinline__ int swz(int row) { return (row >> 2) & 3; }
+
+// s_waitcnt with vmcnt <= n and the other counters unconstrained (gfx9
+// encoding: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt_hi[15:14]).
+template <int n>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(n >= 0 && n < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((n & 15) | (7 << 4) | (15 << 8) | ((n >> 4) << 14));
+}
+
+template <int BM, int BN, int WAVES_N, int WAVES_M, int STAGES>
 struct GemmCfg {
-  static constexpr int kThreads = 64 * WAVES_N * WAVES_M;
+  static constexpr int kWaves = WAVES_N * WAVES_M;
+  static constexpr int kThreads = 64 * kWaves;
   static constexpr int kTN = BN / WAVES_N / 32;  // 32-row weight tiles per wave
   static constexpr int kTM = BM / WAVES_M / 32;  // 32-row token tiles per wave
-  static constexpr int kABytes = BM * 128;
-  static constexpr int kWBytes = BN * 128;
+  static constexpr int kABytes = BM * kSlice;
+  static constexpr int kWBytes = BN * kSlice;
   static constexpr int kStage = kABytes + kWBytes;
-  static constexpr int kLds = 2 * kStage;
+  static constexpr int kLds = STAGES * kStage;
+  static constexpr int kASlabs = BM / 16 / kWaves;  // 1 KiB (16-row) slabs per wave
+  static constexpr int kWSlabs = BN / 16 / kWaves;
+  // vector-memory ops one wave issues per stage: slabs + its token scales
+  static constexpr int kOpsPerStage = kASlabs + kWSlabs + kTM;
   static_assert(kTN >= 1 && kTM >= 1, "wave tile must hold a 32x32 MFMA tile");
-  static_assert(BM % (8 * WAVES_N * WAVES_M) == 0 && BN % (8 * WAVES_N * WAVES_M) == 0,
-                "each wave loads whole 8-row slabs");
+  static_assert(BM % (16 * kWaves) == 0 && BN % (16 * kWaves) == 0,
+                "each wave loads whole 16-row slabs");
+  static_assert(128 % (BN / WAVES_N) == 0 || (BN / WAVES_N) == 128,
+                "a wave's weight rows stay inside one 128-row scale block");
+  static_assert(kLds <= 160 * 1024, "LDS");
+  static_assert(STAGES >= 2, "stages");
+  static_assert((STAGES - 2) * kOpsPerStage < 64, "vmcnt");
 };
 
-// Issue this wave's share of one K step's tile loads (rows of 128 B) from
-// global memory straight into LDS. Each instruction moves 8 rows: lane i
-// writes LDS bytes [i*16, i*16+16) of the 1 KiB slab, i.e. row i/8, physical
-// chunk i%8, and therefore reads logical chunk (i%8) ^ (row & 7).
-template <int ROWS, int WAVES>
-__device__ __forceinline__ void load_tile(const uint8_t* __restrict__ g, int64_t ld, int row0,
-                                          int row_max, int64_t k_off, uint8_t* lds, int wave,
-                                          int lane) {
-  constexpr int kSlabs = ROWS / 8 / WAVES;
-  const int r_in = lane >> 3;
-  const int p = lane & 7;
+// This wave's share of one stage: 16-row slabs of 64 B. Lane i writes LDS
+// bytes [i*16, i*16+16) of its slab: row i/4, physical chunk i%4, so it
+// reads logical chunk (i%4) ^ swz(row).
+template <int SLABS>
+__device__ __forceinline__ void load_slabs(const uint8_t* __restrict__ g, int64_t ld, int row0,
+                                           int row_max, int64_t k_off, uint8_t* lds, int first,
+                                           int lane) {
+  const int r_in = lane >> 2;
+  const int p = lane & 3;
 #pragma unroll
-  for (int j = 0; j < kSlabs; ++j) {
-    const int slab = wave * kSlabs + j;
-    const int row = slab * 8 + r_in;
-    const int c = p ^ (row & 7);
+  for (int j = 0; j < SLABS; ++j) {
+    const int slab = first + j;
+    const int row = slab * 16 + r_in;
+    const int c = p ^ swz(row);
     int grow = row0 + row;
     grow = grow < row_max ? grow : row_max;  // tail rows re-read the last row
     const uint8_t* src = g + (int64_t)grow * ld + k_off + c * 16;
@@ -70,28 +95,27 @@ __device__ __forceinline__ void load_tile(const uint8_t* __restrict__ g, int64_t
   }
 }
 
-// One lane's 32-byte fragment of row `row` for K-half `half` (bytes
-// [half*64 + (lane/32)*32, +32) of the 128-B row), read through the swizzle.
-__device__ __forceinline__ v8i read_frag(const uint8_t* lds, int row, int half, int lane) {
-  const int c0 = half * 4 + (lane >> 5) * 2;
-  const int sw = row & 7;
-  const v4i* base = reinterpret_cast<const v4i*>(lds + row * 128);
-  v4i lo = base[c0 ^ sw];
-  v4i hi = base[(c0 + 1) ^ sw];
+// A lane's 32-byte MFMA fragment: bytes [(lane/32)*32, +32) of a 64-B row.
+__device__ __forceinline__ v8i read_frag(const uint8_t* lds, int row, int lane) {
+  const int c0 = (lane >> 5) * 2;
+  const int sw = swz(row);
+  const v4i* base = reinterpret_cast<const v4i*>(lds + row * kSlice);
+  const v4i lo = base[c0 ^ sw];
+  const v4i hi = base[(c0 + 1) ^ sw];
   v8i r;
   r[0] = lo[0]; r[1] = lo[1]; r[2] = lo[2]; r[3] = lo[3];
   r[4] = hi[0]; r[5] = hi[1]; r[6] = hi[2]; r[7] = hi[3];
   return r;
 }
 
-template <int BM, int BN, int WAVES_N, int WAVES_M>
-__global__ __launch_bounds__(64 * WAVES_N * WAVES_M, 1) void gemm_fp8_bs_kernel(
+template <int BM, int BN, int WAVES_N, int WAVES_M, int STAGES>
+__global__ __launch_bounds__(64 * WAVES_N * WAVES_M)
+__attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_fp8_bs_kernel(
     const uint8_t* __restrict__ A, const float* __restrict__ sA, const uint8_t* __restrict__ W,
     const float* __restrict__ sW, uint16_t* __restrict__ C, int M, int N, int K, int64_t lda,
     int64_t ldc, int64_t sa_ld, int tiles_m, int tiles_n, int group_m) {
-  using Cfg = GemmCfg<BM, BN, WAVES_N, WAVES_M>;
+  using Cfg = GemmCfg<BM, BN, WAVES_N, WAVES_M, STAGES>;
   constexpr int TN = Cfg::kTN, TM = Cfg::kTM;
-  constexpr int WAVES = WAVES_N * WAVES_M;
   __shared__ __attribute__((aligned(1024))) uint8_t smem[Cfg::kLds];
 
   // ---- tile scheduling: XCD-contiguous bands, grouped along M ----------
@@ -111,14 +135,14 @@ __global__ __launch_bounds__(64 * WAVES_N * WAVES_M, 1) void gemm_fp8_bs_kernel(
   const int tile_m = first_m + (id % width) % gsize;
   const int tile_n = (id % width) / gsize;
 
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
   const int wn = wave % WAVES_N;
   const int wm = wave / WAVES_N;
   const int m0 = tile_m * BM;
   const int n0 = tile_n * BN;
-  const int KT = K >> 7;
+  const int KT = K >> 7;        // scale blocks
+  const int KS = K / kSlice;    // pipeline slices (two per scale block)
 
   v16f acc[TN][TM];
 #pragma unroll
@@ -128,67 +152,86 @@ __global__ __launch_bounds__(64 * WAVES_N * WAVES_M, 1) void gemm_fp8_bs_kernel(
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[a][b][e] = 0.0f;
 
-  // this lane's tokens (one per token tile) and the scale rows it reads
   int tok[TM];
 #pragma unroll
   for (int b = 0; b < TM; ++b) {
-    int m = m0 + wm * TM * 32 + b * 32 + (lane & 31);
+    const int m = m0 + wm * TM * 32 + b * 32 + (lane & 31);
     tok[b] = m < M ? m : M - 1;
   }
-  int wblk[TN];
-#pragma unroll
-  for (int a = 0; a < TN; ++a) wblk[a] = ((n0 + wn * TN * 32 + a * 32) >> 7) * KT;
+  const float* sw_row = sW + (int64_t)((n0 + wn * TN * 32) >> 7) * KT;
 
-  // prologue: stage 0
-  load_tile<BM, WAVES>(A, lda, m0, M - 1, 0, smem, wave, lane);
-  load_tile<BN, WAVES>(W, K, n0, N - 1, 0, smem + Cfg::kABytes, wave, lane);
+  // sa_ring[s][b]: token scales of the scale block of the slice in stage s.
+  // The K loop below is unrolled by STAGES, so every stage index is a
+  // compile-time constant and the ring stays in registers.
+  float sa_ring[STAGES][TM];
+  auto issue = [&](int slice, int stage) {
+    uint8_t* buf = smem + stage * Cfg::kStage;
+    const int64_t k_off = (int64_t)slice * kSlice;
+    load_slabs<Cfg::kASlabs>(A, lda, m0, M - 1, k_off, buf, wave * Cfg::kASlabs, lane);
+    load_slabs<Cfg::kWSlabs>(W, K, n0, N - 1, k_off, buf + Cfg::kABytes, wave * Cfg::kWSlabs,
+                             lane);
+    const int64_t kb = slice >> 1;
+#pragma unroll
+    for (int b = 0; b < TM; ++b) sa_ring[stage][b] = sA[kb * sa_ld + tok[b]];
+  };
 
-  float sa_next[TM];
 #pragma unroll
-  for (int b = 0; b < TM; ++b) sa_next[b] = sA[tok[b]];
+  for (int s = 0; s < STAGES - 1; ++s)
+    if (s < KS) issue(s, s);
 
-  for (int kt = 0; kt < KT; ++kt) {
-    const int stage = kt & 1;
-    float sa[TM];
+  float s_prev[TM];
 #pragma unroll
-    for (int b = 0; b < TM; ++b) sa[b] = sa_next[b];
-    float sw[TN];
-#pragma unroll
-    for (int a = 0; a < TN; ++a) sw[a] = sW[wblk[a] + kt];
+  for (int b = 0; b < TM; ++b) s_prev[b] = 0.0f;
+  bool skip = false;
 
-    __builtin_amdgcn_s_waitcnt(0);  // this wave's LDS-bound loads landed
-    __syncthreads();                // ... and every other wave's
-    if (kt + 1 < KT) {
-      uint8_t* nxt = smem + (stage ^ 1) * Cfg::kStage;
-      const int64_t k_off = (int64_t)(kt + 1) * 128;
-      load_tile<BM, WAVES>(A, lda, m0, M - 1, k_off, nxt, wave, lane);
-      load_tile<BN, WAVES>(W, K, n0, N - 1, k_off, nxt + Cfg::kABytes, wave, lane);
+  for (int base = 0; base < KS; base += STAGES) {
 #pragma unroll
-      for (int b = 0; b < TM; ++b) sa_next[b] = sA[(int64_t)(kt + 1) * sa_ld + tok[b]];
-    }
+    for (int stage = 0; stage < STAGES; ++stage) {
+      const int ks = base + stage;
+      if (ks < KS) {
+        // slices ks+1 .. ks+STAGES-2 may stay in flight
+        if (ks + STAGES - 2 < KS) {
+          wait_vmcnt<(STAGES - 2) * Cfg::kOpsPerStage>();
+        } else {
+          wait_vmcnt<0>();
+        }
+        lds_barrier();
+        if (ks + STAGES - 1 < KS) issue(ks + STAGES - 1, (stage + STAGES - 1) % STAGES);
 
-    const uint8_t* sa_lds = smem + stage * Cfg::kStage;
-    const uint8_t* sw_lds = sa_lds + Cfg::kABytes;
-    v8i wf[2][TN], af[2][TM];
+        if ((ks & 1) == 0) {
+          // entering scale block kb: acc <- acc * s_prev / s_kb
+          const float sw = sw_row[ks >> 1];
+          skip = sw == 0.0f;  // wave-uniform
+          if (!skip) {
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
+            for (int b = 0; b < TM; ++b) {
+              const float s_cur = sa_ring[stage][b] * sw;
+              const float r = s_prev[b] / s_cur;  // 0 until the first block
 #pragma unroll
-      for (int a = 0; a < TN; ++a)
-        wf[h][a] = read_frag(sw_lds, wn * TN * 32 + a * 32 + (lane & 31), h, lane);
+              for (int a = 0; a < TN; ++a)
 #pragma unroll
-      for (int b = 0; b < TM; ++b)
-        af[h][b] = read_frag(sa_lds, wm * TM * 32 + b * 32 + (lane & 31), h, lane);
-    }
+                for (int e = 0; e < 16; ++e) acc[a][b][e] *= r;
+              s_prev[b] = s_cur;
+            }
+          }
+        }
+        if (!skip) {
+          const uint8_t* a_lds = smem + stage * Cfg::kStage;
+          const uint8_t* w_lds = a_lds + Cfg::kABytes;
+          v8i wf[TN], af[TM];
 #pragma unroll
-    for (int a = 0; a < TN; ++a) {
+          for (int a = 0; a < TN; ++a)
+            wf[a] = read_frag(w_lds, wn * TN * 32 + a * 32 + (lane & 31), lane);
 #pragma unroll
-      for (int b = 0; b < TM; ++b) {
-        v16f p = {};
-        p = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(wf[0][a], af[0][b], p, 0, 0, 0, 0, 0, 0);
-        p = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(wf[1][a], af[1][b], p, 0, 0, 0, 0, 0, 0);
-        const float s = sa[b] * sw[a];
+          for (int b = 0; b < TM; ++b)
+            af[b] = read_frag(a_lds, wm * TM * 32 + b * 32 + (lane & 31), lane);
 #pragma unroll
-        for (int e = 0; e < 16; ++e) acc[a][b][e] = fmaf(p[e], s, acc[a][b][e]);
+          for (int a = 0; a < TN; ++a)
+#pragma unroll
+            for (int b = 0; b < TM; ++b)
+              acc[a][b] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+                  wf[a], af[b], acc[a][b], 0, 0, 0, 0, 0, 0);
+        }
       }
     }
   }
@@ -198,6 +241,7 @@ __global__ __launch_bounds__(64 * WAVES_N * WAVES_M, 1) void gemm_fp8_bs_kernel(
   for (int b = 0; b < TM; ++b) {
     const int m = m0 + wm * TM * 32 + b * 32 + (lane & 31);
     if (m >= M) continue;
+    const float s = s_prev[b];
     uint16_t* crow = C + (int64_t)m * ldc;
 #pragma unroll
     for (int a = 0; a < TN; ++a) {
@@ -205,22 +249,22 @@ __global__ __launch_bounds__(64 * WAVES_N * WAVES_M, 1) void gemm_fp8_bs_kernel(
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         uint2 v;
-        v.x = pack2_bf16(acc[a][b][g * 4 + 0], acc[a][b][g * 4 + 1]);
-        v.y = pack2_bf16(acc[a][b][g * 4 + 2], acc[a][b][g * 4 + 3]);
+        v.x = pack2_bf16(acc[a][b][g * 4 + 0] * s, acc[a][b][g * 4 + 1] * s);
+        v.y = pack2_bf16(acc[a][b][g * 4 + 2] * s, acc[a][b][g * 4 + 3] * s);
         *reinterpret_cast<uint2*>(crow + nbase + g * 8) = v;
       }
     }
   }
 }
 
-template <int BM, int BN, int WN, int WM>
+template <int BM, int BN, int WN, int WM, int ST>
 int launch(const void* A, const float* sA, const void* W, const float* sW, void* C, int M, int N,
            int K, int64_t lda, int64_t ldc, int64_t sa_ld, int group_m, hipStream_t stream) {
-  using Cfg = GemmCfg<BM, BN, WN, WM>;
+  using Cfg = GemmCfg<BM, BN, WN, WM, ST>;
   const int tiles_m = (M + BM - 1) / BM;
   const int tiles_n = N / BN;
   const int total = tiles_m * tiles_n;
-  hipLaunchKernelGGL((gemm_fp8_bs_kernel<BM, BN, WN, WM>), dim3(total), dim3(Cfg::kThreads), 0,
+  hipLaunchKernelGGL((gemm_fp8_bs_kernel<BM, BN, WN, WM, ST>), dim3(total), dim3(Cfg::kThreads), 0,
                      stream, (const uint8_t*)A, sA, (const uint8_t*)W, sW, (uint16_t*)C, M, N, K,
                      lda, ldc, sa_ld, tiles_m, tiles_n, group_m < 1 ? 1 : group_m);
   QX_LAUNCH_STATUS();
@@ -231,8 +275,10 @@ int launch(const void* A, const float* sA, const void* W, const float* sW, void*
 
 extern "C" {
 
-// Tile configurations: 0 = 128 tokens x 256 weights (default), 1 = 256 x 256,
-// 2 = 128 x 128. Chosen by the caller per shape; all give the same result.
+// Tile configurations (tokens x weights, waves, 64-byte K stages); all give
+// the same result: 0: 256x256, 8 waves, 4; 1: 256x256, 4 waves, 4;
+// 2: 128x128, 4 waves, 4; 3: 128x256, 4 waves, 3; 4: 256x128, 4 waves, 3;
+// 5: 256x128, 4 waves, 2; 6: 256x128, 4 waves, 4.
 int qx_gemm_fp8_blockscaled(const void* A, const float* sA, const void* W, const float* sW,
                             void* C, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldc,
                             int64_t sa_ld, int config, hipStream_t stream) {
@@ -253,12 +299,21 @@ int qx_gemm_fp8_blockscaled(const void* A, const float* sA, const void* W, const
   switch (config) {
     case 0:
       QX_CHECK(n % 256 == 0, "gemm config 0 needs N %% 256 == 0 (N=%d)", n);
-      return qx::launch<128, 256, 2, 2>(A, sA, W, sW, C, m, n, k, lda, ldc, sa_ld, 8, stream);
+      return qx::launch<256, 256, 2, 4, 4>(A, sA, W, sW, C, m, n, k, lda, ldc, sa_ld, 4, stream);
     case 1:
       QX_CHECK(n % 256 == 0, "gemm config 1 needs N %% 256 == 0 (N=%d)", n);
-      return qx::launch<256, 256, 2, 2>(A, sA, W, sW, C, m, n, k, lda, ldc, sa_ld, 4, stream);
+      return qx::launch<256, 256, 2, 2, 4>(A, sA, W, sW, C, m, n, k, lda, ldc, sa_ld, 4, stream);
     case 2:
-      return qx::launch<128, 128, 2, 2>(A, sA, W, sW, C, m, n, k, lda, ldc, sa_ld, 8, stream);
+      return qx::launch<128, 128, 2, 2, 4>(A, sA, W, sW, C, m, n, k, lda, ldc, sa_ld, 8, stream);
+    case 3:
+      QX_CHECK(n % 256 == 0, "gemm config 3 needs N %% 256 == 0 (N=%d)", n);
+      return qx::launch<128, 256, 2, 2, 3>(A, sA, W, sW, C, m, n, k, lda, ldc, sa_ld, 8, stream);
+    case 4:
+      return qx::launch<256, 128, 1, 4, 3>(A, sA, W, sW, C, m, n, k, lda, ldc, sa_ld, 8, stream);
+    case 5:
+      return qx::launch<256, 128, 1, 4, 2>(A, sA, W, sW, C, m, n, k, lda, ldc, sa_ld, 8, stream);
+    case 6:
+      return qx::launch<256, 128, 1, 4, 4>(A, sA, W, sW, C, m, n, k, lda, ldc, sa_ld, 8, stream);
     default:
       QX_CHECK(false, "gemm: unknown config %d", config);
   }

@@ -77,6 +77,15 @@ __device__ __forceinline__ float group_sum(float v) {
   return v;
 }
 
+// Workgroup barrier with no memory fence. __syncthreads() (and an
+// LDS-scoped fence) make the compiler drain every vector-memory load in
+// flight before s_barrier, including the global->LDS prefetches of later
+// pipeline stages. Kernels using this barrier wait for their own LDS-bound
+// loads explicitly (s_waitcnt vmcnt) and consume every ds_read result before
+// the barrier; the "memory" clobber keeps the compiler from moving memory
+// accesses across it.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_barrier" ::: "memory"); }
+
 // Per-group FP8 scale: max(amax, 1e-10) / 448 (attention.py:780-781).
 __device__ __forceinline__ float fp8_scale(float amax) {
   return fmaxf(amax, kScaleFloor) / kFp8Max;

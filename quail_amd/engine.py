@@ -24,10 +24,11 @@ from quail_amd import _lib
 
 GROUP = 128
 
-# GEMM tile configuration per (N, K): 0 = 128 tokens x 256 weights,
-# 1 = 256 x 256, 2 = 128 x 128 (see csrc/gemm_fp8.hip). Weight widths that
-# are not multiples of 256 use 2.
+# GEMM tile configuration (see csrc/gemm_fp8.hip): 5 = 256 tokens x 128
+# weights, 4 waves, two 64-byte K stages (48 KiB LDS, two workgroups per CU)
+# measured fastest on the Qwen3 shapes; QUAIL_GEMM_CONFIG overrides it.
 GEMM_CONFIG_ENV = "QUAIL_GEMM_CONFIG"
+GEMM_DEFAULT_CONFIG = 5
 
 
 def _ptr(t):
@@ -42,9 +43,7 @@ def gemm_config(n: int, k: int, m: int) -> int:
     forced = os.environ.get(GEMM_CONFIG_ENV)
     if forced is not None:
         return int(forced)
-    if n % 256:
-        return 2
-    return 0
+    return GEMM_DEFAULT_CONFIG
 
 
 class Engine:
@@ -298,7 +297,7 @@ class Engine:
         if d == GROUP:
             _lib.call("qx_paged_attention", _ptr(q3), q_ld, _ptr(k_pool), _ptr(v_pool),
                       _ptr(unified["cu_q"]), _ptr(unified["used"]), _ptr(table),
-                      table.stride(0), seqs, int(unified["max_q"]), hq, hk, d,
+                      table.stride(0), seqs, int(unified["max_q"]), int(unified["max_used"]), hq, hk, d,
                       self.arena.page_tokens, float(scale), int(unified.get("causal", True)),
                       None, _ptr(o_q), o_q.stride(0), _ptr(o_s), self._scale_ld(o_s), _stream())
         else:
@@ -306,7 +305,7 @@ class Engine:
             o = torch.empty((n, hq * d), dtype=torch.bfloat16, device=q3.device)
             _lib.call("qx_paged_attention", _ptr(q3), q_ld, _ptr(k_pool), _ptr(v_pool),
                       _ptr(unified["cu_q"]), _ptr(unified["used"]), _ptr(table),
-                      table.stride(0), seqs, int(unified["max_q"]), hq, hk, d,
+                      table.stride(0), seqs, int(unified["max_q"]), int(unified["max_used"]), hq, hk, d,
                       self.arena.page_tokens, float(scale), int(unified.get("causal", True)),
                       _ptr(o), None, o.stride(0), None, 0, _stream())
             self.quant(o, output=(o_q, o_s))
@@ -323,7 +322,8 @@ class Engine:
         table = unified["table"]
         _lib.call("qx_paged_attention", _ptr(q3), q3.stride(0), _ptr(k_pool), _ptr(v_pool),
                   _ptr(unified["cu_q"]), _ptr(unified["used"]), _ptr(table), table.stride(0),
-                  unified["used"].shape[0], int(unified["max_q"]), hq, hk, d,
+                  unified["used"].shape[0], int(unified["max_q"]), int(unified["max_used"]),
+                  hq, hk, d,
                   self.arena.page_tokens, float(d ** -0.5), int(unified.get("causal", True)),
                   _ptr(o), None, o.stride(0), None, 0, _stream())
         return o

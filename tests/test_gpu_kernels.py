@@ -98,7 +98,7 @@ def test_gemm_small_shapes_match_dequantized_matmul(m, n, k):
     _bf16_close(out, want)
 
 
-@pytest.mark.parametrize("config", [0, 1, 2])
+@pytest.mark.parametrize("config", [0, 1, 2, 3, 4, 5, 6])
 def test_gemm_tile_configs_agree(config, monkeypatch):
     q, s, wq, ws = _gemm_case(300, 512, 512, seed=9)
     monkeypatch.setenv("QUAIL_GEMM_CONFIG", str(config))
@@ -297,7 +297,8 @@ def test_paged_attention_matches_exact_fp32(hq, hk, d):
     meta = dict(unified=dict(cu_q=torch.tensor(cu, device=DEV),
                              used=torch.tensor(used, device=DEV),
                              table=torch.tensor(table, device=DEV),
-                             max_q=int(np.diff(cu).max()), causal=True))
+                             max_q=int(np.diff(cu).max()), max_used=int(used.max()),
+                             causal=True))
     got = eng.attention_bf16(q.to(DEV), meta, 0)
     torch.testing.assert_close(got.float().cpu().view_as(want), want.float(), rtol=2e-2, atol=2e-2)
     if d == 128:

@@ -27,8 +27,8 @@ def test_argument_errors_return_minus_one_with_a_message():
         _lib.call("qx_gemm_fp8_blockscaled", 16, 16, 16, 16, 16, 1, 256, 100, 128, 256, 1, 0,
                   None)
     with pytest.raises(_lib.QxError, match="head_dim"):
-        _lib.call("qx_paged_attention", 16, 8, 16, 16, 16, 16, 16, 1, 1, 1, 4, 2, 96, 16, 0.1,
-                  1, 16, None, 8, None, 0, None)
+        _lib.call("qx_paged_attention", 16, 8, 16, 16, 16, 16, 16, 1, 1, 1, 64, 4, 2, 96, 16,
+                  0.1, 1, 16, None, 8, None, 0, None)
     with pytest.raises(_lib.QxError, match="1..16"):
         _lib.call("qx_answer_head", 16, 8, 16, 8, 17, 1, 8, 0, None, 1.0, None, None, None,
                   None, None)
