@@ -29,8 +29,9 @@
 // Each wave forms S^T = K Q^T with v_mfma_f32_32x32x16_bf16 so that a lane
 // owns one query column; the online softmax is then lane-local (plus one
 // cross-half shuffle), P^T feeds the PV MFMA directly as its B operand, and
-// O^T keeps one query per lane, so rescaling needs no shuffles. P enters the
-// PV MFMA as a bf16 hi/lo pair, so the output carries fp32-level accuracy.
+// O^T keeps one query per lane, so rescaling needs no shuffles. The PV product
+// runs in fp16: P in (0, 1] keeps 11 significant bits (bf16 would keep 8),
+// and bf16 V converts to fp16 exactly for |v| in [2^-14, 65504].
 #include "qx_common.h"
 #include "qx_status.h"
 
@@ -40,6 +41,7 @@ namespace {
 typedef __attribute__((address_space(3))) void lds_void;
 
 constexpr int kBK = 64;          // keys per KV tile
+constexpr int kPage = 16;        // tokens per arena page
 constexpr int kMaxPages = 2048;  // page-table entries staged in LDS per sequence
 
 // position of key k (0..15) inside its 16-key group of the transposed V tile:
@@ -55,7 +57,7 @@ template <int D, int HPB, int QSUB, bool QUANT>
 __global__ __launch_bounds__(HPB * QSUB * 64) void paged_attention_kernel(
     const uint16_t* __restrict__ q, int64_t q_ld, const uint16_t* __restrict__ kp,
     const uint16_t* __restrict__ vp, const int* __restrict__ cu_q, const int* __restrict__ used,
-    const int* __restrict__ table, int64_t table_ld, int max_used, int HQ, int HK, int page,
+    const int* __restrict__ table, int64_t table_ld, int max_used, int HQ, int HK,
     float scale_log2, int causal, uint16_t* __restrict__ out16, uint8_t* __restrict__ out8,
     int64_t o_ld, float* __restrict__ scales, int64_t s_ld) {
   constexpr int NW = HPB * QSUB;
@@ -105,7 +107,7 @@ __global__ __launch_bounds__(HPB * QSUB * 64) void paged_attention_kernel(
 
   // stage the page-table row
   const int* trow = table + (int64_t)s * table_ld;
-  const int npages = (kv_end + page - 1) / page;
+  const int npages = (kv_end + kPage - 1) / kPage;
   for (int i = tid; i < npages; i += NT) pages_lds[i] = trow[i];
 
   // Q^T fragments (B operand): lane holds query `col`, d = c*16 + half*8 .. +8
@@ -124,7 +126,7 @@ __global__ __launch_bounds__(HPB * QSUB * 64) void paged_attention_kernel(
 
   auto pool_row = [&](int kidx) -> int64_t {
     kidx = kidx < kv_end ? kidx : kv_end - 1;  // tail keys re-read the last key (masked)
-    return (int64_t)pages_lds[kidx / page] * page + (kidx % page);
+    return (int64_t)pages_lds[kidx / kPage] * kPage + (kidx % kPage);
   };
   // K rows of tile t straight into LDS: lane i of a slab writes bytes
   // [16i, 16i+16): key i / KCH of the slab, physical chunk i % KCH
@@ -141,12 +143,14 @@ __global__ __launch_bounds__(HPB * QSUB * 64) void paged_attention_kernel(
     }
   };
   uint4 vreg[V_UNITS][2];
+  // V work unit: (key pair, 8-column chunk dc) with key pairs fastest, so one
+  // ds_write_b32 instruction of a wave fills whole transposed rows
   auto fetch_v = [&](int t) {
 #pragma unroll
     for (int u = 0; u < V_UNITS; ++u) {
       const int unit = tid + u * NT;
       if (unit < V_TOTAL) {
-        const int key = (unit / KCH) * 2, dc = unit % KCH;
+        const int key = (unit % (kBK / 2)) * 2, dc = unit / (kBK / 2);
         vreg[u][0] =
             *reinterpret_cast<const uint4*>(vbase + pool_row(t * kBK + key) * kv_row + dc * 8);
         vreg[u][1] =
@@ -159,18 +163,21 @@ __global__ __launch_bounds__(HPB * QSUB * 64) void paged_attention_kernel(
     for (int u = 0; u < V_UNITS; ++u) {
       const int unit = tid + u * NT;
       if (unit < V_TOTAL) {
-        const int key = (unit / KCH) * 2, dc = unit % KCH;
+        const int key = (unit % (kBK / 2)) * 2, dc = unit / (kBK / 2);
         const uint32_t aw[4] = {vreg[u][0].x, vreg[u][0].y, vreg[u][0].z, vreg[u][0].w};
         const uint32_t bw[4] = {vreg[u][1].x, vreg[u][1].y, vreg[u][1].z, vreg[u][1].w};
         const int pos = (key >> 4) * 16 + vt_pos(key & 15);  // even; pos+1 holds key+1
         const int chunk = pos >> 3, within = (pos & 7) * 2;
+        // lanes of odd chunks write the rows in rotated order, so the two
+        // chunks of a wave land in opposite 32-bank halves
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
+        for (int e0 = 0; e0 < 8; ++e0) {
+          const int e = (e0 + (dc & 1)) & 7;
           const int d = dc * 8 + e;
-          const uint32_t lo = (e & 1) ? (aw[e >> 1] >> 16) : (aw[e >> 1] & 0xffffu);
-          const uint32_t hi = (e & 1) ? (bw[e >> 1] >> 16) : (bw[e >> 1] & 0xffffu);
+          const float lo = (e & 1) ? hi_bf16(aw[e >> 1]) : lo_bf16(aw[e >> 1]);
+          const float hi = (e & 1) ? hi_bf16(bw[e >> 1]) : lo_bf16(bw[e >> 1]);
           *reinterpret_cast<uint32_t*>(&vt_lds[buf][0] + d * (kBK * 2) +
-                                       ((chunk ^ ((d >> 1) & 7)) * 16) + within) = lo | (hi << 16);
+                                       ((chunk ^ ((d >> 1) & 7)) * 16) + within) = pack2_f16(lo, hi);
         }
       }
     }
@@ -183,6 +190,11 @@ __global__ __launch_bounds__(HPB * QSUB * 64) void paged_attention_kernel(
     for (int e = 0; e < 16; ++e) o[d][e] = 0.f;
   float m_run = -INFINITY, l_run = 0.f;
   const int lim = causal ? min(off + r + 1, used_s) : used_s;  // keys < lim are visible
+  // the smallest visible-key limit over this wave's rows, and whether all 32
+  // of its rows are real: tiles below that limit skip the mask
+  const int wave_first = qt * BQ + qsub * 32;
+  const int wave_lim_min = causal ? min(off + wave_first + 1, used_s) : used_s;
+  const bool wave_rows_full = wave_first + 32 <= q_len;
 
   if (ntiles > 0) {
     // prologue: tile 0 into buffer 0
@@ -193,8 +205,9 @@ __global__ __launch_bounds__(HPB * QSUB * 64) void paged_attention_kernel(
     lds_barrier();
   }
 
-  for (int t = 0; t < ntiles; ++t) {
-    const int buf = t & 1;
+  // one KV tile; `buf` is a literal at both call sites below, so every LDS
+  // address is a per-lane base plus a constant offset
+  auto tile = [&](const int t, const int buf) {
     const bool more = t + 1 < ntiles;
     if (more) {
       issue_k(t + 1, buf ^ 1);
@@ -204,78 +217,104 @@ __global__ __launch_bounds__(HPB * QSUB * 64) void paged_attention_kernel(
     if (t0 < wave_end) {  // wave-uniform: a tile wholly past this wave's rows is skipped
       // ---- S^T = K Q^T for two 32-key subtiles -------------------------
       const uint8_t* kl = &k_lds[buf][0];
-      v16f sacc[2];
+      // four independent accumulator chains (2 key subtiles x even/odd d
+      // steps), so consecutive MFMAs never wait on each other
+      v16f sacc[2], sodd[2];
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
-        v16f a = {};
-        const int key = ks * 32 + col;
-#pragma unroll
-        for (int c = 0; c < ND16; ++c) {
-          const int lc = 2 * c + half;
-          const v8s kf = *reinterpret_cast<const v8s*>(kl + key * KROW + ((lc ^ kswz<D>(key)) * 16));
-          a = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, kf),
-                                                      __builtin_bit_cast(v8bf, qf[c]), a, 0, 0, 0);
-        }
-        sacc[ks] = a;
+        sacc[ks] = v16f{};
+        sodd[ks] = v16f{};
       }
-      // ---- mask, online softmax (lane = one query; partner lane^32) -----
-      float tmax = -INFINITY;
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks)
+      for (int c = 0; c < ND16; ++c) {
+        const int lc = 2 * c + half;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int kidx = t0 + ks * 32 + (i >> 2) * 8 + half * 4 + (i & 3);
-          float v = sacc[ks][i] * scale_log2;
-          v = (kidx < lim && r_ok) ? v : -INFINITY;
-          sacc[ks][i] = v;
-          tmax = fmaxf(tmax, v);
+        for (int ks = 0; ks < 2; ++ks) {
+          const int key = ks * 32 + col;
+          const v8s kf = *reinterpret_cast<const v8s*>(kl + key * KROW + ((lc ^ kswz<D>(key)) * 16));
+          if (c & 1)
+            sodd[ks] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                __builtin_bit_cast(v8bf, kf), __builtin_bit_cast(v8bf, qf[c]), sodd[ks], 0, 0, 0);
+          else
+            sacc[ks] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                __builtin_bit_cast(v8bf, kf), __builtin_bit_cast(v8bf, qf[c]), sacc[ks], 0, 0, 0);
         }
+      }
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) sacc[ks] += sodd[ks];
+      // ---- mask, online softmax (lane = one query; partner lane^32) -----
+      // a tile every row of this wave sees whole needs no mask
+      const bool full = t0 + kBK <= wave_lim_min && wave_rows_full;
+      // the running max is kept on raw scores (scale_log2 > 0), and the scale
+      // folds into one fma per score: p = exp2(s * scale_log2 - m * scale_log2)
+      float tmax = -INFINITY;
+      if (full) {
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) tmax = fmaxf(tmax, sacc[ks][i]);
+      } else {
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const int kidx = t0 + ks * 32 + (i >> 2) * 8 + half * 4 + (i & 3);
+            const float v = (kidx < lim && r_ok) ? sacc[ks][i] : -INFINITY;
+            sacc[ks][i] = v;
+            tmax = fmaxf(tmax, v);
+          }
+      }
       tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
       const float m_new = fmaxf(m_run, tmax);
-      const float m_use = m_new == -INFINITY ? 0.f : m_new;
-      const float alpha = exp2f(m_run - m_use);
+      const float m_use = m_new == -INFINITY ? 0.f : m_new * scale_log2;
+      const float alpha = __builtin_amdgcn_exp2f(m_run * scale_log2 - m_use);
       float psum = 0.f;
-      v8s pf[4], pl[4];
+      v8h pf[4];
 #pragma unroll
       for (int kc = 0; kc < 4; ++kc) {
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-          const float pv = exp2f(sacc[kc >> 1][(kc & 1) * 8 + j] - m_use);
+          // arguments are <= 0, so v_exp_f32's range is all that is needed
+          const float pv =
+              __builtin_amdgcn_exp2f(fmaf(sacc[kc >> 1][(kc & 1) * 8 + j], scale_log2, -m_use));
           psum += pv;
-          const uint16_t hi = f32_to_bf16(pv);
-          pf[kc][j] = (short)hi;
-          pl[kc][j] = (short)f32_to_bf16(pv - bf16_to_f32(hi));
+          pf[kc][j] = (_Float16)pv;
         }
       }
       psum += __shfl_xor(psum, 32, 64);
       l_run = l_run * alpha + psum;
+      // rescale O only when some lane's running max moved
+      if (__builtin_amdgcn_ballot_w64(m_new != m_run) != 0) {
+#pragma unroll
+        for (int d = 0; d < NDS; ++d)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) o[d][e] *= alpha;
+      }
       m_run = m_new;
-#pragma unroll
-      for (int d = 0; d < NDS; ++d)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) o[d][e] *= alpha;
       // ---- O^T += V^T P^T -------------------------------------------------
       const uint8_t* vl = &vt_lds[buf][0];
+      // d tiles innermost: NDS independent accumulators between dependent MFMAs
 #pragma unroll
-      for (int d = 0; d < NDS; ++d) {
-        const int dr = d * 32 + col;
+      for (int kc = 0; kc < 4; ++kc) {
+        const int lc = 2 * kc + half;
+        v8h vf[NDS];
 #pragma unroll
-        for (int kc = 0; kc < 4; ++kc) {
-          const int lc = 2 * kc + half;
-          const v8s vf =
-              *reinterpret_cast<const v8s*>(vl + dr * (kBK * 2) + ((lc ^ ((dr >> 1) & 7)) * 16));
-          o[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, vf),
-                                                         __builtin_bit_cast(v8bf, pf[kc]), o[d], 0,
-                                                         0, 0);
-          o[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, vf),
-                                                         __builtin_bit_cast(v8bf, pl[kc]), o[d], 0,
-                                                         0, 0);
+        for (int d = 0; d < NDS; ++d) {
+          const int dr = d * 32 + col;
+          vf[d] = *reinterpret_cast<const v8h*>(vl + dr * (kBK * 2) + ((lc ^ ((dr >> 1) & 7)) * 16));
         }
+#pragma unroll
+        for (int d = 0; d < NDS; ++d)
+          o[d] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[d], pf[kc], o[d], 0, 0, 0);
       }
     }
     if (more) store_vt(buf ^ 1);
     __builtin_amdgcn_s_waitcnt(0);  // this wave's K rows landed in LDS
     lds_barrier();
+  };
+  for (int t = 0; t < ntiles; t += 2) {
+    tile(t, 0);
+    if (t + 1 < ntiles) tile(t + 1, 1);
   }
 
   // ---- epilogue: lane holds query `col`, d = dt*32 + (i/4)*8 + half*4 + i%4
@@ -331,12 +370,12 @@ int launch_attn(const void* q, int64_t q_ld, const void* kp, const void* vp, con
   if (out8) {
     hipLaunchKernelGGL((paged_attention_kernel<D, HPB, QSUB, true>), grid, dim3(HPB * QSUB * 64),
                        0, stream, (const uint16_t*)q, q_ld, (const uint16_t*)kp,
-                       (const uint16_t*)vp, cu_q, used, table, table_ld, max_used, HQ, HK, page,
+                       (const uint16_t*)vp, cu_q, used, table, table_ld, max_used, HQ, HK,
                        scale_log2, causal, nullptr, (uint8_t*)out8, o_ld, scales, s_ld);
   } else {
     hipLaunchKernelGGL((paged_attention_kernel<D, HPB, QSUB, false>), grid, dim3(HPB * QSUB * 64),
                        0, stream, (const uint16_t*)q, q_ld, (const uint16_t*)kp,
-                       (const uint16_t*)vp, cu_q, used, table, table_ld, max_used, HQ, HK, page,
+                       (const uint16_t*)vp, cu_q, used, table, table_ld, max_used, HQ, HK,
                        scale_log2, causal, (uint16_t*)out16, nullptr, o_ld, nullptr, 0);
   }
   QX_LAUNCH_STATUS();
@@ -362,7 +401,7 @@ int qx_paged_attention(const void* q, int64_t q_ld, const void* k_pool, const vo
   QX_CHECK(D == 64 || D == 128, "attention: head_dim %lld", (long long)D);
   QX_CHECK(HQ > 0 && HK > 0 && HQ % HK == 0, "attention: heads %lld/%lld", (long long)HQ,
            (long long)HK);
-  QX_CHECK(page > 0, "attention: page");
+  QX_CHECK(page == qx::kPage, "attention: page of %lld tokens (the arena uses 16)", (long long)page);
   QX_CHECK(max_used >= 0 && max_used <= (int64_t)qx::kMaxPages * page,
            "attention: max_used %lld exceeds %d pages", (long long)max_used, qx::kMaxPages);
   QX_CHECK(q_ld % 8 == 0 && o_ld % 4 == 0, "attention: strides");
