@@ -257,6 +257,399 @@ __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_fp8_bs_kernel(
   }
 }
 
+
+// ---------------------------------------------------------------------------
+// Variant with local-read prefetch: the MFMA fragments of slice ks+1 are read
+// from LDS while the MFMAs of slice ks run, so a wave leaving the barrier has
+// its MFMA operands in registers already. The token scales of each slice are
+// staged in LDS by the same direct loads (one dword per lane), so no register
+// array is indexed by a run-time stage. STAGES >= 3 (slice ks+1 must be waited
+// for while slice ks+2 may still be in flight).
+template <int BM, int BN, int WAVES_N, int WAVES_M, int STAGES>
+struct PlrCfg {
+  static constexpr int kWaves = WAVES_N * WAVES_M;
+  static constexpr int kThreads = 64 * kWaves;
+  static constexpr int kTN = BN / WAVES_N / 32;
+  static constexpr int kTM = BM / WAVES_M / 32;
+  static constexpr int kABytes = BM * kSlice;
+  static constexpr int kWBytes = BN * kSlice;
+  static constexpr int kSaBytes = kWaves * 256;  // each wave stages 64 token scales
+  static constexpr int kStage = kABytes + kWBytes + kSaBytes;
+  static constexpr int kLds = STAGES * kStage;
+  static constexpr int kASlabs = BM / 16 / kWaves;
+  static constexpr int kWSlabs = BN / 16 / kWaves;
+  static constexpr int kOpsPerStage = kASlabs + kWSlabs + 1;
+  static_assert(STAGES >= 3, "local-read prefetch needs three stages");
+  static_assert(kTN >= 1 && kTM >= 1, "wave tile");
+  static_assert(BM % (16 * kWaves) == 0 && BN % (16 * kWaves) == 0, "slabs");
+  static_assert(128 % (BN / WAVES_N) == 0 || (BN / WAVES_N) == 128, "weight scale block");
+  static_assert(BM <= 64 * kWaves, "token scales staged by the waves");
+  static_assert(kLds <= 160 * 1024, "LDS");
+  static_assert((STAGES - 3) * kOpsPerStage < 64, "vmcnt");
+};
+
+template <int BM, int BN, int WAVES_N, int WAVES_M, int STAGES>
+__global__ __launch_bounds__(64 * WAVES_N * WAVES_M)
+__attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_fp8_plr_kernel(
+    const uint8_t* __restrict__ A, const float* __restrict__ sA, const uint8_t* __restrict__ W,
+    const float* __restrict__ sW, uint16_t* __restrict__ C, int M, int N, int K, int64_t lda,
+    int64_t ldc, int64_t sa_ld, int tiles_m, int tiles_n, int group_m) {
+  using Cfg = PlrCfg<BM, BN, WAVES_N, WAVES_M, STAGES>;
+  constexpr int TN = Cfg::kTN, TM = Cfg::kTM;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[Cfg::kLds];
+
+  const int total = tiles_m * tiles_n;
+  int id = blockIdx.x;
+  {
+    const int per = (total + 7) / 8;
+    const int xcd = id & 7, local = id >> 3;
+    const int full = total - (per - 1) * 8;
+    id = xcd < full ? xcd * per + local : full * per + (xcd - full) * (per - 1) + local;
+  }
+  const int width = group_m * tiles_n;
+  const int group = id / width;
+  const int first_m = group * group_m;
+  const int gsize = min(tiles_m - first_m, group_m);
+  const int tile_m = first_m + (id % width) % gsize;
+  const int tile_n = (id % width) / gsize;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wn = wave % WAVES_N;
+  const int wm = wave / WAVES_N;
+  const int m0 = tile_m * BM;
+  const int n0 = tile_n * BN;
+  const int KT = K >> 7;
+  const int KS = K / kSlice;
+
+  v16f acc[TN][TM];
+#pragma unroll
+  for (int a = 0; a < TN; ++a)
+#pragma unroll
+    for (int b = 0; b < TM; ++b)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[a][b][e] = 0.0f;
+
+  const float* sw_row = sW + (int64_t)((n0 + wn * TN * 32) >> 7) * KT;
+  // the token whose scale this lane stages (tile rows wave*64 + lane)
+  int sa_tok = m0 + wave * 64 + lane;
+  sa_tok = min(sa_tok, min(m0 + BM, M) - 1);
+
+  auto issue = [&](int slice) {
+    uint8_t* buf = smem + (slice % STAGES) * Cfg::kStage;
+    const int64_t k_off = (int64_t)slice * kSlice;
+    const float* src = sA + (int64_t)(slice >> 1) * sa_ld + sa_tok;
+    __builtin_amdgcn_global_load_lds((const void*)src,
+                                     (lds_void*)(buf + Cfg::kABytes + Cfg::kWBytes + wave * 256),
+                                     4, 0, 0);
+    load_slabs<Cfg::kASlabs>(A, lda, m0, M - 1, k_off, buf, wave * Cfg::kASlabs, lane);
+    load_slabs<Cfg::kWSlabs>(W, K, n0, N - 1, k_off, buf + Cfg::kABytes, wave * Cfg::kWSlabs,
+                             lane);
+  };
+  auto read_frags = [&](int slice, v8i (&wf)[TN], v8i (&af)[TM]) {
+    const uint8_t* a_lds = smem + (slice % STAGES) * Cfg::kStage;
+    const uint8_t* w_lds = a_lds + Cfg::kABytes;
+#pragma unroll
+    for (int a = 0; a < TN; ++a) wf[a] = read_frag(w_lds, wn * TN * 32 + a * 32 + (lane & 31), lane);
+#pragma unroll
+    for (int b = 0; b < TM; ++b) af[b] = read_frag(a_lds, wm * TM * 32 + b * 32 + (lane & 31), lane);
+  };
+
+#pragma unroll
+  for (int s = 0; s < STAGES - 1; ++s)
+    if (s < KS) issue(s);
+  __builtin_amdgcn_s_waitcnt(0);  // the prologue waits once for everything
+  lds_barrier();
+
+  float s_prev[TM];
+#pragma unroll
+  for (int b = 0; b < TM; ++b) s_prev[b] = 0.0f;
+  bool skip = false;
+
+  v8i wf0[TN], af0[TM], wf1[TN], af1[TM];
+  read_frags(0, wf0, af0);
+
+  // one slice: wait for and read slice ks+1 while slice ks's MFMAs run
+  auto step = [&](int ks, v8i (&wf)[TN], v8i (&af)[TM], v8i (&wfn)[TN], v8i (&afn)[TM]) {
+    const bool next = ks + 1 < KS;
+    if (next) {
+      // slice ks+1 landed; slices ks+2 .. ks+STAGES-2 may stay in flight
+      if (ks + STAGES - 2 < KS) {
+        wait_vmcnt<(STAGES - 3) * Cfg::kOpsPerStage>();
+      } else {
+        wait_vmcnt<0>();
+      }
+      lds_barrier();
+      if (ks + STAGES - 1 < KS) issue(ks + STAGES - 1);
+      read_frags(ks + 1, wfn, afn);
+    }
+    if ((ks & 1) == 0) {
+      const float sw = sw_row[ks >> 1];
+      skip = sw == 0.0f;  // wave-uniform
+      if (!skip) {
+        const float* sa_lds = reinterpret_cast<const float*>(
+            smem + (ks % STAGES) * Cfg::kStage + Cfg::kABytes + Cfg::kWBytes);
+#pragma unroll
+        for (int b = 0; b < TM; ++b) {
+          const float s_cur = sa_lds[wm * TM * 32 + b * 32 + (lane & 31)] * sw;
+          const float r = s_prev[b] / s_cur;  // 0 until the first block
+#pragma unroll
+          for (int a = 0; a < TN; ++a)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[a][b][e] *= r;
+          s_prev[b] = s_cur;
+        }
+      }
+    }
+    if (!skip) {
+#pragma unroll
+      for (int a = 0; a < TN; ++a)
+#pragma unroll
+        for (int b = 0; b < TM; ++b)
+          acc[a][b] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(wf[a], af[b], acc[a][b], 0,
+                                                                      0, 0, 0, 0, 0);
+    }
+  };
+  for (int ks = 0; ks < KS; ks += 2) {
+    step(ks, wf0, af0, wf1, af1);
+    if (ks + 1 < KS) step(ks + 1, wf1, af1, wf0, af0);
+  }
+
+#pragma unroll
+  for (int b = 0; b < TM; ++b) {
+    const int m = m0 + wm * TM * 32 + b * 32 + (lane & 31);
+    if (m >= M) continue;
+    const float s = s_prev[b];
+    uint16_t* crow = C + (int64_t)m * ldc;
+#pragma unroll
+    for (int a = 0; a < TN; ++a) {
+      const int nbase = n0 + wn * TN * 32 + a * 32 + (lane >> 5) * 4;
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        uint2 v;
+        v.x = pack2_bf16(acc[a][b][g * 4 + 0] * s, acc[a][b][g * 4 + 1] * s);
+        v.y = pack2_bf16(acc[a][b][g * 4 + 2] * s, acc[a][b][g * 4 + 3] * s);
+        *reinterpret_cast<uint2*>(crow + nbase + g * 8) = v;
+      }
+    }
+  }
+}
+
+template <int BM, int BN, int WN, int WM, int ST>
+int launch_plr(const void* A, const float* sA, const void* W, const float* sW, void* C, int M,
+               int N, int K, int64_t lda, int64_t ldc, int64_t sa_ld, int group_m,
+               hipStream_t stream) {
+  using Cfg = PlrCfg<BM, BN, WN, WM, ST>;
+  const int tiles_m = (M + BM - 1) / BM;
+  const int tiles_n = N / BN;
+  const int total = tiles_m * tiles_n;
+  hipLaunchKernelGGL((gemm_fp8_plr_kernel<BM, BN, WN, WM, ST>), dim3(total), dim3(Cfg::kThreads),
+                     0, stream, (const uint8_t*)A, sA, (const uint8_t*)W, sW, (uint16_t*)C, M, N,
+                     K, lda, ldc, sa_ld, tiles_m, tiles_n, group_m < 1 ? 1 : group_m);
+  QX_LAUNCH_STATUS();
+}
+
+
+// ---- 128-byte slices: one 128-K scale block per pipeline stage ------------
+// Rows of 128 B (8 chunks of 16 B), chunk-swizzled by ((row >> 1) & 7); a
+// 1 KiB direct-load slab is 8 rows; a lane's MFMA fragment for K-half h is
+// bytes [h*64 + (lane/32)*32, +32).
+__device__ __forceinline__ int swz128(int row) { return (row >> 1) & 7; }
+
+template <int SLABS>
+__device__ __forceinline__ void load_slabs128(const uint8_t* __restrict__ g, int64_t ld, int row0,
+                                              int row_max, int64_t k_off, uint8_t* lds,
+                                              int first, int lane) {
+  const int r_in = lane >> 3;
+  const int p = lane & 7;
+#pragma unroll
+  for (int j = 0; j < SLABS; ++j) {
+    const int slab = first + j;
+    const int row = slab * 8 + r_in;
+    const int c = p ^ swz128(row);
+    int grow = row0 + row;
+    grow = grow < row_max ? grow : row_max;
+    const uint8_t* src = g + (int64_t)grow * ld + k_off + c * 16;
+    __builtin_amdgcn_global_load_lds((const void*)src, (lds_void*)(lds + slab * 1024), 16, 0, 0);
+  }
+}
+
+__device__ __forceinline__ v8i read_frag128(const uint8_t* lds, int row, int h, int lane) {
+  const int c0 = h * 4 + (lane >> 5) * 2;
+  const int sw = swz128(row);
+  const v4i* base = reinterpret_cast<const v4i*>(lds + row * 128);
+  const v4i lo = base[c0 ^ sw];
+  const v4i hi = base[(c0 + 1) ^ sw];
+  v8i r;
+  r[0] = lo[0]; r[1] = lo[1]; r[2] = lo[2]; r[3] = lo[3];
+  r[4] = hi[0]; r[5] = hi[1]; r[6] = hi[2]; r[7] = hi[3];
+  return r;
+}
+
+template <int BM, int BN, int WAVES_N, int WAVES_M, int STAGES>
+struct Cfg128 {
+  static constexpr int kWaves = WAVES_N * WAVES_M;
+  static constexpr int kThreads = 64 * kWaves;
+  static constexpr int kTN = BN / WAVES_N / 32;
+  static constexpr int kTM = BM / WAVES_M / 32;
+  static constexpr int kABytes = BM * 128;
+  static constexpr int kWBytes = BN * 128;
+  static constexpr int kStage = kABytes + kWBytes;
+  static constexpr int kLds = STAGES * kStage;
+  static constexpr int kASlabs = BM / 8 / kWaves;
+  static constexpr int kWSlabs = BN / 8 / kWaves;
+  static constexpr int kOpsPerStage = kASlabs + kWSlabs + kTM;
+  static_assert(kTN >= 1 && kTM >= 1, "wave tile");
+  static_assert(BM % (8 * kWaves) == 0 && BN % (8 * kWaves) == 0, "slabs");
+  static_assert(128 % (BN / WAVES_N) == 0 || (BN / WAVES_N) == 128, "weight scale block");
+  static_assert(kLds <= 160 * 1024, "LDS");
+  static_assert(STAGES >= 2 && (STAGES - 2) * kOpsPerStage < 64, "stages");
+};
+
+template <int BM, int BN, int WAVES_N, int WAVES_M, int STAGES>
+__global__ __launch_bounds__(64 * WAVES_N * WAVES_M) void gemm_fp8_k128_kernel(
+    const uint8_t* __restrict__ A, const float* __restrict__ sA, const uint8_t* __restrict__ W,
+    const float* __restrict__ sW, uint16_t* __restrict__ C, int M, int N, int K, int64_t lda,
+    int64_t ldc, int64_t sa_ld, int tiles_m, int tiles_n, int group_m) {
+  using Cfg = Cfg128<BM, BN, WAVES_N, WAVES_M, STAGES>;
+  constexpr int TN = Cfg::kTN, TM = Cfg::kTM;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[Cfg::kLds];
+
+  const int total = tiles_m * tiles_n;
+  int id = blockIdx.x;
+  {
+    const int per = (total + 7) / 8;
+    const int xcd = id & 7, local = id >> 3;
+    const int full = total - (per - 1) * 8;
+    id = xcd < full ? xcd * per + local : full * per + (xcd - full) * (per - 1) + local;
+  }
+  const int width = group_m * tiles_n;
+  const int group = id / width;
+  const int first_m = group * group_m;
+  const int gsize = min(tiles_m - first_m, group_m);
+  const int tile_m = first_m + (id % width) % gsize;
+  const int tile_n = (id % width) / gsize;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wn = wave % WAVES_N;
+  const int wm = wave / WAVES_N;
+  const int m0 = tile_m * BM;
+  const int n0 = tile_n * BN;
+  const int KT = K >> 7;
+
+  v16f acc[TN][TM];
+#pragma unroll
+  for (int a = 0; a < TN; ++a)
+#pragma unroll
+    for (int b = 0; b < TM; ++b)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[a][b][e] = 0.0f;
+  int tok[TM];
+#pragma unroll
+  for (int b = 0; b < TM; ++b) tok[b] = min(m0 + wm * TM * 32 + b * 32 + (lane & 31), M - 1);
+  const float* sw_row = sW + (int64_t)((n0 + wn * TN * 32) >> 7) * KT;
+
+  float sa_ring[STAGES][TM];
+  auto issue = [&](int kb, int stage) {
+    uint8_t* buf = smem + stage * Cfg::kStage;
+    const int64_t k_off = (int64_t)kb * 128;
+    load_slabs128<Cfg::kASlabs>(A, lda, m0, M - 1, k_off, buf, wave * Cfg::kASlabs, lane);
+    load_slabs128<Cfg::kWSlabs>(W, K, n0, N - 1, k_off, buf + Cfg::kABytes, wave * Cfg::kWSlabs,
+                                lane);
+#pragma unroll
+    for (int b = 0; b < TM; ++b) sa_ring[stage][b] = sA[(int64_t)kb * sa_ld + tok[b]];
+  };
+#pragma unroll
+  for (int st = 0; st < STAGES - 1; ++st)
+    if (st < KT) issue(st, st);
+
+  float s_prev[TM];
+#pragma unroll
+  for (int b = 0; b < TM; ++b) s_prev[b] = 0.0f;
+
+  for (int base = 0; base < KT; base += STAGES) {
+#pragma unroll
+    for (int stage = 0; stage < STAGES; ++stage) {
+      const int kb = base + stage;
+      if (kb < KT) {
+        if (kb + STAGES - 2 < KT) {
+          wait_vmcnt<(STAGES - 2) * Cfg::kOpsPerStage>();
+        } else {
+          wait_vmcnt<0>();
+        }
+        lds_barrier();
+        if (kb + STAGES - 1 < KT) issue(kb + STAGES - 1, (stage + STAGES - 1) % STAGES);
+        const float sw = sw_row[kb];
+        if (sw != 0.0f) {  // wave-uniform; a zero weight-scale block adds nothing
+#pragma unroll
+          for (int b = 0; b < TM; ++b) {
+            const float s_cur = sa_ring[stage][b] * sw;
+            const float r = s_prev[b] / s_cur;
+#pragma unroll
+            for (int a = 0; a < TN; ++a)
+#pragma unroll
+              for (int e = 0; e < 16; ++e) acc[a][b][e] *= r;
+            s_prev[b] = s_cur;
+          }
+          const uint8_t* a_lds = smem + stage * Cfg::kStage;
+          const uint8_t* w_lds = a_lds + Cfg::kABytes;
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            v8i wf[TN], af[TM];
+#pragma unroll
+            for (int a = 0; a < TN; ++a)
+              wf[a] = read_frag128(w_lds, wn * TN * 32 + a * 32 + (lane & 31), h, lane);
+#pragma unroll
+            for (int b = 0; b < TM; ++b)
+              af[b] = read_frag128(a_lds, wm * TM * 32 + b * 32 + (lane & 31), h, lane);
+#pragma unroll
+            for (int a = 0; a < TN; ++a)
+#pragma unroll
+              for (int b = 0; b < TM; ++b)
+                acc[a][b] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+                    wf[a], af[b], acc[a][b], 0, 0, 0, 0, 0, 0);
+          }
+        }
+      }
+    }
+  }
+
+#pragma unroll
+  for (int b = 0; b < TM; ++b) {
+    const int m = m0 + wm * TM * 32 + b * 32 + (lane & 31);
+    if (m >= M) continue;
+    const float s = s_prev[b];
+    uint16_t* crow = C + (int64_t)m * ldc;
+#pragma unroll
+    for (int a = 0; a < TN; ++a) {
+      const int nbase = n0 + wn * TN * 32 + a * 32 + (lane >> 5) * 4;
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        uint2 v;
+        v.x = pack2_bf16(acc[a][b][g * 4 + 0] * s, acc[a][b][g * 4 + 1] * s);
+        v.y = pack2_bf16(acc[a][b][g * 4 + 2] * s, acc[a][b][g * 4 + 3] * s);
+        *reinterpret_cast<uint2*>(crow + nbase + g * 8) = v;
+      }
+    }
+  }
+}
+
+template <int BM, int BN, int WN, int WM, int ST>
+int launch128(const void* A, const float* sA, const void* W, const float* sW, void* C, int M,
+              int N, int K, int64_t lda, int64_t ldc, int64_t sa_ld, int group_m,
+              hipStream_t stream) {
+  using Cfg = Cfg128<BM, BN, WN, WM, ST>;
+  const int tiles_m = (M + BM - 1) / BM;
+  const int tiles_n = N / BN;
+  const int total = tiles_m * tiles_n;
+  hipLaunchKernelGGL((gemm_fp8_k128_kernel<BM, BN, WN, WM, ST>), dim3(total),
+                     dim3(Cfg::kThreads), 0, stream, (const uint8_t*)A, sA, (const uint8_t*)W, sW,
+                     (uint16_t*)C, M, N, K, lda, ldc, sa_ld, tiles_m, tiles_n,
+                     group_m < 1 ? 1 : group_m);
+  QX_LAUNCH_STATUS();
+}
+
 template <int BM, int BN, int WN, int WM, int ST>
 int launch(const void* A, const float* sA, const void* W, const float* sW, void* C, int M, int N,
            int K, int64_t lda, int64_t ldc, int64_t sa_ld, int group_m, hipStream_t stream) {
@@ -314,6 +707,26 @@ int qx_gemm_fp8_blockscaled(const void* A, const float* sA, const void* W, const
       return qx::launch<256, 128, 1, 4, 2>(A, sA, W, sW, C, m, n, k, lda, ldc, sa_ld, 8, stream);
     case 6:
       return qx::launch<256, 128, 1, 4, 4>(A, sA, W, sW, C, m, n, k, lda, ldc, sa_ld, 8, stream);
+    case 7:
+      QX_CHECK(n % 256 == 0, "gemm config 7 needs N %% 256 == 0 (N=%d)", n);
+      return qx::launch_plr<256, 256, 2, 4, 4>(A, sA, W, sW, C, m, n, k, lda, ldc, sa_ld, 4,
+                                               stream);
+    case 8:
+      return qx::launch_plr<256, 128, 1, 4, 3>(A, sA, W, sW, C, m, n, k, lda, ldc, sa_ld, 8,
+                                               stream);
+    case 9:
+      return qx::launch_plr<128, 128, 2, 2, 4>(A, sA, W, sW, C, m, n, k, lda, ldc, sa_ld, 8,
+                                               stream);
+    case 10:
+      QX_CHECK(n % 256 == 0, "gemm config 10 needs N %% 256 == 0 (N=%d)", n);
+      return qx::launch128<256, 256, 2, 4, 2>(A, sA, W, sW, C, m, n, k, lda, ldc, sa_ld, 4,
+                                              stream);
+    case 11:
+      return qx::launch128<256, 128, 1, 4, 2>(A, sA, W, sW, C, m, n, k, lda, ldc, sa_ld, 8,
+                                              stream);
+    case 12:
+      return qx::launch128<128, 128, 2, 2, 2>(A, sA, W, sW, C, m, n, k, lda, ldc, sa_ld, 8,
+                                              stream);
     default:
       QX_CHECK(false, "gemm: unknown config %d", config);
   }

@@ -24,11 +24,14 @@ from quail_amd import _lib
 
 GROUP = 128
 
-# GEMM tile configuration (see csrc/gemm_fp8.hip): 5 = 256 tokens x 128
-# weights, 4 waves, two 64-byte K stages (48 KiB LDS, two workgroups per CU)
-# measured fastest on the Qwen3 shapes; QUAIL_GEMM_CONFIG overrides it.
+# GEMM tile configurations (see csrc/gemm_fp8.hip), measured on the Qwen3-4B
+# projection shapes at 8k-16k tokens: 10 = 256 tokens x 256 weights, 8 waves,
+# two 128-byte K stages (128 KiB LDS) is fastest where N >= 4096 or K >= 8192
+# (qkv, gate_up, down); 5 = 256 x 128, 4 waves, two 64-byte K stages (48 KiB,
+# two workgroups per CU) wins on the narrow o_proj. QUAIL_GEMM_CONFIG forces one.
 GEMM_CONFIG_ENV = "QUAIL_GEMM_CONFIG"
 GEMM_DEFAULT_CONFIG = 5
+GEMM_WIDE_CONFIG = 10
 
 
 def _ptr(t):
@@ -43,6 +46,8 @@ def gemm_config(n: int, k: int, m: int) -> int:
     forced = os.environ.get(GEMM_CONFIG_ENV)
     if forced is not None:
         return int(forced)
+    if n % 256 == 0 and (n >= 4096 or k >= 8192):
+        return GEMM_WIDE_CONFIG
     return GEMM_DEFAULT_CONFIG
 
 
