@@ -14,6 +14,13 @@ GEMM launch of the timed region), and the CPU baseline: the oracle's torch
 restatement of the reference path timed on this host on a bounded sample.
 
   python bench.py [--steps K] [--warmup W] [--gpus 1] [--cpu-seconds S]
+  python bench.py --copy-mib 1024 ...     also run one plain copy of that size
+                                          (qx_embed over identity ids) before
+                                          the warmup, to calibrate HBM counters
+  python bench.py --summarize DIR [--copy-mib 1024]
+                                          print the summary of a rocprofv3 CSV
+                                          output directory (kernel stats or
+                                          FETCH_SIZE / WRITE_SIZE counters)
 """
 
 import argparse
@@ -32,6 +39,10 @@ PEAK_FP8 = 5.0e15        # MI355X dense FP8 MFMA, FLOP/s
 PEAK_BF16 = 2.5e15       # dense bf16 MFMA
 PEAK_HBM = 8.0e12        # HBM3E bytes/s
 WORKLOAD = "qwen3-4b"
+# HBM bytes per GEMM launch of this workload, from the FETCH_SIZE and
+# WRITE_SIZE counter runs summarized in this file (copy-calibrated)
+TRAFFIC_FILE = ROOT / "profiles" / "gemm_fp8_qwen3_4b_ai_if_traffic.txt"
+COPY_ROW_ELEMS = 2048    # bf16 elements per row of the calibration copy
 
 
 def parse():
@@ -43,6 +54,10 @@ def parse():
     p.add_argument("--seed", type=int, default=0)
     p.add_argument("--cpu-seconds", type=float, default=15.0,
                    help="target wall time of the CPU baseline sample (0 skips it)")
+    p.add_argument("--copy-mib", type=int, default=0,
+                   help="size of the counter-calibration copy (0: none)")
+    p.add_argument("--summarize", default=None,
+                   help="summarize a rocprofv3 CSV directory and exit")
     return p.parse_args()
 
 
@@ -70,9 +85,10 @@ def attention_pairs(run_packs):
 
 def cpu_baseline(model, workload, target_s):
     """The oracle (the torch restatement of the reference path, fp32
-    contractions, the reference's own CPU arithmetic) on this host: whole
-    documents of the corpus through the first layers, scaled to all layers
-    and reported per fresh token and per document."""
+    contractions, the reference's own CPU arithmetic) on this host: one pack's
+    worth of whole documents (up to the pack budget of rows) through the first
+    layer, after one warm-up pass, repeated to about target_s, scaled to all
+    layers and reported per fresh token and per document."""
     import torch
 
     from oracle import qwen3_ref as ref
@@ -82,7 +98,6 @@ def cpu_baseline(model, workload, target_s):
     torch.set_num_threads(threads)
     ref.set_precision(torch.float32)
     cfg = model.config
-    # the first layers' weights and the embedding on the host
     sample_layers = 1
     sub = type(model)(**vars(model))
     inner = type(model.model)(**vars(model.model))
@@ -92,33 +107,136 @@ def cpu_baseline(model, workload, target_s):
     docs = []
     tokens = 0
     for prompt in workload.prompts:
+        if tokens + len(prompt) > workload.chunk_budget:
+            break
         docs.append(list(prompt))
         tokens += len(prompt)
-        if tokens >= 1024:
-            break
+    ref.forward_documents(m, docs[:2], layers=sample_layers)   # warm-up
+    reps = 0
     t0 = time.perf_counter()
-    ref.forward_documents(m, docs, layers=sample_layers)
-    one = time.perf_counter() - t0
-    # grow the sample to about target_s of CPU work
-    reps = max(1, int(target_s / max(one, 1e-3)))
-    reps = min(reps, 20)
-    t0 = time.perf_counter()
-    for _ in range(reps):
+    while True:
         ref.forward_documents(m, docs, layers=sample_layers)
-    elapsed = time.perf_counter() - t0
+        reps += 1
+        elapsed = time.perf_counter() - t0
+        if elapsed >= target_s or elapsed * (reps + 1) / reps > 2 * target_s:
+            break
     ref.set_precision(torch.float64)
     per_token_layer = elapsed / (reps * tokens * sample_layers)
     tok_s = 1.0 / (per_token_layer * cfg.layers)
     docs_per_token = workload.documents / sum(len(p) for p in workload.prompts)
     return dict(value=round(tok_s * docs_per_token, 3), unit="rows/s", cores=threads,
                 kind="port", tok_s=round(tok_s, 1),
-                sample=(f"{len(docs)} whole documents ({tokens} tokens) x {sample_layers} of "
-                        f"{cfg.layers} layers x {reps} reps, {elapsed:.1f} s, scaled to all "
-                        f"layers; rows/s = tok/s x documents per token of the corpus"))
+                sample=(f"one-pack subset: {len(docs)} whole documents ({tokens} tokens, "
+                        f"shared prefix included) x {sample_layers} of {cfg.layers} layers x "
+                        f"{reps} reps, {elapsed:.1f} s, scaled to all layers; rows/s = tok/s x "
+                        f"documents per prompt token of the corpus"))
+
+
+def _short(name: str) -> str:
+    """A kernel name without its parameter list, at most 110 characters."""
+    name = name.strip('"').replace("(anonymous namespace)::", "")
+    if name.startswith("void "):
+        name = name[5:]
+    depth = 0
+    for i, ch in enumerate(name):
+        if ch == "<":
+            depth += 1
+        elif ch == ">":
+            depth -= 1
+        elif ch == "(" and depth == 0:
+            name = name[:i]
+            break
+    return name if len(name) <= 110 else name[:107] + "..."
+
+
+def summarize(directory: str, copy_mib: int) -> None:
+    """Print a rocprofv3 CSV directory as text: kernel statistics, and for
+    counter runs the mean FETCH_SIZE / WRITE_SIZE per dispatch of each kernel,
+    the calibration factor of the plain copy (qx_embed over identity ids,
+    copy_mib MiB read and written) and the copy-calibrated HBM bytes per FP8
+    GEMM launch."""
+    import csv
+    from collections import defaultdict
+
+    root = Path(directory)
+    stats = sorted(root.rglob("*kernel_stats.csv"))
+    counters = sorted(root.rglob("*counter_collection.csv"))
+    if stats:
+        rows = list(csv.DictReader(open(stats[0])))
+        total = sum(float(r["TotalDurationNs"]) for r in rows)
+        print(f"{'calls':>7} {'total ms':>10} {'avg us':>10} {'share':>6}  kernel")
+        gemm_ns, gemm_calls = 0.0, 0
+        for r in rows:
+            ns, calls = float(r["TotalDurationNs"]), int(r["Calls"])
+            print(f"{calls:7d} {ns / 1e6:10.2f} {ns / calls / 1e3:10.2f} "
+                  f"{ns / total:6.1%}  {_short(r['Name'])}")
+            if "gemm_fp8" in r["Name"]:
+                gemm_ns += ns
+                gemm_calls += calls
+        if gemm_calls:
+            print(f"fp8 gemm, all tile variants: {gemm_calls} launches, "
+                  f"avg {gemm_ns / gemm_calls / 1e3:.2f} us")
+    for path in counters:
+        per = defaultdict(lambda: defaultdict(list))
+        for r in csv.DictReader(open(path)):
+            per[r["Counter_Name"]][_short(r["Kernel_Name"])].append(float(r["Counter_Value"]))
+        for counter, kernels in per.items():
+            print(f"\n{counter} (KiB per dispatch)")
+            print(f"{'calls':>7} {'mean KiB':>14}  kernel")
+            for k, v in sorted(kernels.items(), key=lambda kv: -sum(kv[1])):
+                print(f"{len(v):7d} {sum(v) / len(v):14.1f}  {k}")
+            copy = [v for k, v in kernels.items() if "embed_kernel" in k]
+            gemm = [x for k, v in kernels.items() if "gemm_fp8" in k for x in v]
+            if copy and copy_mib and gemm:
+                known = copy_mib * 2**20
+                factor = known / (copy[0][-1] * 1024)
+                mean = sum(gemm) / len(gemm) * 1024 * factor
+                print(f"copy calibration: {copy_mib} MiB moved, counter reads "
+                      f"{copy[0][-1] * 1024 / 2**20:.1f} MiB, factor {factor:.4f}")
+                print(f"{counter}_bytes_per_gemm_launch = {mean:.0f}")
+
+
+def load_traffic():
+    """HBM bytes per FP8 GEMM launch (FETCH + WRITE, copy-calibrated) from the
+    committed counter summary, or None when it is absent."""
+    if not TRAFFIC_FILE.exists():
+        return None
+    vals = {}
+    for line in TRAFFIC_FILE.read_text().splitlines():
+        if "_bytes_per_gemm_launch =" in line:
+            key, val = line.split("=")
+            vals[key.strip()] = float(val)
+    fetch = vals.get("FETCH_SIZE_bytes_per_gemm_launch")
+    write = vals.get("WRITE_SIZE_bytes_per_gemm_launch")
+    if fetch is None or write is None:
+        return None
+    return dict(fetch=fetch, write=write, total=fetch + write)
+
+
+def copy_calibration(mib: int) -> None:
+    """One plain copy of mib MiB (qx_embed over identity ids: every row read
+    once, written once), for counter calibration."""
+    import torch
+
+    from quail_amd import _lib
+    rows = mib * 2**20 // (2 * COPY_ROW_ELEMS)
+    src = torch.empty((rows, COPY_ROW_ELEMS), dtype=torch.bfloat16, device="cuda")
+    src.fill_(1.0)
+    dst = torch.empty_like(src)
+    ids = torch.arange(rows, dtype=torch.int64, device="cuda")
+    torch.cuda.synchronize()
+    _lib.call("qx_embed", src.data_ptr(), COPY_ROW_ELEMS, ids.data_ptr(), dst.data_ptr(),
+              COPY_ROW_ELEMS, rows, COPY_ROW_ELEMS, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    log(f"calibration copy: {rows} rows x {2 * COPY_ROW_ELEMS} B = {mib} MiB")
+    del src, dst, ids
 
 
 def main():
     args = parse()
+    if args.summarize:
+        summarize(args.summarize, args.copy_mib)
+        return
     if args.gpus != 1:
         print(json.dumps({"error": f"--gpus {args.gpus}: this benchmark runs on one GPU; "
                                    "the path shards by documents with no exchange, so N GPUs "
@@ -166,6 +284,8 @@ def main():
 
     log(f"setup {t_build:.1f} s: {wl.documents} documents, {cfg.layers} layers, "
         f"{num_pages} KV pages")
+    if args.copy_mib:
+        copy_calibration(args.copy_mib)
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -197,6 +317,11 @@ def main():
         s[2] += 1
     gemm_tflops = gemm_flops / (gemm_ms * 1e-3) / 1e12
     launches = len(timer)
+    # operands read once and the bf16 result written once: A (M x K e4m3),
+    # W (N x K e4m3), C (M x N bf16) and both scale arrays
+    gemm_bytes = sum(m * k + n * k + 2 * m * n + 4 * (m * k // 128 + n * k // 16384)
+                     for m, n, k, _, _ in timer)
+    traffic = load_traffic()
 
     fresh = stats[0]["fresh_tokens"]
     docs = wl.documents
@@ -253,7 +378,9 @@ def main():
             "peak": PEAK_FP8 / 1e12,
             "unit": "TFLOP/s",
             "frac": round(gemm_tflops * 1e12 / PEAK_FP8, 4),
-            "traffic": None,
+            "traffic": traffic and round(traffic["total"]),
+            "traffic_source": traffic and str(TRAFFIC_FILE.relative_to(ROOT)),
+            "algorithmic_bytes_per_launch": round(gemm_bytes / max(launches, 1)),
             "launches": launches,
             "avg_launch_us": round(gemm_ms * 1e3 / max(launches, 1), 2),
             "gemm_time_share": round(gemm_ms * 1e-3 / elapsed, 4),
