@@ -274,6 +274,9 @@ class Engine:
         hq, hk, d = self.num_q_heads, self.num_kv_heads, self.head_dim
         if chunk.attention_mode != "unified":
             raise ValueError("this engine runs the unified attention path")
+        for key in ("shared", "canvas"):
+            if chunk.meta.get(key) is not None:
+                raise ValueError(f"this engine has no {key}-row attention path")
         q3 = q.view(n, hq, d)
         k3 = k.view(n, hk, d)
         v3 = v.view(n, hk, d) if v.is_contiguous() else v
