@@ -121,21 +121,25 @@ int qx_group_quant(const void* x, int64_t x_ld, void* q, int64_t q_ld, float* sc
 
 /*
  * k_pool[dst[i]] = k[src[i]], v_pool[dst[i]] = v[src[i]] for rows of
- * row_elems bf16; dst[i] < 0 writes nothing. Source rows have strides k_ld
- * and v_ld (v may be the strided v slice of qkv). Replaces the Triton
- * kv_row_scatter (attention.py:885-897) of Engine.kv_row_scatter /
- * write_kv (attention.py:1165-1195), including its pool-to-pool tail copy.
+ * row_elems 16-bit values; dst[i] < 0 writes nothing. Source rows have
+ * strides k_ld and v_ld (v may be the strided v slice of qkv). The V pool
+ * holds fp16: with v_to_f16 the bf16 V rows are converted (round to nearest
+ * even) as they are written; without it (the pool-to-pool tail copy) rows
+ * are copied unchanged. Replaces the Triton kv_row_scatter
+ * (attention.py:885-897) of Engine.kv_row_scatter / write_kv
+ * (attention.py:1165-1195), including its pool-to-pool tail copy.
  */
 int qx_kv_scatter(const void* k, int64_t k_ld, const void* v, int64_t v_ld, void* k_pool,
                   void* v_pool, const int64_t* src, const int64_t* dst, int64_t count,
-                  int64_t row_elems, hipStream_t stream);
+                  int64_t row_elems, int v_to_f16, hipStream_t stream);
 
 /* out[i] = table[ids[i]] (bf16 rows). Replaces vLLM embed_tokens (qwen3.py:123). */
 int qx_embed(const void* table, int64_t t_ld, const int64_t* ids, void* out, int64_t o_ld,
              int64_t n, int64_t H, hipStream_t stream);
 
 /*
- * Varlen GQA attention reading K/V through a block table: sequence s has
+ * Varlen GQA attention reading K (bf16) and V (fp16, as qx_kv_scatter
+ * writes it) through a block table: sequence s has
  * query rows [cu_q[s], cu_q[s+1]) and keys [0, used[s]) at pool rows
  * table[s*table_ld + j/page]*page + j%page; causal masking aligned
  * bottom-right. Replaces Engine.attention_unified -> _paged ->

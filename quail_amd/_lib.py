@@ -35,7 +35,7 @@ SIGNATURES = {
                         _i64, _f32, _p],
     "qx_silu_mul_quant": [_p, _i64, _p, _i64, _p, _i64, _i64, _i64, _p],
     "qx_group_quant": [_p, _i64, _p, _i64, _p, _i64, _i64, _i64, _p],
-    "qx_kv_scatter": [_p, _i64, _p, _i64, _p, _p, _p, _p, _i64, _i64, _p],
+    "qx_kv_scatter": [_p, _i64, _p, _i64, _p, _p, _p, _p, _i64, _i64, _i32, _p],
     "qx_embed": [_p, _i64, _p, _p, _i64, _i64, _i64, _p],
     "qx_paged_attention": [_p, _i64, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64,
                            _i64, _i64, _f32, _i32, _p, _p, _i64, _p, _i64, _p],

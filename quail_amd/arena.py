@@ -43,7 +43,9 @@ class KVArena:
         storage = torch.empty(2 * self.num_layers * size, dtype=self.dtype, device=self.device)
         parts = storage.split([size] * (2 * self.num_layers))
         self.k = [p.view(rows, heads, dim) for p in parts[0::2]]
-        self.v = [p.view(rows, heads, dim) for p in parts[1::2]]
+        # V pages hold fp16 (same 16-bit slots): the attention's PV product
+        # runs in fp16, so V is converted once, when it is written
+        self.v = [p.view(torch.float16).view(rows, heads, dim) for p in parts[1::2]]
         self._capacity_rows = {}
         self._holds = {}
         self._deferred = set()

@@ -21,17 +21,18 @@
 // sequence x HPB query heads sharing one KV head: one wave per (tile, head),
 // so every K/V tile staged in LDS serves HPB * QSUB * 32 query rows. KV is
 // consumed in 64-key tiles, double buffered: while a tile is computed, the
-// next tile's K rows travel HBM -> LDS directly (global_load_lds) and its V
-// rows are fetched into registers, to be written transposed into the other
-// LDS buffer once the compute is done; one barrier per tile. The sequence's
-// page-table row is staged in LDS once.
+// next tile's K and V rows travel HBM -> LDS directly (global_load_lds),
+// one barrier per tile. The sequence's page-table row is staged in LDS once.
 //
 // Each wave forms S^T = K Q^T with v_mfma_f32_32x32x16_bf16 so that a lane
 // owns one query column; the online softmax is then lane-local (plus one
 // cross-half shuffle), P^T feeds the PV MFMA directly as its B operand, and
-// O^T keeps one query per lane, so rescaling needs no shuffles. The PV product
-// runs in fp16: P in (0, 1] keeps 11 significant bits (bf16 would keep 8),
-// and bf16 V converts to fp16 exactly for |v| in [2^-14, 65504].
+// O^T keeps one query per lane, so rescaling needs no shuffles. The V^T
+// operand of the PV MFMA comes straight from the row-major V tile through
+// gfx950's transposing LDS read (ds_read_b64_tr_b16). The PV product runs in
+// fp16: P in (0, 1] keeps 11 significant bits (bf16 would keep 8), and the V
+// pool holds fp16 (qx_kv_scatter converts bf16 V rows once, exactly for |v|
+// in [2^-14, 65504]).
 #include "qx_common.h"
 #include "qx_status.h"
 
@@ -44,14 +45,18 @@ constexpr int kBK = 64;          // keys per KV tile
 constexpr int kPage = 16;        // tokens per arena page
 constexpr int kMaxPages = 2048;  // page-table entries staged in LDS per sequence
 
-// position of key k (0..15) inside its 16-key group of the transposed V tile:
-// the 8 keys one MFMA lane-half consumes become contiguous
-__device__ __forceinline__ int vt_pos(int k) { return ((k >> 2) & 1) * 8 + (k >> 3) * 4 + (k & 3); }
+typedef short v4s __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4s lds_v4s;
 
 // 16-B chunk swizzle of a K row (2*D bytes): the 16 rows of one ds_read_b128
 // phase map to 16 distinct 16-B bank groups of the 64-bank LDS
 template <int D>
 __device__ __forceinline__ int kswz(int key) { return D == 128 ? (key & 15) : ((key >> 1) & 7); }
+
+// 16-B chunk swizzle of a V row: one transposing read covers 4 consecutive
+// keys x 4 chunks per 32-lane phase, which land in 16 distinct bank groups
+template <int D>
+__device__ __forceinline__ int vswz(int key) { return D == 128 ? ((key & 3) << 2) : (((key >> 1) & 1) << 2); }
 
 template <int D, int HPB, int QSUB, bool QUANT>
 __global__ __launch_bounds__(HPB * QSUB * 64) void paged_attention_kernel(
@@ -65,17 +70,18 @@ __global__ __launch_bounds__(HPB * QSUB * 64) void paged_attention_kernel(
   constexpr int BQ = 32 * QSUB;  // query rows per workgroup
   constexpr int ND16 = D / 16;   // MFMA k-steps over the head dim
   constexpr int NDS = D / 32;    // 32-row d tiles of O^T
-  constexpr int KCH = D / 8;     // 16-byte chunks per K row
-  constexpr int KROW = D * 2;    // bytes per K row
-  constexpr int K_BYTES = kBK * KROW;
-  constexpr int VT_BYTES = D * kBK * 2;
-  constexpr int KEYS_PER_SLAB = 1024 / KROW;            // keys per direct-load instruction
-  constexpr int K_SLABS = kBK / KEYS_PER_SLAB / NW;     // per wave per tile
-  constexpr int V_TOTAL = (kBK / 2) * KCH;              // key pairs x 8-d chunks per tile
-  constexpr int V_UNITS = (V_TOTAL + NT - 1) / NT;      // per thread
-  static_assert(K_SLABS >= 1 && K_SLABS * KEYS_PER_SLAB * NW == kBK, "K slabs");
-  __shared__ __attribute__((aligned(1024))) uint8_t k_lds[2][K_BYTES];
-  __shared__ __attribute__((aligned(16))) uint8_t vt_lds[2][VT_BYTES];
+  constexpr int KCH = D / 8;     // 16-byte chunks per K or V row
+  constexpr int ROW = D * 2;     // bytes per K or V row
+  constexpr int T_BYTES = kBK * ROW;
+  constexpr int KEYS_PER_SLAB = 1024 / ROW;         // keys per direct-load instruction
+  constexpr int SLABS = kBK / KEYS_PER_SLAB / NW;   // per wave per tile, for K and for V
+  static_assert(SLABS >= 1 && SLABS * KEYS_PER_SLAB * NW == kBK, "slabs");
+  // separate objects per buffer, so the compiler can see that the direct
+  // loads into one buffer never alias the reads of the other
+  __shared__ __attribute__((aligned(1024))) uint8_t k_lds0[T_BYTES];
+  __shared__ __attribute__((aligned(1024))) uint8_t k_lds1[T_BYTES];
+  __shared__ __attribute__((aligned(1024))) uint8_t v_lds0[T_BYTES];
+  __shared__ __attribute__((aligned(1024))) uint8_t v_lds1[T_BYTES];
   __shared__ int pages_lds[kMaxPages];
 
   const int s = blockIdx.y;
@@ -124,64 +130,47 @@ __global__ __launch_bounds__(HPB * QSUB * 64) void paged_attention_kernel(
   __builtin_amdgcn_s_waitcnt(0);
   lds_barrier();  // pages_lds visible
 
-  auto pool_row = [&](int kidx) -> int64_t {
-    kidx = kidx < kv_end ? kidx : kv_end - 1;  // tail keys re-read the last key (masked)
-    return (int64_t)pages_lds[kidx / kPage] * kPage + (kidx % kPage);
-  };
-  // K rows of tile t straight into LDS: lane i of a slab writes bytes
-  // [16i, 16i+16): key i / KCH of the slab, physical chunk i % KCH
-  auto issue_k = [&](int t, int buf) {
+  // K and V rows of tile t straight into LDS: lane i of a slab writes bytes
+  // [16i, 16i+16): key i / KCH of the slab, physical chunk i % KCH, which
+  // holds logical chunk (i % KCH) ^ swizzle(key)
+  auto issue = [&](int t, int buf) {
 #pragma unroll
-    for (int j = 0; j < K_SLABS; ++j) {
-      const int slab = wave * K_SLABS + j;
+    for (int j = 0; j < SLABS; ++j) {
+      const int slab = wave * SLABS + j;
       const int key = slab * KEYS_PER_SLAB + lane / KCH;
       const int p = lane % KCH;
-      const int c = p ^ kswz<D>(key);
-      const uint16_t* src = kbase + pool_row(t * kBK + key) * kv_row + c * 8;
-      __builtin_amdgcn_global_load_lds((const void*)src,
-                                       (lds_void*)(&k_lds[buf][0] + slab * 1024), 16, 0, 0);
+      int kidx = t * kBK + key;
+      kidx = kidx < kv_end ? kidx : kv_end - 1;  // tail keys re-read the last key (masked)
+      const int64_t prow = (int64_t)pages_lds[kidx / kPage] * kPage + (kidx % kPage);
+      const uint16_t* ksrc = kbase + prow * kv_row + (p ^ kswz<D>(key)) * 8;
+      const uint16_t* vsrc = vbase + prow * kv_row + (p ^ vswz<D>(key)) * 8;
+      __builtin_amdgcn_global_load_lds((const void*)ksrc,
+                                       (lds_void*)((buf ? k_lds1 : k_lds0) + slab * 1024), 16, 0,
+                                       0);
+      __builtin_amdgcn_global_load_lds((const void*)vsrc,
+                                       (lds_void*)((buf ? v_lds1 : v_lds0) + slab * 1024), 16, 0,
+                                       0);
     }
   };
-  uint4 vreg[V_UNITS][2];
-  // V work unit: (key pair, 8-column chunk dc) with key pairs fastest, so one
-  // ds_write_b32 instruction of a wave fills whole transposed rows
-  auto fetch_v = [&](int t) {
+
+  // lane-constant parts of the LDS read addresses
+  // K fragment (A operand of S^T): key `col` (+32 for the second subtile),
+  // d chunk 2c + half
+  int k_off[ND16];
 #pragma unroll
-    for (int u = 0; u < V_UNITS; ++u) {
-      const int unit = tid + u * NT;
-      if (unit < V_TOTAL) {
-        const int key = (unit % (kBK / 2)) * 2, dc = unit / (kBK / 2);
-        vreg[u][0] =
-            *reinterpret_cast<const uint4*>(vbase + pool_row(t * kBK + key) * kv_row + dc * 8);
-        vreg[u][1] =
-            *reinterpret_cast<const uint4*>(vbase + pool_row(t * kBK + key + 1) * kv_row + dc * 8);
-      }
-    }
-  };
-  auto store_vt = [&](int buf) {
+  for (int c = 0; c < ND16; ++c) k_off[c] = col * ROW + (((2 * c + half) ^ kswz<D>(col)) * 16);
+  // V^T fragment (A operand of O^T) by transposing reads: lane 16g + x reads
+  // 4 halfwords of key 4*half + x/4 (+8 for the second read) at d offset
+  // 16*(g&1) + 4*(x&3) within each 32-d tile
+  int v_off[NDS];
+  {
+    const int x = lane & 15;
+    const int key_rel = 4 * half + (x >> 2);
+    const int chunk = 2 * ((lane >> 4) & 1) + ((x & 3) >> 1);
 #pragma unroll
-    for (int u = 0; u < V_UNITS; ++u) {
-      const int unit = tid + u * NT;
-      if (unit < V_TOTAL) {
-        const int key = (unit % (kBK / 2)) * 2, dc = unit / (kBK / 2);
-        const uint32_t aw[4] = {vreg[u][0].x, vreg[u][0].y, vreg[u][0].z, vreg[u][0].w};
-        const uint32_t bw[4] = {vreg[u][1].x, vreg[u][1].y, vreg[u][1].z, vreg[u][1].w};
-        const int pos = (key >> 4) * 16 + vt_pos(key & 15);  // even; pos+1 holds key+1
-        const int chunk = pos >> 3, within = (pos & 7) * 2;
-        // lanes of odd chunks write the rows in rotated order, so the two
-        // chunks of a wave land in opposite 32-bank halves
-#pragma unroll
-        for (int e0 = 0; e0 < 8; ++e0) {
-          const int e = (e0 + (dc & 1)) & 7;
-          const int d = dc * 8 + e;
-          const float lo = (e & 1) ? hi_bf16(aw[e >> 1]) : lo_bf16(aw[e >> 1]);
-          const float hi = (e & 1) ? hi_bf16(bw[e >> 1]) : lo_bf16(bw[e >> 1]);
-          *reinterpret_cast<uint32_t*>(&vt_lds[buf][0] + d * (kBK * 2) +
-                                       ((chunk ^ ((d >> 1) & 7)) * 16) + within) = pack2_f16(lo, hi);
-        }
-      }
-    }
-  };
+    for (int dt = 0; dt < NDS; ++dt)
+      v_off[dt] = key_rel * ROW + (((dt * 4 + chunk) ^ vswz<D>(key_rel)) * 16) + 8 * (x & 1);
+  }
 
   v16f o[NDS];
 #pragma unroll
@@ -197,10 +186,7 @@ __global__ __launch_bounds__(HPB * QSUB * 64) void paged_attention_kernel(
   const bool wave_rows_full = wave_first + 32 <= q_len;
 
   if (ntiles > 0) {
-    // prologue: tile 0 into buffer 0
-    issue_k(0, 0);
-    fetch_v(0);
-    store_vt(0);
+    issue(0, 0);  // prologue: tile 0 into buffer 0
     __builtin_amdgcn_s_waitcnt(0);
     lds_barrier();
   }
@@ -208,15 +194,11 @@ __global__ __launch_bounds__(HPB * QSUB * 64) void paged_attention_kernel(
   // one KV tile; `buf` is a literal at both call sites below, so every LDS
   // address is a per-lane base plus a constant offset
   auto tile = [&](const int t, const int buf) {
-    const bool more = t + 1 < ntiles;
-    if (more) {
-      issue_k(t + 1, buf ^ 1);
-      fetch_v(t + 1);
-    }
+    if (t + 1 < ntiles) issue(t + 1, buf ^ 1);
     const int t0 = t * kBK;
     if (t0 < wave_end) {  // wave-uniform: a tile wholly past this wave's rows is skipped
       // ---- S^T = K Q^T for two 32-key subtiles -------------------------
-      const uint8_t* kl = &k_lds[buf][0];
+      const uint8_t* kl = buf ? k_lds1 : k_lds0;
       // four independent accumulator chains (2 key subtiles x even/odd d
       // steps), so consecutive MFMAs never wait on each other
       v16f sacc[2], sodd[2];
@@ -227,11 +209,9 @@ __global__ __launch_bounds__(HPB * QSUB * 64) void paged_attention_kernel(
       }
 #pragma unroll
       for (int c = 0; c < ND16; ++c) {
-        const int lc = 2 * c + half;
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
-          const int key = ks * 32 + col;
-          const v8s kf = *reinterpret_cast<const v8s*>(kl + key * KROW + ((lc ^ kswz<D>(key)) * 16));
+          const v8s kf = *reinterpret_cast<const v8s*>(kl + ks * 32 * ROW + k_off[c]);
           if (c & 1)
             sodd[ks] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
                 __builtin_bit_cast(v8bf, kf), __builtin_bit_cast(v8bf, qf[c]), sodd[ks], 0, 0, 0);
@@ -292,24 +272,28 @@ __global__ __launch_bounds__(HPB * QSUB * 64) void paged_attention_kernel(
       }
       m_run = m_new;
       // ---- O^T += V^T P^T -------------------------------------------------
-      const uint8_t* vl = &vt_lds[buf][0];
-      // d tiles innermost: NDS independent accumulators between dependent MFMAs
+      // MFMA kc covers keys kc/2*32 + (kc&1)*16 + {4*half + 0..3, 8 + 4*half + 0..3}
+      // in its k slots half*8 + 0..7, the order in which P^T's lanes hold them
+      const uint8_t* vl = buf ? v_lds1 : v_lds0;
 #pragma unroll
       for (int kc = 0; kc < 4; ++kc) {
-        const int lc = 2 * kc + half;
+        const int kbase_b = ((kc >> 1) * 32 + (kc & 1) * 16) * ROW;
         v8h vf[NDS];
 #pragma unroll
         for (int d = 0; d < NDS; ++d) {
-          const int dr = d * 32 + col;
-          vf[d] = *reinterpret_cast<const v8h*>(vl + dr * (kBK * 2) + ((lc ^ ((dr >> 1) & 7)) * 16));
+          const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (lds_v4s*)(vl + kbase_b + v_off[d]));
+          const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (lds_v4s*)(vl + kbase_b + 8 * ROW + v_off[d]));
+          const v8s both = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+          vf[d] = __builtin_bit_cast(v8h, both);
         }
 #pragma unroll
         for (int d = 0; d < NDS; ++d)
           o[d] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[d], pf[kc], o[d], 0, 0, 0);
       }
     }
-    if (more) store_vt(buf ^ 1);
-    __builtin_amdgcn_s_waitcnt(0);  // this wave's K rows landed in LDS
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's K and V rows of tile t + 1 landed
     lds_barrier();
   };
   for (int t = 0; t < ntiles; t += 2) {

@@ -48,13 +48,6 @@ constexpr int kOperandLoadPolicy = 16;
 
 __device__ __forceinline__ int swz(int row) { return (row >> 2) & 3; }
 
-// s_waitcnt with vmcnt <= n and the other counters unconstrained (gfx9
-// encoding: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt_hi[15:14]).
-template <int n>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(n >= 0 && n < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((n & 15) | (7 << 4) | (15 << 8) | ((n >> 4) << 14));
-}
 
 template <int BM, int BN, int WAVES_N, int WAVES_M, int STAGES>
 struct GemmCfg {
@@ -502,7 +495,9 @@ struct Cfg128 {
   static constexpr int kTM = BM / WAVES_M / 32;
   static constexpr int kABytes = BM * 128;
   static constexpr int kWBytes = BN * 128;
-  static constexpr int kSaBytes = BM * 4;  // the tile's token scales of the block
+  // the tile's token scales of the block: 64 slots per wave, the first
+  // kSaPerWave of them used
+  static constexpr int kSaBytes = 256 * WAVES_N * WAVES_M;
   static constexpr int kStage = kABytes + kWBytes + kSaBytes;
   static constexpr int kLds = STAGES * kStage;
   static constexpr int kASlabs = BM / 8 / kWaves;
@@ -576,12 +571,13 @@ __global__ __launch_bounds__(64 * WAVES_N * WAVES_M) void gemm_fp8_k128_kernel(
     load_slabs128<Cfg::kWSlabs>(W, K, n0, N - 1, k_off, buf + Cfg::kABytes, wave * Cfg::kWSlabs,
                                 lane);
     // token scales of the tile for this block, beside its operands: lane i of
-    // wave w loads the scale of tile row w * kSaPerWave + i
-    if (lane < Cfg::kSaPerWave) {
-      const int t = min(m0 + wave * Cfg::kSaPerWave + lane, M - 1);
-      __builtin_amdgcn_global_load_lds(
-          (const void*)(sA + (int64_t)kb * sa_ld + t),
-          (lds_void*)(buf + Cfg::kABytes + Cfg::kWBytes + wave * Cfg::kSaPerWave * 4), 4, 0, 0);
+    // wave w loads the scale of tile row w * kSaPerWave + i into slot
+    // w * 64 + i (lanes past kSaPerWave repeat a row into unused slots)
+    {
+      const int t = min(m0 + wave * Cfg::kSaPerWave + lane % Cfg::kSaPerWave, M - 1);
+      __builtin_amdgcn_global_load_lds((const void*)(sA + (int64_t)kb * sa_ld + t),
+                                       (lds_void*)(buf + Cfg::kABytes + Cfg::kWBytes + wave * 256),
+                                       4, 0, 0);
     }
     sw_ring[stage] = __builtin_nontemporal_load(sw_row + kb);
     if (WARM) {
@@ -630,7 +626,9 @@ __global__ __launch_bounds__(64 * WAVES_N * WAVES_M) void gemm_fp8_k128_kernel(
             const float* sa_lds =
                 reinterpret_cast<const float*>(smem + stage * Cfg::kStage + Cfg::kABytes +
                                                Cfg::kWBytes);
-            const float s_cur = sa_lds[wm * TM * 32 + b * 32 + (lane & 31)] * sw;
+            const int row = wm * TM * 32 + b * 32 + (lane & 31);
+            const float s_cur =
+                sa_lds[(row / Cfg::kSaPerWave) * 64 + row % Cfg::kSaPerWave] * sw;
             const float r = s_prev[b] / s_cur;
 #pragma unroll
             for (int a = 0; a < TN; ++a)

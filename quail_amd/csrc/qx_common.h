@@ -98,6 +98,14 @@ __device__ __forceinline__ float group_sum(float v) {
 // accesses across it.
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_barrier" ::: "memory"); }
 
+// s_waitcnt with vmcnt <= n and the other counters unconstrained (gfx9
+// encoding: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt_hi[15:14]).
+template <int n>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(n >= 0 && n < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((n & 15) | (7 << 4) | (15 << 8) | ((n >> 4) << 14));
+}
+
 // Per-group FP8 scale: max(amax, 1e-10) / 448 (attention.py:780-781).
 __device__ __forceinline__ float fp8_scale(float amax) {
   return fmaxf(amax, kScaleFloor) / kFp8Max;

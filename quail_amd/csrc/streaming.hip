@@ -346,6 +346,9 @@ __global__ __launch_bounds__(256) void group_quant_kernel(const uint16_t* __rest
 // ---------------------------------------------------------------------------
 // pool[dst[i]] = rows[src[i]] for K and V; dst < 0 writes nothing
 // (attention.py:885-897). One wave per pair; rows are row_elems bf16.
+// V_F16: V source rows are bf16 and the V pool holds fp16 (round to nearest
+// even, exact for |v| in [2^-14, 65504]); otherwise both are copied as they are
+template <bool V_F16>
 __global__ __launch_bounds__(256) void kv_scatter_kernel(
     const uint16_t* __restrict__ k, int64_t k_ld, const uint16_t* __restrict__ v, int64_t v_ld,
     uint16_t* __restrict__ kp, uint16_t* __restrict__ vp, const int64_t* __restrict__ src,
@@ -363,7 +366,14 @@ __global__ __launch_bounds__(256) void kv_scatter_kernel(
   const int nch = row_elems >> 3;
   for (int c = lane; c < nch; c += 64) {
     kd[c] = ks[c];
-    vd[c] = vs[c];
+    uint4 w = vs[c];
+    if (V_F16) {
+      w.x = pack2_f16(lo_bf16(w.x), hi_bf16(w.x));
+      w.y = pack2_f16(lo_bf16(w.y), hi_bf16(w.y));
+      w.z = pack2_f16(lo_bf16(w.z), hi_bf16(w.z));
+      w.w = pack2_f16(lo_bf16(w.w), hi_bf16(w.w));
+    }
+    vd[c] = w;
   }
 }
 
@@ -525,16 +535,24 @@ int qx_group_quant(const void* x, int64_t x_ld, void* q, int64_t q_ld, float* sc
 
 int qx_kv_scatter(const void* k, int64_t k_ld, const void* v, int64_t v_ld, void* k_pool,
                   void* v_pool, const int64_t* src, const int64_t* dst, int64_t count,
-                  int64_t row_elems, hipStream_t stream) {
+                  int64_t row_elems, int v_to_f16, hipStream_t stream) {
   QX_CHECK(k && v && k_pool && v_pool && src && dst, "kv_scatter: null pointer");
   QX_CHECK(row_elems > 0 && row_elems % 8 == 0, "kv_scatter: row %lld", (long long)row_elems);
   QX_CHECK(k_ld % 8 == 0 && v_ld % 8 == 0 && aligned16(k) && aligned16(v) && aligned16(k_pool) &&
                aligned16(v_pool),
            "kv_scatter: alignment");
   if (count == 0) return QX_OK;
-  hipLaunchKernelGGL(kv_scatter_kernel, dim3((unsigned)((count + 3) / 4)), dim3(256), 0, stream,
-                     (const uint16_t*)k, k_ld, (const uint16_t*)v, v_ld, (uint16_t*)k_pool,
-                     (uint16_t*)v_pool, src, dst, (int)count, (int)row_elems);
+  if (v_to_f16) {
+    hipLaunchKernelGGL(kv_scatter_kernel<true>, dim3((unsigned)((count + 3) / 4)), dim3(256), 0,
+                       stream, (const uint16_t*)k, k_ld, (const uint16_t*)v, v_ld,
+                       (uint16_t*)k_pool, (uint16_t*)v_pool, src, dst, (int)count,
+                       (int)row_elems);
+  } else {
+    hipLaunchKernelGGL(kv_scatter_kernel<false>, dim3((unsigned)((count + 3) / 4)), dim3(256), 0,
+                       stream, (const uint16_t*)k, k_ld, (const uint16_t*)v, v_ld,
+                       (uint16_t*)k_pool, (uint16_t*)v_pool, src, dst, (int)count,
+                       (int)row_elems);
+  }
   QX_LAUNCH_STATUS();
 }
 

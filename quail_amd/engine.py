@@ -241,14 +241,20 @@ class Engine:
         return q, k
 
     def kv_row_scatter(self, k3, v3, src, dst, layer):
-        """Scatter KV rows into the layer's arena pages; dst < 0 is padding."""
+        """Scatter KV rows into the layer's arena pages; dst < 0 is padding.
+
+        The V pages hold fp16 (the PV product runs in fp16): bf16 V rows are
+        converted as they are written; rows already in the pools (the tail
+        copy, v3 of dtype float16) are copied unchanged."""
         count = src.shape[0]
         row = self.num_kv_heads * self.head_dim
         k_pool, v_pool = self.arena.layer_kv(layer)
+        if v_pool.dtype != torch.float16:
+            raise ValueError(f"V pool dtype {v_pool.dtype}: this engine keeps V pages in fp16")
         k_ld = k3.stride(0)
         v_ld = v3.stride(0)
         _lib.call("qx_kv_scatter", _ptr(k3), k_ld, _ptr(v3), v_ld, _ptr(k_pool), _ptr(v_pool),
-                  _ptr(src), _ptr(dst), count, row, _stream())
+                  _ptr(src), _ptr(dst), count, row, int(v3.dtype != torch.float16), _stream())
 
     def write_kv(self, k3, v3, meta, *, copy_tail=True):
         """Write fresh rows and retained partial pages (attention.py:1175-1195)."""

@@ -251,7 +251,7 @@ def test_kv_scatter_is_bit_exact_and_skips_negative_rows():
     k = torch.randn(n, hk * d, generator=g).to(torch.bfloat16).to(DEV)
     v = qkv[:, 40 * 128:]                         # strided v slice of qkv
     kp = torch.zeros(256, hk, d, dtype=torch.bfloat16, device=DEV)
-    vp = torch.zeros_like(kp)
+    vp = torch.zeros(256, hk, d, dtype=torch.float16, device=DEV)   # V pages are fp16
     src = torch.arange(n, device=DEV)
     dst = torch.randperm(256, generator=g)[:n].to(DEV)
     dst[5] = -1
@@ -259,7 +259,8 @@ def test_kv_scatter_is_bit_exact_and_skips_negative_rows():
     eng.kv_row_scatter(k, v, src, dst, 0)
     ok = dst >= 0
     assert torch.equal(kp[dst[ok]], k.view(n, hk, d)[ok])
-    assert torch.equal(vp[dst[ok]], v.reshape(n, hk, d)[ok])
+    # bf16 -> fp16 round to nearest even, as torch converts
+    assert torch.equal(vp[dst[ok]], v.reshape(n, hk, d)[ok].float().half())
     written = torch.zeros(256, dtype=torch.bool, device=DEV)
     written[dst[ok]] = True
     assert torch.all(kp[~written] == 0)
@@ -293,7 +294,8 @@ def test_paged_attention_matches_exact_fp32(hq, hk, d):
     page = 16
     q, kp, vp, cu, used, table = _paged_case(hq + d, hq, hk, d, page, 6, 160)
     want = ref.paged_attention(q, kp, vp, cu, used, table, page)
-    eng = _engine(hq, hk, d, arena=_Arena(kp.to(DEV), vp.to(DEV), page))
+    # the engine's V pages hold fp16 (what qx_kv_scatter writes); the oracle reads bf16 V
+    eng = _engine(hq, hk, d, arena=_Arena(kp.to(DEV), vp.float().half().to(DEV), page))
     meta = dict(unified=dict(cu_q=torch.tensor(cu, device=DEV),
                              used=torch.tensor(used, device=DEV),
                              table=torch.tensor(table, device=DEV),
