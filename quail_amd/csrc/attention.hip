@@ -20,9 +20,10 @@
 // Kernel layout (CDNA4). A workgroup is QSUB 32-row query tiles of one
 // sequence x HPB query heads sharing one KV head: one wave per (tile, head),
 // so every K/V tile staged in LDS serves HPB * QSUB * 32 query rows. KV is
-// consumed in 64-key tiles, double buffered: while a tile is computed, the
-// next tile's K and V rows travel HBM -> LDS directly (global_load_lds),
-// one barrier per tile. The sequence's page-table row is staged in LDS once.
+// consumed in 64-key tiles, software pipelined: each step computes S of the
+// next tile beside the softmax and PV of the current one, while K and V rows
+// of later tiles travel HBM -> LDS directly (global_load_lds) into double
+// buffers; one barrier per step. The sequence's page-table row is staged in LDS once.
 //
 // Each wave forms S^T = K Q^T with v_mfma_f32_32x32x16_bf16 so that a lane
 // owns one query column; the online softmax is then lane-local (plus one
@@ -78,10 +79,9 @@ __global__ __launch_bounds__(HPB * QSUB * 64) void paged_attention_kernel(
   static_assert(SLABS >= 1 && SLABS * KEYS_PER_SLAB * NW == kBK, "slabs");
   // separate objects per buffer, so the compiler can see that the direct
   // loads into one buffer never alias the reads of the other
-  __shared__ __attribute__((aligned(1024))) uint8_t k_lds0[T_BYTES];
-  __shared__ __attribute__((aligned(1024))) uint8_t k_lds1[T_BYTES];
-  __shared__ __attribute__((aligned(1024))) uint8_t v_lds0[T_BYTES];
-  __shared__ __attribute__((aligned(1024))) uint8_t v_lds1[T_BYTES];
+  __shared__ __attribute__((aligned(1024))) uint8_t kv_lds[2][2][T_BYTES];  // [buffer][K, V]
+  auto k_buf = [&](int b) -> uint8_t* { return &kv_lds[b][0][0]; };
+  auto v_buf = [&](int b) -> uint8_t* { return &kv_lds[b][1][0]; };
   __shared__ int pages_lds[kMaxPages];
 
   const int s = blockIdx.y;
@@ -123,6 +123,11 @@ __global__ __launch_bounds__(HPB * QSUB * 64) void paged_attention_kernel(
     const uint16_t* qrow = q + (int64_t)(q0 + rr) * q_ld + head * D;
 #pragma unroll
     for (int c = 0; c < ND16; ++c) qf[c] = *reinterpret_cast<const v8s*>(qrow + c * 16 + half * 8);
+    // consume the Q fragments here, before any KV load is issued: the
+    // compiler's own waits for them would otherwise land inside the tile
+    // loop, behind the KV loads it does not track, and drain those too
+#pragma unroll
+    for (int c = 0; c < ND16; ++c) asm volatile("" ::"v"(qf[c]));
   }
   const int64_t kv_row = (int64_t)HK * D;  // elements per pool row
   const uint16_t* kbase = kp + kvh * D;
@@ -133,23 +138,22 @@ __global__ __launch_bounds__(HPB * QSUB * 64) void paged_attention_kernel(
   // K and V rows of tile t straight into LDS: lane i of a slab writes bytes
   // [16i, 16i+16): key i / KCH of the slab, physical chunk i % KCH, which
   // holds logical chunk (i % KCH) ^ swizzle(key)
-  auto issue = [&](int t, int buf) {
+  // K (or V) rows of tile t straight into LDS; tiles past the last re-read
+  // the last key (in bounds, never used)
+  auto issue = [&](int t, int buf, bool v) {
 #pragma unroll
     for (int j = 0; j < SLABS; ++j) {
       const int slab = wave * SLABS + j;
       const int key = slab * KEYS_PER_SLAB + lane / KCH;
       const int p = lane % KCH;
       int kidx = t * kBK + key;
-      kidx = kidx < kv_end ? kidx : kv_end - 1;  // tail keys re-read the last key (masked)
+      kidx = kidx < kv_end ? kidx : kv_end - 1;
       const int64_t prow = (int64_t)pages_lds[kidx / kPage] * kPage + (kidx % kPage);
-      const uint16_t* ksrc = kbase + prow * kv_row + (p ^ kswz<D>(key)) * 8;
-      const uint16_t* vsrc = vbase + prow * kv_row + (p ^ vswz<D>(key)) * 8;
-      __builtin_amdgcn_global_load_lds((const void*)ksrc,
-                                       (lds_void*)((buf ? k_lds1 : k_lds0) + slab * 1024), 16, 0,
-                                       0);
-      __builtin_amdgcn_global_load_lds((const void*)vsrc,
-                                       (lds_void*)((buf ? v_lds1 : v_lds0) + slab * 1024), 16, 0,
-                                       0);
+      if (v) {
+        lds_dma16(vbase + prow * kv_row + (p ^ vswz<D>(key)) * 8, v_buf(buf) + slab * 1024);
+      } else {
+        lds_dma16(kbase + prow * kv_row + (p ^ kswz<D>(key)) * 8, k_buf(buf) + slab * 1024);
+      }
     }
   };
 
@@ -185,120 +189,119 @@ __global__ __launch_bounds__(HPB * QSUB * 64) void paged_attention_kernel(
   const int wave_lim_min = causal ? min(off + wave_first + 1, used_s) : used_s;
   const bool wave_rows_full = wave_first + 32 <= q_len;
 
-  if (ntiles > 0) {
-    issue(0, 0);  // prologue: tile 0 into buffer 0
-    __builtin_amdgcn_s_waitcnt(0);
-    lds_barrier();
-  }
-
-  // one KV tile; `buf` is a literal at both call sites below, so every LDS
-  // address is a per-lane base plus a constant offset
-  auto tile = [&](const int t, const int buf) {
-    if (t + 1 < ntiles) issue(t + 1, buf ^ 1);
-    const int t0 = t * kBK;
-    if (t0 < wave_end) {  // wave-uniform: a tile wholly past this wave's rows is skipped
-      // ---- S^T = K Q^T for two 32-key subtiles -------------------------
-      const uint8_t* kl = buf ? k_lds1 : k_lds0;
-      // four independent accumulator chains (2 key subtiles x even/odd d
-      // steps), so consecutive MFMAs never wait on each other
-      v16f sacc[2], sodd[2];
+  // Software pipeline over KV tiles, two LDS buffers each for K and V.
+  // Step t computes S of tile t + 1 (K buffer (t+1)%2) in the same basic
+  // block as the softmax and PV of tile t (V buffer t%2), so the S MFMAs of
+  // one tile overlap the VALU work of the previous one; meanwhile K of tile
+  // t + 2 and V of tile t + 1 load into the buffers steps t - 2 and t - 1
+  // released. Tiles past this wave's rows are fully masked (they add
+  // nothing); tiles past the last are computed from stale data and dropped.
+  auto s_tile = [&](const int buf, v16f (&sacc)[2]) {
+    const uint8_t* kl = k_buf(buf);
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) sacc[ks] = v16f{};
+#pragma unroll
+    for (int c = 0; c < ND16; ++c)
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
-        sacc[ks] = v16f{};
-        sodd[ks] = v16f{};
+        const v8s kf = *reinterpret_cast<const v8s*>(kl + ks * 32 * ROW + k_off[c]);
+        sacc[ks] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+            __builtin_bit_cast(v8bf, kf), __builtin_bit_cast(v8bf, qf[c]), sacc[ks], 0, 0, 0);
       }
+  };
+  auto mask_tile = [&](const int t, v16f (&sacc)[2]) {
+    // a tile every row of this wave sees whole needs no mask (wave-uniform)
+    const int t0 = t * kBK;
+    if (t0 + kBK <= wave_lim_min && wave_rows_full) return;
 #pragma unroll
-      for (int c = 0; c < ND16; ++c) {
+    for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-          const v8s kf = *reinterpret_cast<const v8s*>(kl + ks * 32 * ROW + k_off[c]);
-          if (c & 1)
-            sodd[ks] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-                __builtin_bit_cast(v8bf, kf), __builtin_bit_cast(v8bf, qf[c]), sodd[ks], 0, 0, 0);
-          else
-            sacc[ks] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-                __builtin_bit_cast(v8bf, kf), __builtin_bit_cast(v8bf, qf[c]), sacc[ks], 0, 0, 0);
-        }
+      for (int i = 0; i < 16; ++i) {
+        const int kidx = t0 + ks * 32 + (i >> 2) * 8 + half * 4 + (i & 3);
+        sacc[ks][i] = (kidx < lim && r_ok) ? sacc[ks][i] : -INFINITY;
       }
+  };
+  auto softmax_pv = [&](const int buf, v16f (&sacc)[2]) {
+    // the running max is kept on raw scores (scale_log2 > 0), and the scale
+    // folds into one fma per score: p = exp2(s * scale_log2 - m * scale_log2)
+    float tmax = -INFINITY;
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks) sacc[ks] += sodd[ks];
-      // ---- mask, online softmax (lane = one query; partner lane^32) -----
-      // a tile every row of this wave sees whole needs no mask
-      const bool full = t0 + kBK <= wave_lim_min && wave_rows_full;
-      // the running max is kept on raw scores (scale_log2 > 0), and the scale
-      // folds into one fma per score: p = exp2(s * scale_log2 - m * scale_log2)
-      float tmax = -INFINITY;
-      if (full) {
+    for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
-        for (int ks = 0; ks < 2; ++ks)
+      for (int i = 0; i < 16; ++i) tmax = fmaxf(tmax, sacc[ks][i]);
+    tmax = max_halves(tmax);
+    const float m_new = fmaxf(m_run, tmax);
+    const float m_use = m_new == -INFINITY ? 0.f : m_new * scale_log2;
+    const float alpha = __builtin_amdgcn_exp2f(m_run * scale_log2 - m_use);
+    float psum = 0.f;
+    v8h pf[4];
 #pragma unroll
-          for (int i = 0; i < 16; ++i) tmax = fmaxf(tmax, sacc[ks][i]);
-      } else {
+    for (int kc = 0; kc < 4; ++kc) {
 #pragma unroll
-        for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-          for (int i = 0; i < 16; ++i) {
-            const int kidx = t0 + ks * 32 + (i >> 2) * 8 + half * 4 + (i & 3);
-            const float v = (kidx < lim && r_ok) ? sacc[ks][i] : -INFINITY;
-            sacc[ks][i] = v;
-            tmax = fmaxf(tmax, v);
-          }
-      }
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-      const float m_new = fmaxf(m_run, tmax);
-      const float m_use = m_new == -INFINITY ? 0.f : m_new * scale_log2;
-      const float alpha = __builtin_amdgcn_exp2f(m_run * scale_log2 - m_use);
-      float psum = 0.f;
-      v8h pf[4];
-#pragma unroll
-      for (int kc = 0; kc < 4; ++kc) {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          // arguments are <= 0, so v_exp_f32's range is all that is needed
-          const float pv =
-              __builtin_amdgcn_exp2f(fmaf(sacc[kc >> 1][(kc & 1) * 8 + j], scale_log2, -m_use));
-          psum += pv;
-          pf[kc][j] = (_Float16)pv;
-        }
-      }
-      psum += __shfl_xor(psum, 32, 64);
-      l_run = l_run * alpha + psum;
-      // rescale O only when some lane's running max moved
-      if (__builtin_amdgcn_ballot_w64(m_new != m_run) != 0) {
-#pragma unroll
-        for (int d = 0; d < NDS; ++d)
-#pragma unroll
-          for (int e = 0; e < 16; ++e) o[d][e] *= alpha;
-      }
-      m_run = m_new;
-      // ---- O^T += V^T P^T -------------------------------------------------
-      // MFMA kc covers keys kc/2*32 + (kc&1)*16 + {4*half + 0..3, 8 + 4*half + 0..3}
-      // in its k slots half*8 + 0..7, the order in which P^T's lanes hold them
-      const uint8_t* vl = buf ? v_lds1 : v_lds0;
-#pragma unroll
-      for (int kc = 0; kc < 4; ++kc) {
-        const int kbase_b = ((kc >> 1) * 32 + (kc & 1) * 16) * ROW;
-        v8h vf[NDS];
-#pragma unroll
-        for (int d = 0; d < NDS; ++d) {
-          const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-              (lds_v4s*)(vl + kbase_b + v_off[d]));
-          const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-              (lds_v4s*)(vl + kbase_b + 8 * ROW + v_off[d]));
-          const v8s both = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-          vf[d] = __builtin_bit_cast(v8h, both);
-        }
-#pragma unroll
-        for (int d = 0; d < NDS; ++d)
-          o[d] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[d], pf[kc], o[d], 0, 0, 0);
+      for (int j = 0; j < 8; ++j) {
+        // arguments are <= 0, so v_exp_f32's range is all that is needed
+        const float pv =
+            __builtin_amdgcn_exp2f(fmaf(sacc[kc >> 1][(kc & 1) * 8 + j], scale_log2, -m_use));
+        psum += pv;
+        pf[kc][j] = (_Float16)pv;
       }
     }
-    __builtin_amdgcn_s_waitcnt(0);  // this wave's K and V rows of tile t + 1 landed
+    psum = sum_halves(psum);
+    l_run = l_run * alpha + psum;
+    // alpha is 1 where the max did not move; rescaling unconditionally keeps
+    // this step one basic block
+#pragma unroll
+    for (int d = 0; d < NDS; ++d)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) o[d][e] *= alpha;
+    m_run = m_new;
+    // O^T += V^T P^T: MFMA kc covers keys kc/2*32 + (kc&1)*16 +
+    // {4*half + 0..3, 8 + 4*half + 0..3} in its k slots half*8 + 0..7, the
+    // order in which P^T's lanes hold them
+    const uint8_t* vl = v_buf(buf);
+#pragma unroll
+    for (int kc = 0; kc < 4; ++kc) {
+      const int kbase_b = ((kc >> 1) * 32 + (kc & 1) * 16) * ROW;
+      v8h vf[NDS];
+#pragma unroll
+      for (int d = 0; d < NDS; ++d) {
+        const v4s lo =
+            __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(vl + kbase_b + v_off[d]));
+        const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (lds_v4s*)(vl + kbase_b + 8 * ROW + v_off[d]));
+        const v8s both = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        vf[d] = __builtin_bit_cast(v8h, both);
+      }
+#pragma unroll
+      for (int d = 0; d < NDS; ++d)
+        o[d] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[d], pf[kc], o[d], 0, 0, 0);
+    }
+  };
+
+  v16f sa[2], sb[2];
+  if (ntiles > 0) {
+    // prologue: K and V of tile 0 and K of tile 1, then S of tile 0
+    issue(0, 0, false);
+    issue(0, 0, true);
+    issue(1, 1, false);
+    wait_vmcnt<0>();
+    lds_barrier();
+    s_tile(0, sa);
+    lds_barrier();  // every wave has read K of tile 0 before step 0 reloads its buffer
+  }
+  // one step; `cur` (the parity of t) is a literal at both call sites
+  auto step = [&](const int t, const int cur, v16f (&s_cur)[2], v16f (&s_next)[2]) {
+    issue(t + 2, cur, false);    // K buffer of tile t, read by step t - 1
+    issue(t + 1, cur ^ 1, true);  // V buffer of tile t - 1, read by step t - 1
+    mask_tile(t, s_cur);
+    s_tile(cur ^ 1, s_next);      // K of tile t + 1, loaded during step t - 1
+    softmax_pv(cur, s_cur);
+    wait_vmcnt<0>();  // this wave's loads of this step landed
     lds_barrier();
   };
   for (int t = 0; t < ntiles; t += 2) {
-    tile(t, 0);
-    if (t + 1 < ntiles) tile(t + 1, 1);
+    step(t, 0, sa, sb);
+    if (t + 1 < ntiles) step(t + 1, 1, sb, sa);
   }
 
   // ---- epilogue: lane holds query `col`, d = dt*32 + (i/4)*8 + half*4 + i%4
@@ -314,7 +317,7 @@ __global__ __launch_bounds__(HPB * QSUB * 64) void paged_attention_kernel(
         o[d][e] = v;
         amax = fmaxf(amax, fabsf(v));
       }
-    amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
+    amax = max_halves(amax);
     const float sc = fp8_scale(amax);
     if (r_ok) {
       uint8_t* orow = out8 + row * o_ld + head * D;

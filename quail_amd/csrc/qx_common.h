@@ -89,6 +89,21 @@ __device__ __forceinline__ float group_sum(float v) {
   return v;
 }
 
+// Max / sum of x over lanes l and l ^ 32 (the two halves of a wave64),
+// through one v_permlane32_swap instead of an LDS permute: after the swap
+// the pair holds (x[l], x[l + 32]) on lanes l < 32 and (x[l - 32], x[l]) on
+// the others.
+__device__ __forceinline__ float max_halves(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum_halves(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 // Workgroup barrier with no memory fence. __syncthreads() (and an
 // LDS-scoped fence) make the compiler drain every vector-memory load in
 // flight before s_barrier, including the global->LDS prefetches of later
@@ -104,6 +119,29 @@ template <int n>
 __device__ __forceinline__ void wait_vmcnt() {
   static_assert(n >= 0 && n < 64, "vmcnt range");
   __builtin_amdgcn_s_waitcnt((n & 15) | (7 << 4) | (15 << 8) | ((n >> 4) << 14));
+}
+
+typedef __attribute__((address_space(3))) uint8_t lds_u8;
+
+// Direct HBM -> LDS load of 16 bytes per lane (lane i writes lds + 16 i),
+// written as inline assembly so that the compiler does not track it as an
+// LDS write: it would otherwise wait for every such load in flight before
+// any later LDS read, including reads of other buffers. Callers order these
+// loads with explicit s_waitcnt vmcnt and barriers. Loads the compiler does
+// not count can only make its own vmcnt waits stricter (vector memory loads
+// complete in order). M0 is saved and restored around the load.
+__device__ __forceinline__ void lds_dma16(const void* src, const uint8_t* lds) {
+  const uint32_t addr = (uint32_t)(uintptr_t)(lds_u8*)lds;
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %1\n\t"
+      "s_nop 1\n\t"
+      "global_load_lds_dwordx4 %2, off\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "s"(addr), "v"(src)
+      : "memory");
 }
 
 // Per-group FP8 scale: max(amax, 1e-10) / 448 (attention.py:780-781).
