@@ -232,7 +232,11 @@ __global__ __launch_bounds__(HPB * QSUB * 64) void paged_attention_kernel(
     tmax = max_halves(tmax);
     const float m_new = fmaxf(m_run, tmax);
     const float m_use = m_new == -INFINITY ? 0.f : m_new * scale_log2;
-    const float alpha = __builtin_amdgcn_exp2f(m_run * scale_log2 - m_use);
+    // exactly 1 while the max holds, so a tile that adds nothing to a row
+    // (wholly masked for it) leaves its state bit for bit: a row's result
+    // then does not depend on how many such tiles its workgroup visits
+    const float alpha =
+        m_run == m_new ? 1.0f : __builtin_amdgcn_exp2f((m_run - m_new) * scale_log2);
     float psum = 0.f;
     v8h pf[4];
 #pragma unroll
