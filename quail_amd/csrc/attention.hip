@@ -323,6 +323,7 @@ __global__ __launch_bounds__(HPB * QSUB * 64) void paged_attention_kernel(
       }
     amax = max_halves(amax);
     const float sc = fp8_scale(amax);
+    const float rsc = recip(sc);
     if (r_ok) {
       uint8_t* orow = out8 + row * o_ld + head * D;
 #pragma unroll
@@ -331,7 +332,8 @@ __global__ __launch_bounds__(HPB * QSUB * 64) void paged_attention_kernel(
         for (int g = 0; g < 4; ++g) {
           const int dd = d * 32 + g * 8 + half * 4;
           *reinterpret_cast<uint32_t*>(orow + dd) =
-              pack4_fp8(o[d][g * 4] / sc, o[d][g * 4 + 1] / sc, o[d][g * 4 + 2] / sc, o[d][g * 4 + 3] / sc);
+              pack4_fp8(div_by(o[d][g * 4], sc, rsc), div_by(o[d][g * 4 + 1], sc, rsc),
+                        div_by(o[d][g * 4 + 2], sc, rsc), div_by(o[d][g * 4 + 3], sc, rsc));
         }
       if (half == 0) scales[(int64_t)head * s_ld + row] = sc;
     }

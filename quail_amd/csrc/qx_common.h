@@ -144,6 +144,21 @@ __device__ __forceinline__ void lds_dma16(const void* src, const uint8_t* lds) {
       : "memory");
 }
 
+// y / s from the hardware reciprocal r = rcp(s) and one FMA correction of
+// the quotient (the residual y - q0 s is exact in an FMA), which gives the
+// correctly rounded quotient except in rare ties of double rounding; three
+// instructions instead of IEEE division's ten. Callers pass r once per group.
+__device__ __forceinline__ float div_by(float y, float s, float r) {
+  const float q0 = y * r;
+  return fmaf(fmaf(-q0, s, y), r, q0);
+}
+
+// 1 / s to within an ulp: the hardware reciprocal refined by one Newton step.
+__device__ __forceinline__ float recip(float s) {
+  const float r = __builtin_amdgcn_rcpf(s);
+  return fmaf(fmaf(-r, s, 1.0f), r, r);
+}
+
 // Per-group FP8 scale: max(amax, 1e-10) / 448 (attention.py:780-781).
 __device__ __forceinline__ float fp8_scale(float amax) {
   return fmaxf(amax, kScaleFloor) / kFp8Max;

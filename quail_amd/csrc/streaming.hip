@@ -113,10 +113,13 @@ __global__ __launch_bounds__(kRowThreads) void norm_quant_kernel(
     }
     amax = group_max<16>(amax);
     const float scale = fp8_scale(amax);
+    const float rs = recip(scale);
     if (live) {
       uint2 o;
-      o.x = pack4_fp8(y[0] / scale, y[1] / scale, y[2] / scale, y[3] / scale);
-      o.y = pack4_fp8(y[4] / scale, y[5] / scale, y[6] / scale, y[7] / scale);
+      o.x = pack4_fp8(div_by(y[0], scale, rs), div_by(y[1], scale, rs), div_by(y[2], scale, rs),
+                      div_by(y[3], scale, rs));
+      o.y = pack4_fp8(div_by(y[4], scale, rs), div_by(y[5], scale, rs), div_by(y[6], scale, rs),
+                      div_by(y[7], scale, rs));
       *reinterpret_cast<uint2*>(qrow + c * 8) = o;
       if ((lane & 15) == 0) scales[(int64_t)(c >> 4) * s_ld + row] = scale;
     }
@@ -316,11 +319,16 @@ __global__ __launch_bounds__(256) void group_quant_kernel(const uint16_t* __rest
     if (SILU) {
       uint4 u = *reinterpret_cast<const uint4*>(xrow + I + col);
       uint32_t uw[4] = {u.x, u.y, u.z, u.w};
+      // sigmoid(g) = 1 / (1 + e^-g), e^-g = 2^(-g log2 e) on v_exp_f32; past
+      // |g| ~ 88 the exponential saturates to 0 or inf and sigmoid to 1 or 0
+      constexpr float kLog2e = 1.4426950408889634f;
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
-        float g0 = lo_bf16(gw[k]), g1 = hi_bf16(gw[k]);
-        y[2 * k] = g0 * (1.0f / (1.0f + expf(-g0))) * lo_bf16(uw[k]);
-        y[2 * k + 1] = g1 * (1.0f / (1.0f + expf(-g1))) * hi_bf16(uw[k]);
+        const float g0 = lo_bf16(gw[k]), g1 = hi_bf16(gw[k]);
+        const float d0 = 1.0f + __builtin_amdgcn_exp2f(-g0 * kLog2e);
+        const float d1 = 1.0f + __builtin_amdgcn_exp2f(-g1 * kLog2e);
+        y[2 * k] = g0 * recip(d0) * lo_bf16(uw[k]);
+        y[2 * k + 1] = g1 * recip(d1) * hi_bf16(uw[k]);
       }
     } else {
 #pragma unroll
@@ -334,10 +342,13 @@ __global__ __launch_bounds__(256) void group_quant_kernel(const uint16_t* __rest
   }
   amax = group_max<16>(amax);
   const float scale = fp8_scale(amax);
+  const float rs = recip(scale);
   if (live) {
     uint2 o;
-    o.x = pack4_fp8(y[0] / scale, y[1] / scale, y[2] / scale, y[3] / scale);
-    o.y = pack4_fp8(y[4] / scale, y[5] / scale, y[6] / scale, y[7] / scale);
+    o.x = pack4_fp8(div_by(y[0], scale, rs), div_by(y[1], scale, rs), div_by(y[2], scale, rs),
+                    div_by(y[3], scale, rs));
+    o.y = pack4_fp8(div_by(y[4], scale, rs), div_by(y[5], scale, rs), div_by(y[6], scale, rs),
+                    div_by(y[7], scale, rs));
     *reinterpret_cast<uint2*>(q + (int64_t)row * q_ld + col) = o;
     if ((lane & 15) == 0) scales[(int64_t)(col >> 7) * s_ld + row] = scale;
   }
