@@ -170,6 +170,20 @@ int qx_answer_head(const void* normed, int64_t n_ld, const void* rows, int64_t r
                    float* logits, uint8_t* bits, float* yes_no, float* score,
                    hipStream_t stream);
 
+/*
+ * Host function (no device work): the prefix tree of n documents, document i
+ * being tokens[offsets[i] .. offsets[i+1]) (offsets[0] == 0, host memory).
+ * order[k] = the k-th document in lexicographic token order (stable);
+ * shared[i] = min(common prefix with its predecessor in that order,
+ * len(i) - 1) rounded down to page_tokens; parent[i] = the document it
+ * borrows from (its predecessor or, climbing, the nearest ancestor that
+ * borrowed at least as much), -1 if shared[i] == 0. Replaces
+ * PrefixIndex::new / PrefixIndex::tree (crates/quail-planner/src/inputs/
+ * prefix.rs:33-73) behind PrefixTree (quail/common/tokens.py:440-484).
+ */
+int qx_prefix_tree(const int64_t* tokens, const int64_t* offsets, int64_t n,
+                   int64_t page_tokens, int64_t* order, int64_t* parent, int64_t* shared);
+
 #ifdef __cplusplus
 }
 #endif

@@ -39,6 +39,7 @@ SIGNATURES = {
     "qx_embed": [_p, _i64, _p, _p, _i64, _i64, _i64, _p],
     "qx_paged_attention": [_p, _i64, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64,
                            _i64, _i64, _f32, _i32, _p, _p, _i64, _p, _i64, _p],
+    "qx_prefix_tree": [_p, _p, _i64, _i64, _p, _p, _p],
     "qx_answer_head": [_p, _i64, _p, _i64, _i64, _i64, _i64, _i32, _p, _f32, _p, _p, _p, _p,
                        _p],
 }

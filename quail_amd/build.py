@@ -1,8 +1,9 @@
 """Build libquail_mi355x.so, the C-ABI library of gfx950 kernels, in-tree.
 
 `python -m quail_amd.build` compiles every `csrc/*.hip` with hipcc for
-gfx950 and links them into `quail_amd/libquail_mi355x.so`. The library has
-no torch dependency; Python reaches it through ctypes (quail_amd/_lib.py).
+gfx950 and every host-only `csrc/*.cpp` (the packing runtime) with g++, and
+links them into `quail_amd/libquail_mi355x.so`. The library has no torch
+dependency; Python reaches it through ctypes (quail_amd/_lib.py).
 """
 
 import concurrent.futures
@@ -34,20 +35,28 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found; the gfx950 kernels cannot be built")
 
 
+HOST_FLAGS = ["-O3", "-fPIC", "-std=c++17", "-Wall"]
+
+
 def _compile(src: Path, obj: Path) -> None:
-    cmd = [hipcc(), *FLAGS, "-I", str(CSRC), "-c", str(src), "-o", str(obj)]
+    if src.suffix == ".cpp":
+        # host-only C++ (the packing runtime): the system compiler
+        cmd = [shutil.which("g++") or "g++", *HOST_FLAGS, "-I", str(CSRC), "-c", str(src),
+               "-o", str(obj)]
+    else:
+        cmd = [hipcc(), *FLAGS, "-I", str(CSRC), "-c", str(src), "-o", str(obj)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
-        raise RuntimeError(f"hipcc failed on {src.name}:\n{proc.stderr}")
+        raise RuntimeError(f"{cmd[0]} failed on {src.name}:\n{proc.stderr}")
 
 
 def build(verbose: bool = False) -> Path:
     """Compile and link the library; returns its path."""
     BUILD.mkdir(exist_ok=True)
-    sources = sorted(CSRC.glob("*.hip"))
+    sources = sorted(CSRC.glob("*.hip")) + sorted(CSRC.glob("*.cpp"))
     if not sources:
         raise RuntimeError(f"no HIP sources under {CSRC}")
-    objects = [BUILD / (src.stem + ".o") for src in sources]
+    objects = [BUILD / (src.name.replace(".", "_") + ".o") for src in sources]
     workers = min(len(sources), max(1, min(8, os.cpu_count() or 1)))
     with concurrent.futures.ThreadPoolExecutor(workers) as pool:
         futures = [pool.submit(_compile, s, o) for s, o in zip(sources, objects)]

@@ -167,8 +167,10 @@ __device__ __forceinline__ float fp8_scale(float amax) {
 }  // namespace qx
 
 // Status codes of every extern "C" entry point.
+#ifndef QX_OK
 #define QX_OK 0
 #define QX_EINVAL (-1)
+#endif
 
 // Record a launch error (if any) as the entry point's return value.
 #define QX_LAUNCH_STATUS()                          \

@@ -2,6 +2,11 @@
 // QX_EINVAL (-1) after recording a message here, or a positive hipError_t.
 #pragma once
 
+#ifndef QX_OK
+#define QX_OK 0
+#define QX_EINVAL (-1)
+#endif
+
 namespace qx {
 void set_error(const char* fmt, ...);
 }

@@ -12,6 +12,8 @@ freed once its answer is read, or when its last borrower is admitted.
 import time
 from collections import deque
 
+import numpy as np
+
 from quail_amd.admission import StageAdmission
 from quail_amd.chunk import ArenaFullError, InputStaging, pack_chunk, upload
 from quail_amd.prefix import PrefixIndex
@@ -37,7 +39,9 @@ class StageRun:
         t0 = time.perf_counter()
         tree = None
         if self.use_tree:
-            prompts = [list(p) + [int(s) for suf in sufs for s in suf]
+            prompts = [np.concatenate([np.asarray(p, dtype=np.int64)] +
+                                      [np.asarray(suf, dtype=np.int64).reshape(-1)
+                                       for suf in sufs])
                        for p, sufs in zip(self.prefixes, self.suffixes)]
             tree = PrefixIndex(prompts).tree(self.arena.page_tokens)
         adm = StageAdmission(self.prefixes, self.suffixes, self.arena, self.chunk_budget,

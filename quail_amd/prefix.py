@@ -1,6 +1,7 @@
 """Prefix tree over the documents' token sequences.
 
-Restates the reference planner's PrefixIndex / PrefixTree
+The tree itself is computed by qx_prefix_tree (csrc/host_prefix.cpp), which
+restates the reference planner's PrefixIndex / PrefixTree
 (crates/quail-planner/src/inputs/prefix.rs:14-121; Python wrapper
 quail/common/tokens.py:440-484):
 
@@ -14,13 +15,9 @@ quail/common/tokens.py:440-484):
 
 from dataclasses import dataclass
 
+import numpy as np
 
-def _common_prefix(a, b) -> int:
-    n = min(len(a), len(b))
-    i = 0
-    while i < n and a[i] == b[i]:
-        i += 1
-    return i
+from quail_amd import _lib
 
 
 @dataclass(frozen=True)
@@ -58,25 +55,34 @@ class PrefixTree:
 
 
 class PrefixIndex:
-    """Documents in sorted token order and what each shares with its predecessor."""
+    """Documents in sorted token order and what each shares with its
+    predecessor, computed by the native qx_prefix_tree (host C++).
+
+    documents: token sequences (numpy arrays or lists of ints >= 0)."""
 
     def __init__(self, documents):
-        docs = [tuple(int(t) for t in d) for d in documents]
-        self.order = sorted(range(len(docs)), key=docs.__getitem__)
-        self.shared = [0] * len(docs)
-        for prev, cur in zip(self.order, self.order[1:]):
-            common = _common_prefix(docs[prev], docs[cur])
-            self.shared[cur] = min(common, max(len(docs[cur]) - 1, 0))
+        docs = [np.asarray(d, dtype=np.int64).reshape(-1) for d in documents]
+        lengths = np.fromiter((len(d) for d in docs), dtype=np.int64, count=len(docs))
+        self._offsets = np.zeros(len(docs) + 1, dtype=np.int64)
+        np.cumsum(lengths, out=self._offsets[1:])
+        self._tokens = (np.concatenate(docs) if docs else np.zeros(0, dtype=np.int64))
+        self._tokens = np.ascontiguousarray(self._tokens, dtype=np.int64)
+        order, _, shared = self._native(1)
+        self.order = order.tolist()
+        self.shared = shared.tolist()
+
+    def _native(self, page_tokens):
+        n = len(self._offsets) - 1
+        order = np.empty(n, dtype=np.int64)
+        parent = np.empty(n, dtype=np.int64)
+        shared = np.empty(n, dtype=np.int64)
+        ptr = lambda a: a.ctypes.data if a.size else None
+        _lib.call("qx_prefix_tree", ptr(self._tokens), self._offsets.ctypes.data, n,
+                  int(page_tokens), ptr(order), ptr(parent), ptr(shared))
+        return order, parent, shared
 
     def tree(self, page_tokens: int) -> PrefixTree:
-        shared = [s // page_tokens * page_tokens for s in self.shared]
-        parent = [None] * len(shared)
-        for prev, cur in zip(self.order, self.order[1:]):
-            want = shared[cur]
-            if want <= 0:
-                continue
-            owner = prev
-            while parent[owner] is not None and shared[owner] >= want:
-                owner = parent[owner]
-            parent[cur] = owner
-        return PrefixTree(order=list(self.order), parent=parent, shared=shared)
+        order, parent, shared = self._native(page_tokens)
+        return PrefixTree(order=order.tolist(),
+                          parent=[None if p < 0 else int(p) for p in parent],
+                          shared=shared.tolist())

@@ -1,9 +1,15 @@
-"""Prefix tree against the reference planner's known answers
-(crates/quail-planner/tests/prefix.rs:10-76) and a brute-force restatement."""
+"""Prefix tree (the native qx_prefix_tree) against the reference planner's
+known answers (crates/quail-planner/tests/prefix.rs:10-76), the oracle's
+restatement and a brute-force definition."""
 
 import itertools
 import random
 
+import numpy as np
+import pytest
+
+from oracle import prefix_ref
+from quail_amd import _lib
 from quail_amd.prefix import PrefixIndex, ReaderGroup
 
 DOCS = [[1, 2, 3, 4, 5], [1, 2, 3, 4, 9], [1, 2, 3, 4, 5], [], [7, 8], [1, 2]]
@@ -64,8 +70,40 @@ def test_random_corpora_match_definition():
             assert tree.order == order
             assert tree.shared == shared
             assert tree.parent == parent
+            assert prefix_ref.PrefixIndex(docs).tree(page) == (order, parent, shared)
             # a parent precedes its child in the order
             pos = {d: i for i, d in enumerate(tree.order)}
             for child, p in enumerate(tree.parent):
                 if p is not None:
                     assert pos[p] < pos[child]
+
+
+def test_oracle_matches_the_known_answers():
+    index = prefix_ref.PrefixIndex(DOCS)
+    assert index.order == [3, 5, 0, 2, 1, 4]
+    assert index.shared == [2, 4, 4, 0, 0, 0]
+    assert index.tree(2)[1] == [5, 0, 0, None, None, None]
+
+
+def test_large_corpus_matches_the_oracle():
+    """A Qwen3-4B-sized corpus: 512 documents behind one 64-token prefix,
+    with some duplicated and nested documents."""
+    rng = np.random.default_rng(5)
+    prefix = rng.integers(0, 151936, 64)
+    docs = [np.concatenate([prefix, rng.integers(0, 151936, int(n))])
+            for n in rng.integers(32, 600, 500)]
+    docs += [docs[3].copy(), docs[7][:100].copy(), prefix[:40].copy(), np.zeros(0, np.int64)]
+    docs += [np.concatenate([docs[9][:200], rng.integers(0, 5, 30)]) for _ in range(8)]
+    for page in (1, 16):
+        got = PrefixIndex(docs).tree(page)
+        want = prefix_ref.PrefixIndex([d.tolist() for d in docs]).tree(page)
+        assert (got.order, got.parent, got.shared) == want
+
+
+def test_native_rejects_bad_offsets():
+    tokens = np.arange(6, dtype=np.int64)
+    offsets = np.array([0, 4, 2], dtype=np.int64)
+    out = [np.empty(2, dtype=np.int64) for _ in range(3)]
+    with pytest.raises(_lib.QxError, match="offsets"):
+        _lib.call("qx_prefix_tree", tokens.ctypes.data, offsets.ctypes.data, 2, 16,
+                  *(o.ctypes.data for o in out))
