@@ -199,11 +199,12 @@ def pack_chunk(arena, groups, *, attention_mode="unified", mask="causal", timing
         max_q=int(np.diff(cu_q_arr).max()) if len(cu_q) > 1 else 0,
         max_used=int(used.max()) if len(used) else 0, causal=True)
     cu_a_arr = np.asarray(cu_a, dtype=np.int32)
-    meta = dict(layer=0, unified=unified, cu_a=cu_a_arr,
-                max_a=int(np.diff(cu_a_arr).max()) if len(cu_a) > 1 else 0)
     ids = _cat(id_parts)
     positions = _cat(pos_parts)
     final = _cat(finals)
+    meta = dict(layer=0, unified=unified, cu_a=cu_a_arr,
+                max_a=int(np.diff(cu_a_arr).max()) if len(cu_a) > 1 else 0,
+                final_query=_final_query(cu_q_arr, used, table, final))
     if timing is not None:
         timing["pack_py"] = timing.get("pack_py", 0.0) + (t1 - t0)
         timing["pack_unified"] = timing.get("pack_unified", 0.0) + (time.perf_counter() - t1)
@@ -213,6 +214,23 @@ def pack_chunk(arena, groups, *, attention_mode="unified", mask="causal", timing
                  fresh_keys=tuple(fresh_keys),
                  rows_per_answer=np.concatenate(rows_per_answer) if multi else None,
                  host_ids=ids, host_positions=positions)
+
+
+def _final_query(cu_q, used, table, final):
+    """Attention metadata with one query per final row: final row r of
+    sequence s (i = r - cu_q[s], q_len rows) sees the keys [0, used[s] -
+    q_len + i + 1) through table[s], so as a one-row sequence it reads
+    exactly what it reads inside its own sequence. The last layer needs
+    nothing else from the attention."""
+    final = np.asarray(final, dtype=np.int64)
+    if not len(final):
+        return None
+    seq = np.searchsorted(cu_q, final, side="right") - 1
+    q_len = cu_q[seq + 1] - cu_q[seq]
+    visible = (used[seq] - q_len + (final - cu_q[seq]) + 1).astype(np.int32)
+    return dict(cu_q=np.arange(len(final) + 1, dtype=np.int32), used=visible,
+                table=np.ascontiguousarray(table[seq]), max_q=1,
+                max_used=int(visible.max()), causal=True)
 
 
 # ---- staging ----------------------------------------------------------------
@@ -272,5 +290,12 @@ def upload(chunk: Chunk, staging: InputStaging) -> Chunk:
     dev["table"] = staging.copy("block_table", u["table"], torch.int32)
     chunk.host["unified"] = u
     chunk.meta["unified"] = dev
+    fq = chunk.meta.get("final_query")
+    if fq is not None:
+        chunk.host["final_query"] = fq
+        chunk.meta["final_query"] = dict(
+            fq, cu_q=staging.copy("final_cu_q", fq["cu_q"], torch.int32),
+            used=staging.copy("final_used", fq["used"], torch.int32),
+            table=staging.copy("final_table", fq["table"], torch.int32))
     chunk.meta["cu_a"] = staging.copy("cu_a", chunk.meta["cu_a"], torch.int32)
     return chunk

@@ -144,6 +144,37 @@ __device__ __forceinline__ void lds_dma16(const void* src, const uint8_t* lds) {
       : "memory");
 }
 
+// The same with device scope (sc1: the vector L1 keeps no copy), for
+// operands every workgroup streams once.
+__device__ __forceinline__ void lds_dma16_stream(const void* src, const uint8_t* lds) {
+  const uint32_t addr = (uint32_t)(uintptr_t)(lds_u8*)lds;
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %1\n\t"
+      "s_nop 1\n\t"
+      "global_load_lds_dwordx4 %2, off sc1\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "s"(addr), "v"(src)
+      : "memory");
+}
+
+// 4 bytes per lane (lane i writes lds + 4 i), untracked like lds_dma16.
+__device__ __forceinline__ void lds_dma4(const void* src, const uint8_t* lds) {
+  const uint32_t addr = (uint32_t)(uintptr_t)(lds_u8*)lds;
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %1\n\t"
+      "s_nop 1\n\t"
+      "global_load_lds_dword %2, off\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "s"(addr), "v"(src)
+      : "memory");
+}
+
 // y / s from the hardware reciprocal r = rcp(s) and one FMA correction of
 // the quotient (the residual y - q0 s is exact in an FMA), which gives the
 // correctly rounded quotient except in rare ties of double rounding; three

@@ -291,39 +291,61 @@ class Engine:
     def attention_unified(self, q3, k3, v3, meta, *, softmax_scale=None, output=None):
         """Write the chunk's KV to its pages, then one paged causal call with
         the o_proj input quantization fused (attention.py:1477-1573)."""
-        n = q3.shape[0]
-        hq, hk, d = self.num_q_heads, self.num_kv_heads, self.head_dim
-        unified = meta["unified"]
-        if unified is None:
+        if meta["unified"] is None:
             raise ValueError("this engine reads KV from arena pages; pack with pages")
         self.write_kv(k3, v3, meta)
-        layer = meta["layer"]
+        out = self._paged(q3, meta["unified"], meta["layer"], softmax_scale, output)
+        meta["layer"] += 1
+        return out
+
+    def attention_final(self, q, k, v, chunk, rows):
+        """The last layer's attention: write the pack's KV (every row: later
+        packs may borrow it), then attend only for `rows` (the pass's final
+        rows) through meta["final_query"], one query per row seeing exactly
+        the keys it sees inside its own sequence. Returns the o_proj input of
+        those rows, bit-identical to theirs in the full call."""
+        n = q.shape[0]
+        hq, hk, d = self.num_q_heads, self.num_kv_heads, self.head_dim
+        meta = chunk.meta
+        fq = meta.get("final_query")
+        if fq is None or meta["unified"] is None:
+            raise ValueError("the pack carries no final-row attention metadata")
+        k3 = k.view(n, hk, d)
+        v3 = v.view(n, hk, d) if v.is_contiguous() else v
+        self.write_kv(k3, v3, meta)
+        qf = q.view(n, hq, d).index_select(0, rows)
+        out = self._paged(qf, fq, meta["layer"], None, None)
+        meta["layer"] += 1
+        return out
+
+    def _paged(self, q3, tables, layer, softmax_scale, output):
+        """One paged causal call over `tables` (cu_q, used, table, max_q,
+        max_used) with the o_proj input quantization fused."""
+        n = q3.shape[0]
+        hq, hk, d = self.num_q_heads, self.num_kv_heads, self.head_dim
         k_pool, v_pool = self.arena.layer_kv(layer)
         scale = d ** -0.5 if softmax_scale is None else softmax_scale
-        table = unified["table"]
+        table = tables["table"]
         if output is not None:
             o_q, o_s = output
         else:
             o_q = torch.empty((n, hq * d), dtype=self.fp8, device=q3.device)
             o_s = self._col_major_scales(n, hq * d, q3.device)
-        seqs = unified["used"].shape[0]
+        seqs = tables["used"].shape[0]
         q_ld = q3.stride(0)
+        args = (_ptr(k_pool), _ptr(v_pool), _ptr(tables["cu_q"]), _ptr(tables["used"]),
+                _ptr(table), table.stride(0), seqs, int(tables["max_q"]),
+                int(tables["max_used"]), hq, hk, d, self.arena.page_tokens, float(scale),
+                int(tables.get("causal", True)))
         if d == GROUP:
-            _lib.call("qx_paged_attention", _ptr(q3), q_ld, _ptr(k_pool), _ptr(v_pool),
-                      _ptr(unified["cu_q"]), _ptr(unified["used"]), _ptr(table),
-                      table.stride(0), seqs, int(unified["max_q"]), int(unified["max_used"]), hq, hk, d,
-                      self.arena.page_tokens, float(scale), int(unified.get("causal", True)),
-                      None, _ptr(o_q), o_q.stride(0), _ptr(o_s), self._scale_ld(o_s), _stream())
+            _lib.call("qx_paged_attention", _ptr(q3), q_ld, *args, None, _ptr(o_q),
+                      o_q.stride(0), _ptr(o_s), self._scale_ld(o_s), _stream())
         else:
             # a 128-column FP8 group spans several heads: bf16 out, then quant
             o = torch.empty((n, hq * d), dtype=torch.bfloat16, device=q3.device)
-            _lib.call("qx_paged_attention", _ptr(q3), q_ld, _ptr(k_pool), _ptr(v_pool),
-                      _ptr(unified["cu_q"]), _ptr(unified["used"]), _ptr(table),
-                      table.stride(0), seqs, int(unified["max_q"]), int(unified["max_used"]), hq, hk, d,
-                      self.arena.page_tokens, float(scale), int(unified.get("causal", True)),
-                      _ptr(o), None, o.stride(0), None, 0, _stream())
+            _lib.call("qx_paged_attention", _ptr(q3), q_ld, *args, _ptr(o), None, o.stride(0),
+                      None, 0, _stream())
             self.quant(o, output=(o_q, o_s))
-        meta["layer"] += 1
         return o_q, o_s
 
     def attention_bf16(self, q3, meta, layer):

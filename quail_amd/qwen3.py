@@ -98,12 +98,23 @@ class Qwen3Pipeline:
         q_in, q_scale, residual = engine.embed_norm_quant(
             chunk.input_ids, self.embed.weight, first.input_layernorm)
         hidden = None
+        last = len(self.layers) - 1
+        final = chunk.final_indices
         for index, layer in enumerate(self.layers):
             if index == 0:
                 q, k, v = self._project_qkv(q_in, q_scale, chunk.positions, layer.self_attn)
             else:
                 q, k, v, residual = self.before_attention(hidden, residual, chunk.positions,
                                                           layer)
+            if index == last and chunk.meta.get("final_query") is not None:
+                # past the last layer's KV only the final rows matter: their
+                # attention, o_proj and MLP run alone, bit-identical to what
+                # they are in the full pass (every kernel is row-local)
+                o_in, o_scale = engine.attention_final(q, k, v, chunk, final)
+                residual = residual.index_select(0, final)
+                hidden = self.after_attention(o_in, o_scale, residual, layer)
+                normed, _ = engine.fused_add_rms_norm(hidden, residual, self.final_norm)
+                return normed
             o_in, o_scale = engine.attention(q, k, v, chunk)
             hidden = self.after_attention(o_in, o_scale, residual, layer)
-        return engine.final_norm(hidden, residual, chunk.final_indices, self.final_norm)
+        return engine.final_norm(hidden, residual, final, self.final_norm)

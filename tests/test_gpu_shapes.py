@@ -74,3 +74,33 @@ def test_score_is_sigmoid_of_if_margin():
     got = np.asarray(scores, dtype=np.float64).reshape(-1)
     # the score uses fp32 logits, the margins bf16-rounded ones (readout.py:44-48)
     np.testing.assert_allclose(got, want, atol=2e-2)
+
+
+def test_last_layer_on_final_rows_only_is_bit_identical():
+    """The last layer attends, projects and runs its MLP for the final rows
+    only (chunk.meta["final_query"]); without that metadata the pipeline
+    runs it for every row. The final rows must not change."""
+    from quail_amd.arena import KVArena
+    from quail_amd.admission import StageAdmission
+    from quail_amd.chunk import InputStaging, pack_chunk, upload
+    from quail_amd.prefix import PrefixIndex
+    from quail_amd.qwen3 import Qwen3Pipeline
+
+    wl = make_workload("qwen3-8b", seed=5, documents=5)
+    cfg = CONFIGS[wl.model]
+    model = build_synthetic(cfg, seed=5, device="cuda", layers=LAYERS)
+    outs = []
+    for pruned in (True, False):
+        arena = KVArena(LAYERS, 3 * wl.chunk_budget // 16 + 64, 16, cfg.kv_heads, cfg.head_dim)
+        prefixes, suffixes = wl.groups_input()
+        tree = PrefixIndex(wl.prompts).tree(16)
+        adm = StageAdmission(prefixes, suffixes, arena, wl.chunk_budget, tree=tree)
+        groups = adm.next_chunk()
+        assert adm.done()
+        chunk = pack_chunk(arena, [g for _, g in groups])
+        upload(chunk, InputStaging())
+        if not pruned:
+            chunk.meta["final_query"] = None
+        outs.append(Qwen3Pipeline(model, arena).forward_chunk(chunk).clone())
+    assert outs[0].shape == (wl.documents, cfg.hidden)
+    assert torch.equal(outs[0], outs[1])
