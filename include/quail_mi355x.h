@@ -154,7 +154,21 @@ int qx_paged_attention(const void* q, int64_t q_ld, const void* k_pool, const vo
                        int64_t seqs, int64_t max_q, int64_t max_used, int64_t HQ, int64_t HK,
                        int64_t D, int64_t page, float scale, int causal, void* out_bf16,
                        void* out_fp8, int64_t o_ld, float* scales, int64_t s_ld,
-                       hipStream_t stream);
+                       const int* work, int64_t n_work, hipStream_t stream);
+
+/*
+ * Host function: the work list for qx_paged_attention's `work` argument
+ * (device copy of it, n_work = the return value): one (sequence, query tile)
+ * int pair per query tile that holds rows, in the tile size the call uses for
+ * (HQ / HK, D), heaviest first (most keys to read). With work == NULL the
+ * call launches its full (max_q tiles x seqs) grid instead, whose tiles past
+ * a sequence's rows exit at once. cu_q and used are host copies. Returns the
+ * item count (<= capacity) or -1. No reference counterpart: FlashAttention's
+ * varlen grid is the full one.
+ */
+int64_t qx_paged_attention_work(const int* cu_q, const int* used, int64_t seqs, int64_t HQ,
+                                int64_t HK, int64_t D, int causal, int* work,
+                                int64_t capacity);
 
 /*
  * Last-token answer head over the retained head rows (t <= 16):

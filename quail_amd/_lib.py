@@ -38,11 +38,16 @@ SIGNATURES = {
     "qx_kv_scatter": [_p, _i64, _p, _i64, _p, _p, _p, _p, _i64, _i64, _i32, _p],
     "qx_embed": [_p, _i64, _p, _p, _i64, _i64, _i64, _p],
     "qx_paged_attention": [_p, _i64, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64,
-                           _i64, _i64, _f32, _i32, _p, _p, _i64, _p, _i64, _p],
+                           _i64, _i64, _f32, _i32, _p, _p, _i64, _p, _i64, _p, _i64, _p],
+    "qx_paged_attention_work": [_p, _p, _i64, _i64, _i64, _i64, _i32, _p, _i64],
     "qx_prefix_tree": [_p, _p, _i64, _i64, _p, _p, _p],
     "qx_answer_head": [_p, _i64, _p, _i64, _i64, _i64, _i64, _i32, _p, _f32, _p, _p, _p, _p,
                        _p],
 }
+
+
+# entry points returning a count (>= 0) or -1 instead of a status
+RETURNS_COUNT = {"qx_paged_attention_work"}
 
 
 class QxUnavailable(RuntimeError):
@@ -71,7 +76,8 @@ def load(path: Path = LIB_PATH):
     for name, argtypes in SIGNATURES.items():
         fn = getattr(lib, name)
         fn.argtypes = argtypes
-        fn.restype = ctypes.c_char_p if name == "qx_last_error" else ctypes.c_int
+        fn.restype = (ctypes.c_char_p if name == "qx_last_error" else
+                      ctypes.c_int64 if name in RETURNS_COUNT else ctypes.c_int)
     _LIB = lib
     return lib
 
@@ -86,6 +92,15 @@ def call(name: str, *args) -> None:
         else:
             msg = f"hipError_t {rc}"
         raise QxError(f"{name}: {msg}")
+
+
+def count(name: str, *args) -> int:
+    """Call an entry point that returns a count; raise QxError on -1."""
+    lib = load()
+    n = getattr(lib, name)(*args)
+    if n < 0:
+        raise QxError(f"{name}: {lib.qx_last_error().decode(errors='replace')}")
+    return int(n)
 
 
 def declared_symbols(header: Path = HEADER) -> list:

@@ -69,8 +69,13 @@ def _cat(parts, dtype=np.int64):
     return np.concatenate(parts) if parts else np.empty(0, dtype=dtype)
 
 
-def pack_chunk(arena, groups, *, attention_mode="unified", mask="causal", timing=None):
+def pack_chunk(arena, groups, *, attention_mode="unified", mask="causal", timing=None,
+               attention_heads=None):
     """Pack groups for one unified causal forward pass (host arrays only).
+
+    attention_heads: (HQ, HK, D) of the model; with it the attention
+    metadata also carries the work list of the paged calls (one item per
+    query tile that holds rows, heaviest first, qx_paged_attention_work).
 
     Raises ValueError for layouts this path does not run and ArenaFullError
     when the suffixes' temporary pages do not fit (temporaries allocated so
@@ -205,6 +210,10 @@ def pack_chunk(arena, groups, *, attention_mode="unified", mask="causal", timing
     meta = dict(layer=0, unified=unified, cu_a=cu_a_arr,
                 max_a=int(np.diff(cu_a_arr).max()) if len(cu_a) > 1 else 0,
                 final_query=_final_query(cu_q_arr, used, table, final))
+    if attention_heads is not None:
+        for tables in (unified, meta["final_query"]):
+            if tables is not None:
+                tables["work"], tables["n_work"] = _work_list(tables, attention_heads)
     if timing is not None:
         timing["pack_py"] = timing.get("pack_py", 0.0) + (t1 - t0)
         timing["pack_unified"] = timing.get("pack_unified", 0.0) + (time.perf_counter() - t1)
@@ -214,6 +223,20 @@ def pack_chunk(arena, groups, *, attention_mode="unified", mask="causal", timing
                  fresh_keys=tuple(fresh_keys),
                  rows_per_answer=np.concatenate(rows_per_answer) if multi else None,
                  host_ids=ids, host_positions=positions)
+
+
+def _work_list(tables, heads):
+    """(work pairs, count) of a paged call over `tables` (host arrays)."""
+    from quail_amd import _lib
+    hq, hk, d = heads
+    cu_q = np.ascontiguousarray(tables["cu_q"], dtype=np.int32)
+    used = np.ascontiguousarray(tables["used"], dtype=np.int32)
+    seqs = len(used)
+    cap = int(cu_q[-1]) + seqs if seqs else 1
+    work = np.zeros(2 * max(cap, 1), dtype=np.int32)
+    n = _lib.count("qx_paged_attention_work", cu_q.ctypes.data, used.ctypes.data, seqs, hq, hk,
+                   d, int(tables.get("causal", True)), work.ctypes.data, cap)
+    return work[:2 * n], n
 
 
 def _final_query(cu_q, used, table, final):
@@ -290,6 +313,8 @@ def upload(chunk: Chunk, staging: InputStaging) -> Chunk:
     dev["table"] = staging.copy("block_table", u["table"], torch.int32)
     chunk.host["unified"] = u
     chunk.meta["unified"] = dev
+    if u.get("work") is not None and u["n_work"]:
+        dev["work"] = staging.copy("unified_work", u["work"], torch.int32)
     fq = chunk.meta.get("final_query")
     if fq is not None:
         chunk.host["final_query"] = fq
@@ -297,5 +322,8 @@ def upload(chunk: Chunk, staging: InputStaging) -> Chunk:
             fq, cu_q=staging.copy("final_cu_q", fq["cu_q"], torch.int32),
             used=staging.copy("final_used", fq["used"], torch.int32),
             table=staging.copy("final_table", fq["table"], torch.int32))
+        if fq.get("work") is not None and fq["n_work"]:
+            chunk.meta["final_query"]["work"] = staging.copy("final_work", fq["work"],
+                                                             torch.int32)
     chunk.meta["cu_a"] = staging.copy("cu_a", chunk.meta["cu_a"], torch.int32)
     return chunk

@@ -34,6 +34,9 @@
 // fp16: P in (0, 1] keeps 11 significant bits (bf16 would keep 8), and the V
 // pool holds fp16 (qx_kv_scatter converts bf16 V rows once, exactly for |v|
 // in [2^-14, 65504]).
+#include <algorithm>
+#include <vector>
+
 #include "qx_common.h"
 #include "qx_status.h"
 
@@ -65,7 +68,8 @@ __global__ __launch_bounds__(HPB * QSUB * 64) void paged_attention_kernel(
     const uint16_t* __restrict__ vp, const int* __restrict__ cu_q, const int* __restrict__ used,
     const int* __restrict__ table, int64_t table_ld, int max_used, int HQ, int HK,
     float scale_log2, int causal, uint16_t* __restrict__ out16, uint8_t* __restrict__ out8,
-    int64_t o_ld, float* __restrict__ scales, int64_t s_ld) {
+    int64_t o_ld, float* __restrict__ scales, int64_t s_ld, const int* __restrict__ work,
+    int zgroups, int seqs) {
   constexpr int NW = HPB * QSUB;
   constexpr int NT = NW * 64;
   constexpr int BQ = 32 * QSUB;  // query rows per workgroup
@@ -84,18 +88,31 @@ __global__ __launch_bounds__(HPB * QSUB * 64) void paged_attention_kernel(
   auto v_buf = [&](int b) -> uint8_t* { return &kv_lds[b][1][0]; };
   __shared__ int pages_lds[kMaxPages];
 
-  const int s = blockIdx.y;
-  const int qt = gridDim.x - 1 - blockIdx.x;  // heavy (late) tiles first
+  // the workgroup's (sequence, query tile, head group): from the work list
+  // (one item per real query tile, heaviest first, head groups innermost),
+  // or from the full grid (late query tiles first)
+  int s, qt, zg;
+  if (work) {
+    const int item = blockIdx.x / zgroups;
+    zg = blockIdx.x % zgroups;
+    s = work[2 * item];
+    qt = work[2 * item + 1];
+    if (s < 0 || s >= seqs || qt < 0) return;  // not an item of this call
+  } else {
+    s = blockIdx.y;
+    qt = gridDim.x - 1 - blockIdx.x;
+    zg = blockIdx.z;
+  }
   const int q0 = cu_q[s];
   const int q_len = cu_q[s + 1] - q0;
   if (qt * BQ >= q_len) return;  // uniform over the workgroup
   const int G = HQ / HK;
   const int groups_per_kv = G / HPB;
-  const int kvh = blockIdx.z / groups_per_kv;
+  const int kvh = zg / groups_per_kv;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int head = kvh * G + (blockIdx.z % groups_per_kv) * HPB + (wave % HPB);
+  const int head = kvh * G + (zg % groups_per_kv) * HPB + (wave % HPB);
   const int qsub = wave / HPB;
   const int half = lane >> 5;
   const int col = lane & 31;
@@ -355,23 +372,36 @@ template <int D, int HPB, int QSUB>
 int launch_attn(const void* q, int64_t q_ld, const void* kp, const void* vp, const int* cu_q,
                 const int* used, const int* table, int64_t table_ld, int seqs, int max_q,
                 int max_used, int HQ, int HK, int page, float scale, int causal, void* out16,
-                void* out8, int64_t o_ld, float* scales, int64_t s_ld, hipStream_t stream) {
+                void* out8, int64_t o_ld, float* scales, int64_t s_ld, const int* work,
+                int n_work, hipStream_t stream) {
   const int G = HQ / HK;
   constexpr int BQ = 32 * QSUB;
-  dim3 grid((max_q + BQ - 1) / BQ, seqs, HK * (G / HPB));
+  const int zgroups = HK * (G / HPB);
+  dim3 grid = work ? dim3((unsigned)n_work * zgroups, 1, 1)
+                   : dim3((max_q + BQ - 1) / BQ, seqs, zgroups);
   const float scale_log2 = scale * 1.4426950408889634f;
   if (out8) {
     hipLaunchKernelGGL((paged_attention_kernel<D, HPB, QSUB, true>), grid, dim3(HPB * QSUB * 64),
                        0, stream, (const uint16_t*)q, q_ld, (const uint16_t*)kp,
                        (const uint16_t*)vp, cu_q, used, table, table_ld, max_used, HQ, HK,
-                       scale_log2, causal, nullptr, (uint8_t*)out8, o_ld, scales, s_ld);
+                       scale_log2, causal, nullptr, (uint8_t*)out8, o_ld, scales, s_ld, work,
+                       zgroups, seqs);
   } else {
     hipLaunchKernelGGL((paged_attention_kernel<D, HPB, QSUB, false>), grid, dim3(HPB * QSUB * 64),
                        0, stream, (const uint16_t*)q, q_ld, (const uint16_t*)kp,
                        (const uint16_t*)vp, cu_q, used, table, table_ld, max_used, HQ, HK,
-                       scale_log2, causal, (uint16_t*)out16, nullptr, o_ld, nullptr, 0);
+                       scale_log2, causal, (uint16_t*)out16, nullptr, o_ld, nullptr, 0, work,
+                       zgroups, seqs);
   }
   QX_LAUNCH_STATUS();
+}
+
+// Query rows per workgroup of the configuration dispatched for (D, G):
+// 32 * QSUB with HPB * QSUB = 8 waves.
+inline int attn_query_tile(int64_t D, int64_t G) {
+  (void)D;
+  const int hpb = G % 4 == 0 ? 4 : (G % 2 == 0 ? 2 : 1);
+  return 32 * (8 / hpb);
 }
 
 }  // namespace
@@ -388,7 +418,7 @@ int qx_paged_attention(const void* q, int64_t q_ld, const void* k_pool, const vo
                        int64_t seqs, int64_t max_q, int64_t max_used, int64_t HQ, int64_t HK,
                        int64_t D, int64_t page, float scale, int causal, void* out_bf16,
                        void* out_fp8, int64_t o_ld, float* scales, int64_t s_ld,
-                       hipStream_t stream) {
+                       const int* work, int64_t n_work, hipStream_t stream) {
   QX_CHECK(q && k_pool && v_pool && cu_q && used && table, "attention: null pointer");
   QX_CHECK(out_bf16 || out_fp8, "attention: no output");
   QX_CHECK(D == 64 || D == 128, "attention: head_dim %lld", (long long)D);
@@ -400,7 +430,8 @@ int qx_paged_attention(const void* q, int64_t q_ld, const void* k_pool, const vo
   QX_CHECK(q_ld % 8 == 0 && o_ld % 4 == 0, "attention: strides");
   QX_CHECK(!out_fp8 || (D == 128 && scales), "attention: fused quant needs D=128 and scales");
   QX_CHECK(seqs < 65536, "attention: %lld sequences exceed the grid", (long long)seqs);
-  if (seqs == 0 || max_q == 0) return QX_OK;
+  QX_CHECK(!work || (n_work >= 0 && n_work * HK * 8 < (1LL << 31)), "attention: work items");
+  if (seqs == 0 || max_q == 0 || (work && n_work == 0)) return QX_OK;
   const int G = (int)(HQ / HK);
   const int hpb = G % 4 == 0 ? 4 : (G % 2 == 0 ? 2 : 1);
   const int args_seqs = (int)seqs, args_mq = (int)max_q, args_mu = (int)max_used;
@@ -408,7 +439,7 @@ int qx_paged_attention(const void* q, int64_t q_ld, const void* k_pool, const vo
   return qx::launch_attn<DD, HPB_, QS_>(q, q_ld, k_pool, v_pool, cu_q, used, table, table_ld,   \
                                         args_seqs, args_mq, args_mu, (int)HQ, (int)HK,          \
                                         (int)page, scale, causal, out_bf16, out_fp8, o_ld,      \
-                                        scales, s_ld, stream)
+                                        scales, s_ld, work, (int)n_work, stream)
   if (D == 128) {
     if (hpb == 4) QX_ATTN(128, 4, 2);
     if (hpb == 2) QX_ATTN(128, 2, 4);
@@ -419,6 +450,43 @@ int qx_paged_attention(const void* q, int64_t q_ld, const void* k_pool, const vo
     QX_ATTN(64, 1, 8);
   }
 #undef QX_ATTN
+}
+
+// Host function: the work list of a paged call, one (sequence, query tile)
+// item per query tile holding rows, in the tile size the call dispatches
+// for (HQ / HK, D), heaviest first (most keys to read; ties in sequence and
+// tile order). Returns the number of items (<= capacity) or -1.
+int64_t qx_paged_attention_work(const int* cu_q, const int* used, int64_t seqs, int64_t HQ,
+                                int64_t HK, int64_t D, int causal, int* work,
+                                int64_t capacity) {
+  if (!(cu_q && used && work && seqs >= 0 && HQ > 0 && HK > 0 && HQ % HK == 0)) {
+    qx::set_error("attention_work: arguments");
+    return QX_EINVAL;
+  }
+  const int bq = qx::attn_query_tile(D, HQ / HK);
+  struct Item { int64_t load; int s, qt; };
+  std::vector<Item> items;
+  for (int64_t s = 0; s < seqs; ++s) {
+    const int q_len = cu_q[s + 1] - cu_q[s];
+    const int u = used[s];
+    for (int qt = 0; qt * bq < q_len; ++qt) {
+      const int last = std::min(qt * bq + bq, q_len) - 1;
+      const int keys = causal ? std::min(u, u - q_len + last + 1) : u;
+      items.push_back({(int64_t)keys, (int)s, qt});
+    }
+  }
+  if ((int64_t)items.size() > capacity) {
+    qx::set_error("attention_work: %zu items exceed the capacity %lld", items.size(),
+                  (long long)capacity);
+    return QX_EINVAL;
+  }
+  std::stable_sort(items.begin(), items.end(),
+                   [](const Item& a, const Item& b) { return a.load > b.load; });
+  for (size_t i = 0; i < items.size(); ++i) {
+    work[2 * i] = items[i].s;
+    work[2 * i + 1] = items[i].qt;
+  }
+  return (int64_t)items.size();
 }
 
 }  // extern "C"

@@ -67,7 +67,10 @@ class StageRun:
                     continue
                 raise ArenaFullError("no document fits the free KV arena")
             t = time.perf_counter()
-            chunk = pack_chunk(self.arena, [g for _, g in groups])
+            engine = self.pipeline.engine
+            chunk = pack_chunk(self.arena, [g for _, g in groups],
+                               attention_heads=(engine.num_q_heads, engine.num_kv_heads,
+                                                engine.head_dim))
             upload(chunk, self.staging)
             self.stats["pack_s"] += time.perf_counter() - t
             self.stats["chunks"] += 1

@@ -28,7 +28,27 @@ def test_argument_errors_return_minus_one_with_a_message():
                   None)
     with pytest.raises(_lib.QxError, match="head_dim"):
         _lib.call("qx_paged_attention", 16, 8, 16, 16, 16, 16, 16, 1, 1, 1, 64, 4, 2, 96, 16,
-                  0.1, 1, 16, None, 8, None, 0, None)
+                  0.1, 1, 16, None, 8, None, 0, None, 0, None)
     with pytest.raises(_lib.QxError, match="1..16"):
         _lib.call("qx_answer_head", 16, 8, 16, 8, 17, 1, 8, 0, None, 1.0, None, None, None,
                   None, None)
+
+
+def test_attention_work_list_is_heaviest_first_and_covers_every_tile():
+    import numpy as np
+    # 3 sequences of 100, 1, 200 query rows over 150, 40, 260 keys (causal)
+    cu_q = np.array([0, 100, 101, 301], dtype=np.int32)
+    used = np.array([150, 40, 260], dtype=np.int32)
+    work = np.zeros(2 * 16, dtype=np.int32)
+    n = _lib.count("qx_paged_attention_work", cu_q.ctypes.data, used.ctypes.data, 3, 32, 8,
+                   128, 1, work.ctypes.data, 16)
+    items = [tuple(work[2 * i:2 * i + 2]) for i in range(n)]
+    # query tiles of 64 rows (G = 4): 2 + 1 + 4 of them
+    assert sorted(items) == [(0, 0), (0, 1), (1, 0), (2, 0), (2, 1), (2, 2), (2, 3)]
+    keys = {(0, 0): 114, (0, 1): 150, (1, 0): 40, (2, 0): 124, (2, 1): 188, (2, 2): 252,
+            (2, 3): 260}
+    loads = [keys[it] for it in items]
+    assert loads == sorted(loads, reverse=True)
+    with pytest.raises(_lib.QxError, match="capacity"):
+        _lib.count("qx_paged_attention_work", cu_q.ctypes.data, used.ctypes.data, 3, 32, 8,
+                   128, 1, work.ctypes.data, 3)
