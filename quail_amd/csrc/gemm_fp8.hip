@@ -771,6 +771,14 @@ int qx_gemm_fp8_blockscaled(const void* A, const float* sA, const void* W, const
     case 12:
       return qx::launch128<128, 128, 2, 2, 2>(A, sA, W, sW, C, m, n, k, lda, ldc, sa_ld, 8,
                                               stream);
+    case 14:
+      QX_CHECK(n % 256 == 0, "gemm config 14 needs N %% 256 == 0 (N=%d)", n);
+      return qx::launch128<128, 256, 2, 4, 2>(A, sA, W, sW, C, m, n, k, lda, ldc, sa_ld, 8,
+                                              stream);
+    case 15:
+      QX_CHECK(n % 256 == 0, "gemm config 15 needs N %% 256 == 0 (N=%d)", n);
+      return qx::launch128<128, 256, 4, 2, 2>(A, sA, W, sW, C, m, n, k, lda, ldc, sa_ld, 8,
+                                              stream);
     case 13:
       QX_CHECK(n % 256 == 0, "gemm config 13 needs N %% 256 == 0 (N=%d)", n);
       return qx::launch128<256, 256, 2, 4, 2, true>(A, sA, W, sW, C, m, n, k, lda, ldc, sa_ld,

@@ -24,14 +24,18 @@ from quail_amd import _lib
 
 GROUP = 128
 
-# GEMM tile configurations (see csrc/gemm_fp8.hip), measured on the Qwen3-4B
-# projection shapes at 8k-16k tokens: 10 = 256 tokens x 256 weights, 8 waves,
-# two 128-byte K stages (128 KiB LDS) is fastest where N >= 4096 or K >= 8192
-# (qkv, gate_up, down); 5 = 256 x 128, 4 waves, two 64-byte K stages (48 KiB,
-# two workgroups per CU) wins on the narrow o_proj. QUAIL_GEMM_CONFIG forces one.
+# GEMM tile configurations (see csrc/gemm_fp8.hip); every one computes each
+# output element with the same operations in the same order, so the choice
+# never changes a result bit. 10 = 256 tokens x 256 weights, 8 waves, two
+# 128-byte K stages (128 KiB LDS) is fastest on all four Qwen3-4B
+# projections inside the prefill pass at ~16k tokens (128 x 256 tiles,
+# config 14, fill the 2.5 waves of the narrow projections better in
+# isolation but measured slower in the pass); 5 = 256 x 128, 4 waves,
+# 64-byte stages, takes widths that are not multiples of 256.
+# QUAIL_GEMM_CONFIG forces one.
 GEMM_CONFIG_ENV = "QUAIL_GEMM_CONFIG"
-GEMM_DEFAULT_CONFIG = 5
-GEMM_WIDE_CONFIG = 10
+GEMM_DEFAULT_CONFIG = 10
+GEMM_ODD_WIDTH_CONFIG = 5
 
 
 def _ptr(t):
@@ -46,8 +50,8 @@ def gemm_config(n: int, k: int, m: int) -> int:
     forced = os.environ.get(GEMM_CONFIG_ENV)
     if forced is not None:
         return int(forced)
-    if n % 256 == 0 and (n >= 4096 or k >= 8192):
-        return GEMM_WIDE_CONFIG
+    if n % 256:
+        return GEMM_ODD_WIDTH_CONFIG
     return GEMM_DEFAULT_CONFIG
 
 

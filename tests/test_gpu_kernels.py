@@ -98,13 +98,26 @@ def test_gemm_small_shapes_match_dequantized_matmul(m, n, k):
     _bf16_close(out, want)
 
 
-@pytest.mark.parametrize("config", [0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13])
+@pytest.mark.parametrize("config", list(range(16)))
 def test_gemm_tile_configs_agree(config, monkeypatch):
     q, s, wq, ws = _gemm_case(300, 512, 512, seed=9)
     monkeypatch.setenv("QUAIL_GEMM_CONFIG", str(config))
     out = _run_gemm(q, s, wq, ws)
     want = ref.gemm(q, s, ref.RefLinear(wq, ws))
     _bf16_close(out, want)
+
+
+def test_gemm_configs_are_bit_identical(monkeypatch):
+    """Every tile configuration computes each element with the same
+    operations in the same order (the engine picks configs by shape, and a
+    row's result must not depend on it)."""
+    q, s, wq, ws = _gemm_case(700, 1024, 1024, seed=11)
+    outs = []
+    for config in range(16):
+        monkeypatch.setenv("QUAIL_GEMM_CONFIG", str(config))
+        outs.append(_run_gemm(q, s, wq, ws).cpu())
+    for config, out in enumerate(outs):
+        assert torch.equal(out, outs[0]), config
 
 
 @pytest.mark.parametrize("k,n", [(2560, 6144), (4096, 2560), (2560, 19456), (9728, 2560)])
