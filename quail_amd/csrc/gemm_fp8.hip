@@ -659,21 +659,58 @@ __global__ __launch_bounds__(64 * WAVES_N * WAVES_M) void gemm_fp8_k128_kernel(
     }
   }
 
+  // Epilogue through LDS. A lane's accumulators are one token's values at
+  // 4 runs of 4 columns, so storing them directly makes every store
+  // instruction touch 32 rows of C (8 bytes each); the bf16 tile is staged
+  // in LDS instead (rows = tokens, 16-byte chunks swizzled by the row) and
+  // written back one whole tile row per BN/8 lanes, 16 bytes per lane.
+  // The stores are non-temporal: C is not read again by this launch, and
+  // keeping it out of L2 leaves L2 to the operand rows other workgroups
+  // are about to read (measured 1-8% faster per Qwen3-4B shape).
+  constexpr int kRowBytes = BN * 2;
+  constexpr int kChunks = BN / 8;
+  constexpr int kSwz = (kChunks < 16 ? kChunks : 16) - 1;
+  static_assert(BM * kRowBytes <= Cfg::kLds, "epilogue tile fits the stage buffers");
+  static_assert(64 % kChunks == 0 && BM % Cfg::kWaves == 0 &&
+                    (BM / Cfg::kWaves) % (64 / kChunks) == 0,
+                "epilogue rows");
+  __syncthreads();  // every wave is done with the last stage's operands
 #pragma unroll
   for (int b = 0; b < TM; ++b) {
-    const int m = m0 + wm * TM * 32 + b * 32 + (lane & 31);
-    if (m >= M) continue;
+    const int row = wm * TM * 32 + b * 32 + (lane & 31);
     const float s = s_prev[b];
-    uint16_t* crow = C + (int64_t)m * ldc;
+    uint8_t* lrow = smem + row * kRowBytes;
 #pragma unroll
     for (int a = 0; a < TN; ++a) {
-      const int nbase = n0 + wn * TN * 32 + a * 32 + (lane >> 5) * 4;
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
+        const int off = (wn * TN * 32 + a * 32 + (lane >> 5) * 4 + g * 8) * 2;
         uint2 v;
         v.x = pack2_bf16(acc[a][b][g * 4 + 0] * s, acc[a][b][g * 4 + 1] * s);
         v.y = pack2_bf16(acc[a][b][g * 4 + 2] * s, acc[a][b][g * 4 + 3] * s);
-        *reinterpret_cast<uint2*>(crow + nbase + g * 8) = v;
+        *reinterpret_cast<uint2*>(lrow + ((((off >> 4) ^ (row & kSwz)) << 4) | (off & 15))) = v;
+      }
+    }
+  }
+  __syncthreads();
+  constexpr int kRowsPerOp = 64 / kChunks;
+  constexpr int kRowsPerWave = BM / Cfg::kWaves;
+  const bool wide = ((ldc & 7) == 0) && ((reinterpret_cast<uintptr_t>(C) & 15) == 0);
+  const int c = lane % kChunks;
+#pragma unroll
+  for (int i = 0; i < kRowsPerWave / kRowsPerOp; ++i) {
+    const int row = wave * kRowsPerWave + i * kRowsPerOp + lane / kChunks;
+    const int m = m0 + row;
+    const uint4 v =
+        *reinterpret_cast<const uint4*>(smem + row * kRowBytes + ((c ^ (row & kSwz)) << 4));
+    if (m < M) {
+      uint16_t* dst = C + (int64_t)m * ldc + n0 + c * 8;
+      if (wide) {
+        const v4i w = {(int)v.x, (int)v.y, (int)v.z, (int)v.w};
+        __builtin_nontemporal_store(w, reinterpret_cast<v4i*>(dst));
+      } else {
+        reinterpret_cast<uint2*>(dst)[0] = make_uint2(v.x, v.y);
+        reinterpret_cast<uint2*>(dst)[1] = make_uint2(v.z, v.w);
       }
     }
   }
