@@ -662,14 +662,14 @@ __global__ __launch_bounds__(64 * WAVES_N * WAVES_M) void gemm_fp8_k128_kernel(
   // Epilogue through LDS. A lane's accumulators are one token's values at
   // 4 runs of 4 columns, so storing them directly makes every store
   // instruction touch 32 rows of C (8 bytes each); the bf16 tile is staged
-  // in LDS instead (rows = tokens, 16-byte chunks swizzled by the row) and
-  // written back one whole tile row per BN/8 lanes, 16 bytes per lane.
+  // in LDS instead (rows = tokens, each row padded by 16 bytes so the 32
+  // rows one write instruction touches spread over the banks) and written
+  // back one whole tile row per BN/8 lanes, 16 bytes per lane.
   // The stores are non-temporal: C is not read again by this launch, and
   // keeping it out of L2 leaves L2 to the operand rows other workgroups
   // are about to read (measured 1-8% faster per Qwen3-4B shape).
-  constexpr int kRowBytes = BN * 2;
+  constexpr int kRowBytes = BN * 2 + 16;
   constexpr int kChunks = BN / 8;
-  constexpr int kSwz = (kChunks < 16 ? kChunks : 16) - 1;
   static_assert(BM * kRowBytes <= Cfg::kLds, "epilogue tile fits the stage buffers");
   static_assert(64 % kChunks == 0 && BM % Cfg::kWaves == 0 &&
                     (BM / Cfg::kWaves) % (64 / kChunks) == 0,
@@ -688,7 +688,7 @@ __global__ __launch_bounds__(64 * WAVES_N * WAVES_M) void gemm_fp8_k128_kernel(
         uint2 v;
         v.x = pack2_bf16(acc[a][b][g * 4 + 0] * s, acc[a][b][g * 4 + 1] * s);
         v.y = pack2_bf16(acc[a][b][g * 4 + 2] * s, acc[a][b][g * 4 + 3] * s);
-        *reinterpret_cast<uint2*>(lrow + ((((off >> 4) ^ (row & kSwz)) << 4) | (off & 15))) = v;
+        *reinterpret_cast<uint2*>(lrow + off) = v;
       }
     }
   }
@@ -701,8 +701,7 @@ __global__ __launch_bounds__(64 * WAVES_N * WAVES_M) void gemm_fp8_k128_kernel(
   for (int i = 0; i < kRowsPerWave / kRowsPerOp; ++i) {
     const int row = wave * kRowsPerWave + i * kRowsPerOp + lane / kChunks;
     const int m = m0 + row;
-    const uint4 v =
-        *reinterpret_cast<const uint4*>(smem + row * kRowBytes + ((c ^ (row & kSwz)) << 4));
+    const uint4 v = *reinterpret_cast<const uint4*>(smem + row * kRowBytes + c * 16);
     if (m < M) {
       uint16_t* dst = C + (int64_t)m * ldc + n0 + c * 8;
       if (wide) {
@@ -728,6 +727,241 @@ int launch128(const void* A, const float* sA, const void* W, const float* sW, vo
                      dim3(Cfg::kThreads), 0, stream, (const uint8_t*)A, sA, (const uint8_t*)W, sW,
                      (uint16_t*)C, M, N, K, lda, ldc, sa_ld, tiles_m, tiles_n,
                      group_m < 1 ? 1 : group_m);
+  QX_LAUNCH_STATUS();
+}
+
+// ---- persistent variant -----------------------------------------------------
+// One workgroup per CU walks its XCD's band of tiles (the same bands and
+// group_m order as the one-tile-per-workgroup kernel). The pipeline runs over
+// the flattened (tile, 128-K block) sequence, so the next tile's first block
+// loads into the free stage while the current tile's last block computes and
+// its epilogue stores, where a fresh workgroup would start with an empty
+// pipeline. The epilogue stages C through the stage buffer it has just
+// consumed (its token scales included: they are read before the MFMAs), in
+// TM passes of WAVES_M * 32 rows. Each output element sums the
+// same products in the same order as the other configurations.
+template <int BM, int BN, int WAVES_N, int WAVES_M>
+__global__ __launch_bounds__(64 * WAVES_N * WAVES_M) void gemm_fp8_k128p_kernel(
+    const uint8_t* __restrict__ A, const float* __restrict__ sA, const uint8_t* __restrict__ W,
+    const float* __restrict__ sW, uint16_t* __restrict__ C, int M, int N, int K, int64_t lda,
+    int64_t ldc, int64_t sa_ld, int tiles_m, int tiles_n, int group_m) {
+  constexpr int STAGES = 2;
+  using Cfg = Cfg128<BM, BN, WAVES_N, WAVES_M, STAGES>;
+  constexpr int TN = Cfg::kTN, TM = Cfg::kTM;
+  constexpr int kRowBytes = BN * 2 + 16;  // padded: the 32 rows of one write spread over the banks
+  constexpr int kChunks = BN / 8;
+  constexpr int kPassRows = WAVES_M * 32;
+  constexpr int kRowsPerOp = 64 / kChunks;
+  constexpr int kRowsPerWave = kPassRows / Cfg::kWaves;
+  static_assert(kPassRows * kRowBytes <= Cfg::kStage, "epilogue pass fits a stage");
+  static_assert(64 % kChunks == 0 && kPassRows % Cfg::kWaves == 0 &&
+                    kRowsPerWave % kRowsPerOp == 0,
+                "epilogue rows");
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[Cfg::kLds];
+
+  const int total = tiles_m * tiles_n;
+  const int xcd = blockIdx.x & 7;
+  const int per_xcd = gridDim.x >> 3;  // the grid is a multiple of 8
+  const int local = blockIdx.x >> 3;
+  const int per = (total + 7) / 8;
+  const int full = total - (per - 1) * 8;
+  const int band0 = xcd < full ? xcd * per : full * per + (xcd - full) * (per - 1);
+  const int band = xcd < full ? per : per - 1;
+  const int my_tiles = local < band ? (band - local + per_xcd - 1) / per_xcd : 0;
+  const int KT = K >> 7;
+  const int steps = my_tiles * KT;
+  const int width = group_m * tiles_n;
+  auto origin = [&](int iter, int& m0_, int& n0_) {
+    const int id = band0 + local + iter * per_xcd;
+    const int first_m = (id / width) * group_m;
+    const int gsize = min(tiles_m - first_m, group_m);
+    m0_ = (first_m + (id % width) % gsize) * BM;
+    n0_ = ((id % width) / gsize) * BN;
+  };
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wn = wave % WAVES_N;
+  const int wm = wave / WAVES_N;
+
+  v16f acc[TN][TM];
+#pragma unroll
+  for (int a = 0; a < TN; ++a)
+#pragma unroll
+    for (int b = 0; b < TM; ++b)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[a][b][e] = 0.0f;
+  float s_prev[TM];
+#pragma unroll
+  for (int b = 0; b < TM; ++b) s_prev[b] = 0.0f;
+  float sw_ring[STAGES];
+
+  auto issue = [&](int m0_, int n0_, int kb, int stage) {
+    uint8_t* buf = smem + stage * Cfg::kStage;
+    const int64_t k_off = (int64_t)kb * 128;
+    load_slabs128<Cfg::kASlabs>(A, lda, m0_, M - 1, k_off, buf, wave * Cfg::kASlabs, lane);
+    load_slabs128<Cfg::kWSlabs>(W, K, n0_, N - 1, k_off, buf + Cfg::kABytes, wave * Cfg::kWSlabs,
+                                lane);
+    const int t = min(m0_ + wave * Cfg::kSaPerWave + lane % Cfg::kSaPerWave, M - 1);
+    __builtin_amdgcn_global_load_lds((const void*)(sA + (int64_t)kb * sa_ld + t),
+                                     (lds_void*)(buf + Cfg::kABytes + Cfg::kWBytes + wave * 256),
+                                     4, 0, 0);
+    sw_ring[stage] =
+        __builtin_nontemporal_load(sW + (int64_t)((n0_ + wn * TN * 32) >> 7) * KT + kb);
+  };
+
+  auto epilogue = [&](int m0_, int n0_, int stage) {
+    uint8_t* buf = smem + stage * Cfg::kStage;
+    const bool wide = ((ldc & 7) == 0) && ((reinterpret_cast<uintptr_t>(C) & 15) == 0);
+    const int c = lane % kChunks;
+#pragma unroll
+    for (int b = 0; b < TM; ++b) {
+      // b == 0: every wave is done with this stage's operands; b > 0: with
+      // the previous pass's rows
+      __syncthreads();
+      {
+        const int prow = wm * 32 + (lane & 31);
+        const float s = s_prev[b];
+        uint8_t* lrow = buf + prow * kRowBytes;
+#pragma unroll
+        for (int a = 0; a < TN; ++a) {
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            const int off = (wn * TN * 32 + a * 32 + (lane >> 5) * 4 + g * 8) * 2;
+            uint2 v;
+            v.x = pack2_bf16(acc[a][b][g * 4 + 0] * s, acc[a][b][g * 4 + 1] * s);
+            v.y = pack2_bf16(acc[a][b][g * 4 + 2] * s, acc[a][b][g * 4 + 3] * s);
+            *reinterpret_cast<uint2*>(lrow + off) = v;
+          }
+        }
+      }
+      __syncthreads();
+#pragma unroll
+      for (int i = 0; i < kRowsPerWave / kRowsPerOp; ++i) {
+        const int prow = wave * kRowsPerWave + i * kRowsPerOp + lane / kChunks;
+        const int m = m0_ + (prow >> 5) * TM * 32 + b * 32 + (prow & 31);
+        const uint4 v = *reinterpret_cast<const uint4*>(buf + prow * kRowBytes + c * 16);
+        if (m < M) {
+          uint16_t* dst = C + (int64_t)m * ldc + n0_ + c * 8;
+          if (wide) {
+            const v4i w = {(int)v.x, (int)v.y, (int)v.z, (int)v.w};
+            __builtin_nontemporal_store(w, reinterpret_cast<v4i*>(dst));
+          } else {
+            reinterpret_cast<uint2*>(dst)[0] = make_uint2(v.x, v.y);
+            reinterpret_cast<uint2*>(dst)[1] = make_uint2(v.z, v.w);
+          }
+        }
+      }
+    }
+  };
+
+  // the step being loaded (l_*) runs one ahead of the step being computed (c_*)
+  int l_iter = 0, l_kb = 0, lm0 = 0, ln0 = 0;
+  int c_iter = 0, c_kb = 0, cm0 = 0, cn0 = 0;
+  if (steps > 0) {
+    origin(0, lm0, ln0);
+    cm0 = lm0;
+    cn0 = ln0;
+    issue(lm0, ln0, 0, 0);
+    if (++l_kb == KT) {
+      l_kb = 0;
+      if (++l_iter < my_tiles) origin(l_iter, lm0, ln0);
+    }
+  }
+  for (int s0 = 0; s0 < steps; s0 += STAGES) {
+#pragma unroll
+    for (int stage = 0; stage < STAGES; ++stage) {
+      if (s0 + stage < steps) {
+        wait_vmcnt<0>();  // this step's operands (and any earlier stores) are done
+        lds_barrier();
+        if (s0 + stage + 1 < steps) {
+          issue(lm0, ln0, l_kb, stage ^ 1);
+          if (++l_kb == KT) {
+            l_kb = 0;
+            if (++l_iter < my_tiles) origin(l_iter, lm0, ln0);
+          }
+        }
+        const float sw =
+            __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(sw_ring[stage])));
+        if (sw != 0.0f) {  // wave-uniform; a zero weight-scale block adds nothing
+          const float* sa_lds = reinterpret_cast<const float*>(smem + stage * Cfg::kStage +
+                                                               Cfg::kABytes + Cfg::kWBytes);
+#pragma unroll
+          for (int b = 0; b < TM; ++b) {
+            const int row = wm * TM * 32 + b * 32 + (lane & 31);
+            const float s_cur = sa_lds[(row / Cfg::kSaPerWave) * 64 + row % Cfg::kSaPerWave] * sw;
+            const float r = s_prev[b] / s_cur;
+#pragma unroll
+            for (int a = 0; a < TN; ++a)
+#pragma unroll
+              for (int e = 0; e < 16; ++e) acc[a][b][e] *= r;
+            s_prev[b] = s_cur;
+          }
+          const uint8_t* a_lds = smem + stage * Cfg::kStage;
+          const uint8_t* w_lds = a_lds + Cfg::kABytes;
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            v8i wf[TN], af[TM];
+#pragma unroll
+            for (int a = 0; a < TN; ++a)
+              wf[a] = read_frag128(w_lds, wn * TN * 32 + a * 32 + (lane & 31), h, lane);
+#pragma unroll
+            for (int b = 0; b < TM; ++b)
+              af[b] = read_frag128(a_lds, wm * TM * 32 + b * 32 + (lane & 31), h, lane);
+#pragma unroll
+            for (int a = 0; a < TN; ++a)
+#pragma unroll
+              for (int b = 0; b < TM; ++b)
+                acc[a][b] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+                    wf[a], af[b], acc[a][b], 0, 0, 0, 0, 0, 0);
+          }
+        }
+        if (++c_kb == KT) {
+          epilogue(cm0, cn0, stage);
+          c_kb = 0;
+          if (++c_iter < my_tiles) origin(c_iter, cm0, cn0);
+#pragma unroll
+          for (int b = 0; b < TM; ++b) {
+            s_prev[b] = 0.0f;
+#pragma unroll
+            for (int a = 0; a < TN; ++a)
+#pragma unroll
+              for (int e = 0; e < 16; ++e) acc[a][b][e] = 0.0f;
+          }
+        }
+      }
+    }
+  }
+}
+
+// Workgroups of the persistent kernel: one per CU, a multiple of 8 (one
+// band per XCD); the CU count is read once per device.
+inline int persistent_grid(int total) {
+  static int cus[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (cus[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    cus[dev] = n;
+  }
+  return (total < cus[dev] ? total : cus[dev]) & ~7;
+}
+
+template <int BM, int BN, int WN, int WM>
+int launch128p(const void* A, const float* sA, const void* W, const float* sW, void* C, int M,
+               int N, int K, int64_t lda, int64_t ldc, int64_t sa_ld, int group_m,
+               hipStream_t stream) {
+  using Cfg = Cfg128<BM, BN, WN, WM, 2>;
+  const int tiles_m = (M + BM - 1) / BM;
+  const int tiles_n = N / BN;
+  const int grid = persistent_grid(tiles_m * tiles_n);
+  if (grid < 8)  // too few tiles to share out: one workgroup per tile
+    return launch128<BM, BN, WN, WM, 2>(A, sA, W, sW, C, M, N, K, lda, ldc, sa_ld, group_m,
+                                        stream);
+  hipLaunchKernelGGL((gemm_fp8_k128p_kernel<BM, BN, WN, WM>), dim3(grid), dim3(Cfg::kThreads), 0,
+                     stream, (const uint8_t*)A, sA, (const uint8_t*)W, sW, (uint16_t*)C, M, N, K,
+                     lda, ldc, sa_ld, tiles_m, tiles_n, group_m < 1 ? 1 : group_m);
   QX_LAUNCH_STATUS();
 }
 
@@ -820,6 +1054,11 @@ int qx_gemm_fp8_blockscaled(const void* A, const float* sA, const void* W, const
       QX_CHECK(n % 256 == 0, "gemm config 13 needs N %% 256 == 0 (N=%d)", n);
       return qx::launch128<256, 256, 2, 4, 2, true>(A, sA, W, sW, C, m, n, k, lda, ldc, sa_ld,
                                                     4, stream);
+    case 16:
+      QX_CHECK(n % 256 == 0, "gemm config 16 needs N %% 256 == 0 (N=%d)", n);
+      return qx::launch128p<256, 256, 2, 4>(A, sA, W, sW, C, m, n, k, lda, ldc, sa_ld, 4, stream);
+    case 17:
+      return qx::launch128p<256, 128, 1, 4>(A, sA, W, sW, C, m, n, k, lda, ldc, sa_ld, 8, stream);
     default:
       QX_CHECK(false, "gemm: unknown config %d", config);
   }

@@ -98,7 +98,7 @@ def test_gemm_small_shapes_match_dequantized_matmul(m, n, k):
     _bf16_close(out, want)
 
 
-@pytest.mark.parametrize("config", list(range(16)))
+@pytest.mark.parametrize("config", list(range(18)))
 def test_gemm_tile_configs_agree(config, monkeypatch):
     q, s, wq, ws = _gemm_case(300, 512, 512, seed=9)
     monkeypatch.setenv("QUAIL_GEMM_CONFIG", str(config))
@@ -113,11 +113,26 @@ def test_gemm_configs_are_bit_identical(monkeypatch):
     row's result must not depend on it)."""
     q, s, wq, ws = _gemm_case(700, 1024, 1024, seed=11)
     outs = []
-    for config in range(16):
+    for config in range(18):
         monkeypatch.setenv("QUAIL_GEMM_CONFIG", str(config))
         outs.append(_run_gemm(q, s, wq, ws).cpu())
     for config, out in enumerate(outs):
         assert torch.equal(out, outs[0]), config
+
+
+def test_gemm_persistent_configs_with_several_tiles_per_workgroup(monkeypatch):
+    """More tiles than CUs (9 x 16 tiles of 256x256, 9 x 32 of 256x128, a
+    partial last row of tiles): the persistent configurations (16, 17) walk
+    several tiles per workgroup and must equal the one-tile-per-workgroup
+    configuration bit for bit, and the oracle to the bf16 tolerance."""
+    q, s, wq, ws = _gemm_case(2125, 4096, 384, seed=13)
+    outs = {}
+    for config in (10, 5, 16, 17):
+        monkeypatch.setenv("QUAIL_GEMM_CONFIG", str(config))
+        outs[config] = _run_gemm(q, s, wq, ws).cpu()
+    for config in (5, 16, 17):
+        assert torch.equal(outs[config], outs[10]), config
+    _bf16_close(outs[16], ref.gemm(q, s, ref.RefLinear(wq, ws)))
 
 
 @pytest.mark.parametrize("k,n", [(2560, 6144), (4096, 2560), (2560, 19456), (9728, 2560)])
