@@ -30,6 +30,8 @@
 //     rows of one ds_read_b128 phase cover all 64 LDS banks;
 //   * workgroups are remapped so each XCD (8 per MI355X, each with its own
 //     L2) runs a contiguous band of tiles that share operands.
+#include <type_traits>
+
 #include "qx_common.h"
 #include "qx_status.h"
 
@@ -730,6 +732,474 @@ int launch128(const void* A, const float* sA, const void* W, const float* sW, vo
   QX_LAUNCH_STATUS();
 }
 
+// ---- ping-pong variant ------------------------------------------------------
+// The 8 waves form two groups, waves 0-3 and 4-7 (one of each per SIMD), that
+// run the same code a phase apart: group 1 passes one extra barrier at the
+// start (and group 0 one at the end). A 128-K block is four steps, each ended
+// by a barrier, one "prepare" and one "compute" step per 64-K half h:
+// prepare reads the half's 6 MFMA fragments from LDS into registers (with
+// h = 0, also the block's token scales and the rescale factors); compute
+// issues the half's 8 MFMAs (with h = 0, each tile's accumulators are
+// rescaled just before its first MFMA). So in every phase one wave per SIMD
+// feeds the matrix core while the other does its LDS work.
+// Phases are numbered from group 0's first step. Every wave loads its share
+// of block j + 1 at the start of its step 4j (group 0 in phase 4j, group 1 in
+// phase 4j + 1) and waits for it at the end of its step 4j + 2 (phases 4j + 2
+// and 4j + 3); the first reader of block j + 1 runs in phase 4j + 4. The
+// stage buffer it fills held block j - 1, last read by group 1 in phase
+// 4j - 1. (With LOADERS = 4 only group 0 loads, waiting at the end of its
+// step 4j + 3, which leaves the loads a phase more.) Per output element the
+// operations and their order are those of the other configurations
+// (rescale, then the block's MFMAs in K order): the result is bit-identical.
+template <int BM, int BN, int LOADERS>
+__global__ __launch_bounds__(512) void gemm_fp8_pp_kernel(
+    const uint8_t* __restrict__ A, const float* __restrict__ sA, const uint8_t* __restrict__ W,
+    const float* __restrict__ sW, uint16_t* __restrict__ C, int M, int N, int K, int64_t lda,
+    int64_t ldc, int64_t sa_ld, int tiles_m, int tiles_n, int group_m) {
+  constexpr int WAVES_N = 2, WAVES_M = 4, STAGES = 2;
+  using Cfg = Cfg128<BM, BN, WAVES_N, WAVES_M, STAGES>;
+  constexpr int TN = Cfg::kTN, TM = Cfg::kTM;
+  constexpr int kASlabs = BM / 8 / LOADERS, kWSlabs = BN / 8 / LOADERS;
+  constexpr int kSaPerWave = BM / LOADERS;
+  static_assert(Cfg::kWaves == 8, "two groups of four waves");
+  static_assert(LOADERS == 4 || LOADERS == 8, "group 0 or every wave loads");
+  static_assert(kSaPerWave <= 64 && BM % (8 * LOADERS) == 0 && BN % (8 * LOADERS) == 0,
+                "loads per wave");
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[Cfg::kLds];
+
+  const int total = tiles_m * tiles_n;
+  int id = blockIdx.x;
+  {
+    const int per = (total + 7) / 8;
+    const int xcd = id & 7, local = id >> 3;
+    const int full = total - (per - 1) * 8;
+    id = xcd < full ? xcd * per + local : full * per + (xcd - full) * (per - 1) + local;
+  }
+  const int width = group_m * tiles_n;
+  const int first_m = (id / width) * group_m;
+  const int gsize = min(tiles_m - first_m, group_m);
+  const int m0 = (first_m + (id % width) % gsize) * BM;
+  const int n0 = ((id % width) / gsize) * BN;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wn = wave % WAVES_N;
+  const int wm = wave / WAVES_N;
+  const bool loader = wave < LOADERS;
+  const bool first_group = wave < 4;
+  const int KT = K >> 7;
+
+  v16f acc[TN][TM];
+#pragma unroll
+  for (int a = 0; a < TN; ++a)
+#pragma unroll
+    for (int b = 0; b < TM; ++b)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[a][b][e] = 0.0f;
+  float s_prev[TM], ratio[TM];
+#pragma unroll
+  for (int b = 0; b < TM; ++b) s_prev[b] = ratio[b] = 0.0f;
+  const float* sw_row = sW + (int64_t)((n0 + wn * TN * 32) >> 7) * KT;
+  float sw_stage[STAGES];
+  v8i wf[TN], af[TM];
+  bool run = false;  // the block being prepared or computed has a nonzero weight scale
+
+  // operands and token scales of block kb (group 0), the weight scale (every wave)
+  auto issue = [&](int kb, auto stage_c) __attribute__((always_inline)) {
+    constexpr int stage = decltype(stage_c)::value;
+    if (loader) {
+      uint8_t* buf = smem + stage * Cfg::kStage;
+      const int64_t k_off = (int64_t)kb * 128;
+      load_slabs128<kASlabs>(A, lda, m0, M - 1, k_off, buf, wave * kASlabs, lane);
+      load_slabs128<kWSlabs>(W, K, n0, N - 1, k_off, buf + Cfg::kABytes, wave * kWSlabs, lane);
+      const int t = min(m0 + wave * kSaPerWave + lane % kSaPerWave, M - 1);
+      __builtin_amdgcn_global_load_lds((const void*)(sA + (int64_t)kb * sa_ld + t),
+                                       (lds_void*)(buf + Cfg::kABytes + Cfg::kWBytes + wave * 256),
+                                       4, 0, 0);
+    }
+    sw_stage[stage] = __builtin_nontemporal_load(sw_row + kb);
+  };
+
+  // prepare half h of the block in `stage`
+  auto prep = [&](auto stage_c, auto h_c) __attribute__((always_inline)) {
+    constexpr int stage = decltype(stage_c)::value;
+    constexpr int h = decltype(h_c)::value;
+    const uint8_t* a_lds = smem + stage * Cfg::kStage;
+    const uint8_t* w_lds = a_lds + Cfg::kABytes;
+    if (h == 0) {
+      const float sw =
+          __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(sw_stage[stage])));
+      run = sw != 0.0f;
+      if (run) {
+        const float* sa_lds = reinterpret_cast<const float*>(w_lds + Cfg::kWBytes);
+#pragma unroll
+        for (int b = 0; b < TM; ++b) {
+          const int row = wm * TM * 32 + b * 32 + (lane & 31);
+          const float s_cur = sa_lds[(row / kSaPerWave) * 64 + row % kSaPerWave] * sw;
+          ratio[b] = s_prev[b] / s_cur;
+          s_prev[b] = s_cur;
+        }
+      }
+    }
+    if (run) {
+#pragma unroll
+      for (int a = 0; a < TN; ++a)
+        wf[a] = read_frag128(w_lds, wn * TN * 32 + a * 32 + (lane & 31), h, lane);
+#pragma unroll
+      for (int b = 0; b < TM; ++b)
+        af[b] = read_frag128(a_lds, wm * TM * 32 + b * 32 + (lane & 31), h, lane);
+    }
+    // the stage is refilled a few phases on; its reads must be done by then
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  };
+
+  auto compute = [&](auto h_c) __attribute__((always_inline)) {
+    constexpr int h = decltype(h_c)::value;
+    if (run) {
+#pragma unroll
+      for (int a = 0; a < TN; ++a)
+#pragma unroll
+        for (int b = 0; b < TM; ++b) {
+          if (h == 0) {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[a][b][e] *= ratio[b];
+          }
+          acc[a][b] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(wf[a], af[b], acc[a][b], 0,
+                                                                     0, 0, 0, 0, 0);
+        }
+      if (h == 0) {
+        // each tile's 16 multiplies, then its MFMA: the next tile's
+        // multiplies issue while the MFMA runs
+#pragma unroll
+        for (int i = 0; i < TN * TM; ++i) {
+          __builtin_amdgcn_sched_group_barrier(0x002, 16, 0);  // VALU
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
+        }
+      }
+    }
+  };
+
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  auto block = [&](int j, auto stage_c) __attribute__((always_inline)) {
+    constexpr int stage = decltype(stage_c)::value;
+    if (j + 1 < KT) issue(j + 1, std::integral_constant<int, stage ^ 1>());
+    prep(stage_c, I0());
+    lds_barrier();
+    compute(I0());
+    lds_barrier();
+    prep(stage_c, I1());
+    if (LOADERS == 8) wait_vmcnt<0>();
+    lds_barrier();
+    compute(I1());
+    if (LOADERS == 4) wait_vmcnt<0>();
+    lds_barrier();
+  };
+
+  issue(0, I0());
+  wait_vmcnt<0>();
+  lds_barrier();
+  if (!first_group) lds_barrier();  // group 1 runs one phase behind
+  for (int j = 0; j < KT; j += 2) {
+    block(j, I0());
+    if (j + 1 < KT) block(j + 1, I1());
+  }
+  if (first_group) lds_barrier();
+
+  // epilogue, as in gemm_fp8_k128_kernel: the tile staged in LDS (padded
+  // rows), then whole rows stored, non-temporal
+  constexpr int kRowBytes = BN * 2 + 16;
+  constexpr int kChunks = BN / 8;
+  static_assert(BM * kRowBytes <= Cfg::kLds, "epilogue tile fits the stage buffers");
+  static_assert(64 % kChunks == 0 && (BM / Cfg::kWaves) % (64 / kChunks) == 0, "epilogue rows");
+  __syncthreads();
+#pragma unroll
+  for (int b = 0; b < TM; ++b) {
+    const int row = wm * TM * 32 + b * 32 + (lane & 31);
+    const float s = s_prev[b];
+    uint8_t* lrow = smem + row * kRowBytes;
+#pragma unroll
+    for (int a = 0; a < TN; ++a) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int off = (wn * TN * 32 + a * 32 + (lane >> 5) * 4 + g * 8) * 2;
+        uint2 v;
+        v.x = pack2_bf16(acc[a][b][g * 4 + 0] * s, acc[a][b][g * 4 + 1] * s);
+        v.y = pack2_bf16(acc[a][b][g * 4 + 2] * s, acc[a][b][g * 4 + 3] * s);
+        *reinterpret_cast<uint2*>(lrow + off) = v;
+      }
+    }
+  }
+  __syncthreads();
+  constexpr int kRowsPerOp = 64 / kChunks;
+  constexpr int kRowsPerWave = BM / Cfg::kWaves;
+  const bool wide = ((ldc & 7) == 0) && ((reinterpret_cast<uintptr_t>(C) & 15) == 0);
+  const int c = lane % kChunks;
+#pragma unroll
+  for (int i = 0; i < kRowsPerWave / kRowsPerOp; ++i) {
+    const int row = wave * kRowsPerWave + i * kRowsPerOp + lane / kChunks;
+    const int m = m0 + row;
+    const uint4 v = *reinterpret_cast<const uint4*>(smem + row * kRowBytes + c * 16);
+    if (m < M) {
+      uint16_t* dst = C + (int64_t)m * ldc + n0 + c * 8;
+      if (wide) {
+        const v4i w = {(int)v.x, (int)v.y, (int)v.z, (int)v.w};
+        __builtin_nontemporal_store(w, reinterpret_cast<v4i*>(dst));
+      } else {
+        reinterpret_cast<uint2*>(dst)[0] = make_uint2(v.x, v.y);
+        reinterpret_cast<uint2*>(dst)[1] = make_uint2(v.z, v.w);
+      }
+    }
+  }
+}
+
+template <int BM, int BN, int LOADERS>
+int launch_pp(const void* A, const float* sA, const void* W, const float* sW, void* C, int M,
+              int N, int K, int64_t lda, int64_t ldc, int64_t sa_ld, int group_m,
+              hipStream_t stream) {
+  const int tiles_m = (M + BM - 1) / BM;
+  const int tiles_n = N / BN;
+  hipLaunchKernelGGL((gemm_fp8_pp_kernel<BM, BN, LOADERS>), dim3(tiles_m * tiles_n), dim3(512), 0,
+                     stream,
+                     (const uint8_t*)A, sA, (const uint8_t*)W, sW, (uint16_t*)C, M, N, K, lda,
+                     ldc, sa_ld, tiles_m, tiles_n, group_m < 1 ? 1 : group_m);
+  QX_LAUNCH_STATUS();
+}
+
+// ---- ping-pong variant over 64-K stages ---------------------------------------
+// As gemm_fp8_pp_kernel, but the LDS ring holds four 64-K half-blocks (each
+// with its block's token scales), so loads run three half-blocks ahead
+// (96 KiB in flight per CU instead of 64). Steps per half-block q: prepare q
+// (issue the loads of q + 3, read q's 6 fragments; for an even q also the
+// block's scales and rescale factors), then compute q. Phases are numbered
+// from group 0's first step (group 1 runs one phase behind):
+//   * q + 3 loads into slot (q + 3) % 4 at the start of group 0's phase 2q
+//     (group 1: 2q + 1); that slot held q - 1, last read by group 1's
+//     prepare in phase 2q - 1;
+//   * every wave waits for its loads of q + 1 at the end of its prepare step
+//     of q (phases 2q and 2q + 1); q + 1 is first read in phase 2q + 2.
+template <int BM, int BN>
+__global__ __launch_bounds__(512) void gemm_fp8_pp64_kernel(
+    const uint8_t* __restrict__ A, const float* __restrict__ sA, const uint8_t* __restrict__ W,
+    const float* __restrict__ sW, uint16_t* __restrict__ C, int M, int N, int K, int64_t lda,
+    int64_t ldc, int64_t sa_ld, int tiles_m, int tiles_n, int group_m) {
+  constexpr int WAVES_N = 2, WAVES_M = 4, kWaves = 8, RING = 4, AHEAD = 3;
+  constexpr int TN = BN / WAVES_N / 32, TM = BM / WAVES_M / 32;
+  constexpr int kABytes = BM * 64, kWBytes = BN * 64, kSaBytes = 256 * kWaves;
+  constexpr int kStage = kABytes + kWBytes + kSaBytes;
+  constexpr int kLds = RING * kStage;
+  constexpr int kASlabs = BM / 16 / kWaves, kWSlabs = BN / 16 / kWaves;
+  constexpr int kSaPerWave = BM / kWaves;
+  constexpr int kOps = kASlabs + kWSlabs + 1;  // vector loads per wave per half-block
+  static_assert(TN >= 1 && TM >= 1 && BM % (16 * kWaves) == 0 && BN % (16 * kWaves) == 0,
+                "slabs");
+  static_assert(BN / WAVES_N == 128, "a wave's weight rows are one 128-row scale block");
+  static_assert(kSaPerWave <= 64, "token scales");
+  static_assert(kLds <= 160 * 1024, "LDS");
+  static_assert((AHEAD - 1) * kOps < 64 && AHEAD <= RING - 1, "vmcnt, ring");
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[kLds];
+
+  const int total = tiles_m * tiles_n;
+  int id = blockIdx.x;
+  {
+    const int per = (total + 7) / 8;
+    const int xcd = id & 7, local = id >> 3;
+    const int full = total - (per - 1) * 8;
+    id = xcd < full ? xcd * per + local : full * per + (xcd - full) * (per - 1) + local;
+  }
+  const int width = group_m * tiles_n;
+  const int first_m = (id / width) * group_m;
+  const int gsize = min(tiles_m - first_m, group_m);
+  const int m0 = (first_m + (id % width) % gsize) * BM;
+  const int n0 = ((id % width) / gsize) * BN;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wn = wave % WAVES_N;
+  const int wm = wave / WAVES_N;
+  const bool first_group = wave < 4;
+  const int Q = K >> 6;  // half-blocks
+
+  v16f acc[TN][TM];
+#pragma unroll
+  for (int a = 0; a < TN; ++a)
+#pragma unroll
+    for (int b = 0; b < TM; ++b)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[a][b][e] = 0.0f;
+  float s_prev[TM], ratio[TM];
+#pragma unroll
+  for (int b = 0; b < TM; ++b) s_prev[b] = ratio[b] = 0.0f;
+  const float* sw_row = sW + (int64_t)((n0 + wn * TN * 32) >> 7) * (K >> 7);
+  float sw_ring[2];  // weight scale of the blocks, by block parity
+  v8i wf[TN], af[TM];
+  bool run = false;
+
+  auto issue = [&](int q, auto slot_c) __attribute__((always_inline)) {
+    constexpr int slot = decltype(slot_c)::value;
+    uint8_t* buf = smem + slot * kStage;
+    const int kb = q >> 1;
+    const int64_t k_off = (int64_t)q * 64;
+    load_slabs<kASlabs>(A, lda, m0, M - 1, k_off, buf, wave * kASlabs, lane);
+    load_slabs<kWSlabs>(W, K, n0, N - 1, k_off, buf + kABytes, wave * kWSlabs, lane);
+    const int t = min(m0 + wave * kSaPerWave + lane % kSaPerWave, M - 1);
+    __builtin_amdgcn_global_load_lds((const void*)(sA + (int64_t)kb * sa_ld + t),
+                                     (lds_void*)(buf + kABytes + kWBytes + wave * 256), 4, 0, 0);
+    // slot parity is the half-block's parity: even slots start a block
+    if ((slot & 1) == 0) sw_ring[(slot >> 1) & 1] = __builtin_nontemporal_load(sw_row + kb);
+  };
+
+  auto prep = [&](auto slot_c) __attribute__((always_inline)) {
+    constexpr int slot = decltype(slot_c)::value;
+    const uint8_t* a_lds = smem + slot * kStage;
+    const uint8_t* w_lds = a_lds + kABytes;
+    if ((slot & 1) == 0) {
+      const float sw = __int_as_float(
+          __builtin_amdgcn_readfirstlane(__float_as_int(sw_ring[(slot >> 1) & 1])));
+      run = sw != 0.0f;
+      if (run) {
+        const float* sa_lds = reinterpret_cast<const float*>(w_lds + kWBytes);
+#pragma unroll
+        for (int b = 0; b < TM; ++b) {
+          const int row = wm * TM * 32 + b * 32 + (lane & 31);
+          const float s_cur = sa_lds[(row / kSaPerWave) * 64 + row % kSaPerWave] * sw;
+          ratio[b] = s_prev[b] / s_cur;
+          s_prev[b] = s_cur;
+        }
+      }
+    }
+    if (run) {
+#pragma unroll
+      for (int a = 0; a < TN; ++a) wf[a] = read_frag(w_lds, wn * TN * 32 + a * 32 + (lane & 31), lane);
+#pragma unroll
+      for (int b = 0; b < TM; ++b) af[b] = read_frag(a_lds, wm * TM * 32 + b * 32 + (lane & 31), lane);
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  };
+
+  auto compute = [&](auto h_c) __attribute__((always_inline)) {
+    constexpr int h = decltype(h_c)::value;
+    if (run) {
+#pragma unroll
+      for (int a = 0; a < TN; ++a)
+#pragma unroll
+        for (int b = 0; b < TM; ++b) {
+          if (h == 0) {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[a][b][e] *= ratio[b];
+          }
+          acc[a][b] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(wf[a], af[b], acc[a][b], 0,
+                                                                     0, 0, 0, 0, 0);
+        }
+      if (h == 0) {
+#pragma unroll
+        for (int i = 0; i < TN * TM; ++i) {
+          __builtin_amdgcn_sched_group_barrier(0x002, 16, 0);  // VALU
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
+        }
+      }
+    }
+  };
+
+  auto half_block = [&](int q, auto slot_c) __attribute__((always_inline)) {
+    constexpr int slot = decltype(slot_c)::value;
+    const bool more = q + AHEAD < Q;
+    if (more) issue(q + AHEAD, std::integral_constant<int, (slot + AHEAD) % RING>());
+    prep(slot_c);
+    if (more) {
+      wait_vmcnt<(AHEAD - 1) * kOps>();  // q + 1 has landed
+    } else {
+      wait_vmcnt<0>();
+    }
+    lds_barrier();
+    compute(std::integral_constant<int, slot & 1>());
+    lds_barrier();
+  };
+
+  using std::integral_constant;
+#pragma unroll
+  for (int q = 0; q < AHEAD; ++q) {
+    if (q < Q) {
+      if (q == 0) issue(0, integral_constant<int, 0>());
+      if (q == 1) issue(1, integral_constant<int, 1>());
+      if (q == 2) issue(2, integral_constant<int, 2>());
+    }
+  }
+  if (Q >= AHEAD) {
+    wait_vmcnt<(AHEAD - 1) * kOps>();
+  } else {
+    wait_vmcnt<0>();
+  }
+  lds_barrier();
+  if (!first_group) lds_barrier();  // group 1 runs one phase behind
+  for (int q = 0; q < Q; q += RING) {
+    half_block(q, integral_constant<int, 0>());
+    half_block(q + 1, integral_constant<int, 1>());  // Q is even
+    if (q + 2 < Q) {
+      half_block(q + 2, integral_constant<int, 2>());
+      half_block(q + 3, integral_constant<int, 3>());
+    }
+  }
+  if (first_group) lds_barrier();
+
+  // epilogue as in gemm_fp8_k128_kernel
+  constexpr int kRowBytes = BN * 2 + 16;
+  constexpr int kChunks = BN / 8;
+  static_assert(BM * kRowBytes <= kLds, "epilogue tile fits the ring");
+  static_assert(64 % kChunks == 0 && (BM / kWaves) % (64 / kChunks) == 0, "epilogue rows");
+  __syncthreads();
+#pragma unroll
+  for (int b = 0; b < TM; ++b) {
+    const int row = wm * TM * 32 + b * 32 + (lane & 31);
+    const float s = s_prev[b];
+    uint8_t* lrow = smem + row * kRowBytes;
+#pragma unroll
+    for (int a = 0; a < TN; ++a) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int off = (wn * TN * 32 + a * 32 + (lane >> 5) * 4 + g * 8) * 2;
+        uint2 v;
+        v.x = pack2_bf16(acc[a][b][g * 4 + 0] * s, acc[a][b][g * 4 + 1] * s);
+        v.y = pack2_bf16(acc[a][b][g * 4 + 2] * s, acc[a][b][g * 4 + 3] * s);
+        *reinterpret_cast<uint2*>(lrow + off) = v;
+      }
+    }
+  }
+  __syncthreads();
+  constexpr int kRowsPerOp = 64 / kChunks;
+  constexpr int kRowsPerWave = BM / kWaves;
+  const bool wide = ((ldc & 7) == 0) && ((reinterpret_cast<uintptr_t>(C) & 15) == 0);
+  const int c = lane % kChunks;
+#pragma unroll
+  for (int i = 0; i < kRowsPerWave / kRowsPerOp; ++i) {
+    const int row = wave * kRowsPerWave + i * kRowsPerOp + lane / kChunks;
+    const int m = m0 + row;
+    const uint4 v = *reinterpret_cast<const uint4*>(smem + row * kRowBytes + c * 16);
+    if (m < M) {
+      uint16_t* dst = C + (int64_t)m * ldc + n0 + c * 8;
+      if (wide) {
+        const v4i w = {(int)v.x, (int)v.y, (int)v.z, (int)v.w};
+        __builtin_nontemporal_store(w, reinterpret_cast<v4i*>(dst));
+      } else {
+        reinterpret_cast<uint2*>(dst)[0] = make_uint2(v.x, v.y);
+        reinterpret_cast<uint2*>(dst)[1] = make_uint2(v.z, v.w);
+      }
+    }
+  }
+}
+
+template <int BM, int BN>
+int launch_pp64(const void* A, const float* sA, const void* W, const float* sW, void* C, int M,
+                int N, int K, int64_t lda, int64_t ldc, int64_t sa_ld, int group_m,
+                hipStream_t stream) {
+  const int tiles_m = (M + BM - 1) / BM;
+  const int tiles_n = N / BN;
+  hipLaunchKernelGGL((gemm_fp8_pp64_kernel<BM, BN>), dim3(tiles_m * tiles_n), dim3(512), 0,
+                     stream, (const uint8_t*)A, sA, (const uint8_t*)W, sW, (uint16_t*)C, M, N, K,
+                     lda, ldc, sa_ld, tiles_m, tiles_n, group_m < 1 ? 1 : group_m);
+  QX_LAUNCH_STATUS();
+}
+
 // ---- persistent variant -----------------------------------------------------
 // One workgroup per CU walks its XCD's band of tiles (the same bands and
 // group_m order as the one-tile-per-workgroup kernel). The pipeline runs over
@@ -983,10 +1453,15 @@ int launch(const void* A, const float* sA, const void* W, const float* sW, void*
 
 extern "C" {
 
-// Tile configurations (tokens x weights, waves, 64-byte K stages); all give
-// the same result: 0: 256x256, 8 waves, 4; 1: 256x256, 4 waves, 4;
-// 2: 128x128, 4 waves, 4; 3: 128x256, 4 waves, 3; 4: 256x128, 4 waves, 3;
-// 5: 256x128, 4 waves, 2; 6: 256x128, 4 waves, 4.
+// Tile configurations (tokens x weights); every one gives the same result,
+// bit for bit. 64-K stages: 0: 256x256, 8 waves, 4 stages; 1: 256x256, 4
+// waves, 4; 2: 128x128, 4 waves, 4; 3: 128x256, 4 waves, 3; 4: 256x128, 4
+// waves, 3; 5: 256x128, 4 waves, 2; 6: 256x128, 4 waves, 4; 7-9: the same
+// with the next slice's fragments read during the current MFMAs. 128-K
+// stages (one scale block each): 10: 256x256, 8 waves (the default); 11:
+// 256x128, 4 waves; 12: 128x128; 13: 10 with L2 warming; 14, 15: 128x256;
+// 16, 17: persistent 256x256 / 256x128; 18, 19: 256x256 ping-pong (group 0
+// loads / every wave loads); 20: ping-pong over four 64-K stages.
 int qx_gemm_fp8_blockscaled(const void* A, const float* sA, const void* W, const float* sW,
                             void* C, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldc,
                             int64_t sa_ld, int config, hipStream_t stream) {
@@ -1059,6 +1534,15 @@ int qx_gemm_fp8_blockscaled(const void* A, const float* sA, const void* W, const
       return qx::launch128p<256, 256, 2, 4>(A, sA, W, sW, C, m, n, k, lda, ldc, sa_ld, 4, stream);
     case 17:
       return qx::launch128p<256, 128, 1, 4>(A, sA, W, sW, C, m, n, k, lda, ldc, sa_ld, 8, stream);
+    case 18:
+      QX_CHECK(n % 256 == 0, "gemm config 18 needs N %% 256 == 0 (N=%d)", n);
+      return qx::launch_pp<256, 256, 4>(A, sA, W, sW, C, m, n, k, lda, ldc, sa_ld, 4, stream);
+    case 19:
+      QX_CHECK(n % 256 == 0, "gemm config 19 needs N %% 256 == 0 (N=%d)", n);
+      return qx::launch_pp<256, 256, 8>(A, sA, W, sW, C, m, n, k, lda, ldc, sa_ld, 4, stream);
+    case 20:
+      QX_CHECK(n % 256 == 0, "gemm config 20 needs N %% 256 == 0 (N=%d)", n);
+      return qx::launch_pp64<256, 256>(A, sA, W, sW, C, m, n, k, lda, ldc, sa_ld, 4, stream);
     default:
       QX_CHECK(false, "gemm: unknown config %d", config);
   }

@@ -98,7 +98,7 @@ def test_gemm_small_shapes_match_dequantized_matmul(m, n, k):
     _bf16_close(out, want)
 
 
-@pytest.mark.parametrize("config", list(range(18)))
+@pytest.mark.parametrize("config", list(range(21)))
 def test_gemm_tile_configs_agree(config, monkeypatch):
     q, s, wq, ws = _gemm_case(300, 512, 512, seed=9)
     monkeypatch.setenv("QUAIL_GEMM_CONFIG", str(config))
@@ -113,7 +113,7 @@ def test_gemm_configs_are_bit_identical(monkeypatch):
     row's result must not depend on it)."""
     q, s, wq, ws = _gemm_case(700, 1024, 1024, seed=11)
     outs = []
-    for config in range(18):
+    for config in range(21):
         monkeypatch.setenv("QUAIL_GEMM_CONFIG", str(config))
         outs.append(_run_gemm(q, s, wq, ws).cpu())
     for config, out in enumerate(outs):
@@ -127,10 +127,10 @@ def test_gemm_persistent_configs_with_several_tiles_per_workgroup(monkeypatch):
     configuration bit for bit, and the oracle to the bf16 tolerance."""
     q, s, wq, ws = _gemm_case(2125, 4096, 384, seed=13)
     outs = {}
-    for config in (10, 5, 16, 17):
+    for config in (10, 5, 16, 17, 18, 19, 20):
         monkeypatch.setenv("QUAIL_GEMM_CONFIG", str(config))
         outs[config] = _run_gemm(q, s, wq, ws).cpu()
-    for config in (5, 16, 17):
+    for config in (5, 16, 17, 18, 19, 20):
         assert torch.equal(outs[config], outs[10]), config
     _bf16_close(outs[16], ref.gemm(q, s, ref.RefLinear(wq, ws)))
 
