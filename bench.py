@@ -174,7 +174,7 @@ def summarize(directory: str, copy_mib: int) -> None:
                 gemm_ns += ns
                 gemm_calls += calls
         if gemm_calls:
-            print(f"fp8 gemm, all tile variants: {gemm_calls} launches, "
+            print(f"fp8 gemm, all launches (plain and SwiGLU epilogue): {gemm_calls} launches, "
                   f"avg {gemm_ns / gemm_calls / 1e3:.2f} us")
     for path in counters:
         per = defaultdict(lambda: defaultdict(list))
@@ -307,20 +307,22 @@ def main():
     gemm_ms = 0.0
     gemm_flops = 0.0
     per_shape = {}
-    for m, n, k, start, end in timer:
+    for m, n, k, start, end, swiglu in timer:
         ms = start.elapsed_time(end)
         gemm_ms += ms
         gemm_flops += 2.0 * m * n * k
-        s = per_shape.setdefault(f"{k}x{n}", [0.0, 0.0, 0])
+        s = per_shape.setdefault(f"{k}x{n}" + ("+swiglu" if swiglu else ""), [0.0, 0.0, 0])
         s[0] += 2.0 * m * n * k
         s[1] += ms
         s[2] += 1
     gemm_tflops = gemm_flops / (gemm_ms * 1e-3) / 1e12
     launches = len(timer)
-    # operands read once and the bf16 result written once: A (M x K e4m3),
-    # W (N x K e4m3), C (M x N bf16) and both scale arrays
-    gemm_bytes = sum(m * k + n * k + 2 * m * n + 4 * (m * k // 128 + n * k // 16384)
-                     for m, n, k, _, _ in timer)
+    # operands read once and the result written once: A (M x K e4m3), W (N x K
+    # e4m3) and both scale arrays in; C (M x N bf16) out, or with the SwiGLU
+    # epilogue M x N/2 e4m3 and its M x N/256 scales
+    gemm_bytes = sum(m * k + n * k + 4 * (m * k // 128 + n * k // 16384) +
+                     (m * n // 2 + 4 * (m * n // 256) if swiglu else 2 * m * n)
+                     for m, n, k, _, _, swiglu in timer)
     traffic = load_traffic()
 
     fresh = stats[0]["fresh_tokens"]
@@ -373,7 +375,9 @@ def main():
         "e2e_roofline_frac": round(e2e_frac, 4),
         "roofline": {
             "bound": "mfma",
-            "kernel": "qx_gemm_fp8_blockscaled (all four Qwen3-4B shapes)",
+            "kernel": "FP8 block-scaled GEMM, all four Qwen3-4B projections: "
+                      "qx_gemm_fp8_blockscaled (qkv, o_proj, down) and "
+                      "qx_gemm_fp8_swiglu_quant (gate_up with the SiLU-quant epilogue)",
             "achieved": round(gemm_tflops, 2),
             "peak": PEAK_FP8 / 1e12,
             "unit": "TFLOP/s",

@@ -119,6 +119,23 @@ int qx_silu_mul_quant(const void* gate_up, int64_t gu_ld, void* q, int64_t q_ld,
                       int64_t s_ld, int64_t n, int64_t I, hipStream_t stream);
 
 /*
+ * The gate_up projection and the SiLU-gated product with its per-token
+ * 128-group e4m3 quant in one launch: replaces the pair
+ * Engine.gemm(g_in, g_scale, mlp.gate_up_proj) (attention.py:479-490) +
+ * Engine.activation_quant (attention.py:1245-1249 -> :771-793) that
+ * qwen3.py:66-67 issues. W / sW are the checkpoint's gate_up weight
+ * (2I x K, rows [gate | up]) and weight_scale_inv as they are; A / sA as
+ * for qx_gemm_fp8_blockscaled. Output as qx_silu_mul_quant's: Q (M x I)
+ * e4m3 with leading dimension q_ld, Qs column-major (Qs[g * qs_ld + m]).
+ * Bit-identical to qx_gemm_fp8_blockscaled (any config) followed by
+ * qx_silu_mul_quant; the bf16 gate_up rows are never written.
+ */
+int qx_gemm_fp8_swiglu_quant(const void* A, const float* sA, const void* W, const float* sW,
+                             void* Q, int64_t q_ld, float* Qs, int64_t qs_ld, int64_t M,
+                             int64_t I, int64_t K, int64_t lda, int64_t sa_ld,
+                             hipStream_t stream);
+
+/*
  * Per-token 128-group e4m3 quant of bf16 rows. Replaces Engine.quant ->
  * vLLM per_token_group_quant_fp8 (attention.py:517-532).
  */

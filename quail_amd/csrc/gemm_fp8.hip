@@ -458,10 +458,12 @@ int launch_plr(const void* A, const float* sA, const void* W, const float* sW, v
 // bytes [h*64 + (lane/32)*32, +32).
 __device__ __forceinline__ int swz128(int row) { return (row >> 1) & 7; }
 
+// hi_shift moves tile rows >= 128 by that many global rows (the gate_up
+// tile of the SwiGLU epilogue); a slab never straddles row 128.
 template <int SLABS>
 __device__ __forceinline__ void load_slabs128(const uint8_t* __restrict__ g, int64_t ld, int row0,
                                               int row_max, int64_t k_off, uint8_t* lds,
-                                              int first, int lane) {
+                                              int first, int lane, int hi_shift = 0) {
   const int r_in = lane >> 3;
   const int p = lane & 7;
 #pragma unroll
@@ -469,7 +471,7 @@ __device__ __forceinline__ void load_slabs128(const uint8_t* __restrict__ g, int
     const int slab = first + j;
     const int row = slab * 8 + r_in;
     const int c = p ^ swz128(row);
-    int grow = row0 + row;
+    int grow = row0 + row + (slab >= 16 ? hi_shift : 0);
     grow = grow < row_max ? grow : row_max;
     const uint8_t* src = g + (int64_t)grow * ld + k_off + c * 16;
     __builtin_amdgcn_global_load_lds((const void*)src, (lds_void*)(lds + slab * 1024), 16, 0,
@@ -518,11 +520,22 @@ struct Cfg128 {
 // 128-byte row segment of the block one stage further ahead (into a small
 // LDS sink nothing reads), so that block's rows are on their way into L2
 // when their real loads are issued.
-template <int BM, int BN, int WAVES_N, int WAVES_M, int STAGES, bool WARM>
+//
+// SWIGLU: W (N x K) is a gate_up weight, rows [gate (N/2) | up (N/2)], and
+// tile t covers output columns j0 = 128t.. of both halves: its first 128
+// weight rows are gate rows j0.., the next 128 up rows N/2 + j0... The
+// epilogue then writes silu(gate) * up, FP8-quantized per 128 columns (one
+// group per tile), to Q (M x N/2 e4m3, leading dimension q_ld) and its
+// scales to Qs (column-major, Qs[group * qs_ld + m]) instead of C; the bf16
+// rounding of gate and up is the unfused GEMM's, and the SiLU and quant
+// arithmetic the SiLU-quant kernel's, so the result is bit-identical to
+// qx_gemm_fp8_blockscaled followed by qx_silu_mul_quant.
+template <int BM, int BN, int WAVES_N, int WAVES_M, int STAGES, bool WARM, bool SWIGLU = false>
 __global__ __launch_bounds__(64 * WAVES_N * WAVES_M) void gemm_fp8_k128_kernel(
     const uint8_t* __restrict__ A, const float* __restrict__ sA, const uint8_t* __restrict__ W,
     const float* __restrict__ sW, uint16_t* __restrict__ C, int M, int N, int K, int64_t lda,
-    int64_t ldc, int64_t sa_ld, int tiles_m, int tiles_n, int group_m) {
+    int64_t ldc, int64_t sa_ld, int tiles_m, int tiles_n, int group_m, uint8_t* __restrict__ Q,
+    int64_t q_ld, float* __restrict__ Qs, int64_t qs_ld) {
   using Cfg = Cfg128<BM, BN, WAVES_N, WAVES_M, STAGES>;
   constexpr int TN = Cfg::kTN, TM = Cfg::kTM;
   constexpr int kWarm = WARM ? (BM + BN + 64 * Cfg::kWaves - 1) / (64 * Cfg::kWaves) : 0;
@@ -563,15 +576,20 @@ __global__ __launch_bounds__(64 * WAVES_N * WAVES_M) void gemm_fp8_k128_kernel(
     for (int b = 0; b < TM; ++b)
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[a][b][e] = 0.0f;
-  const float* sw_row = sW + (int64_t)((n0 + wn * TN * 32) >> 7) * KT;
+  // SWIGLU: the tile's weight rows are gate rows j0.. then up rows N/2 + j0..
+  const int w_row0 = SWIGLU ? (n0 >> 1) : n0;
+  const int w_hi_shift = SWIGLU ? (N >> 1) - 128 : 0;
+  static_assert(!SWIGLU || (BN == 256 && WAVES_N == 2), "SwiGLU tiles: 128 gate + 128 up rows");
+  const float* sw_row =
+      sW + (int64_t)((SWIGLU ? w_row0 + wn * ((N >> 1)) : n0 + wn * TN * 32) >> 7) * KT;
 
   float sw_ring[STAGES];
   auto issue = [&](int kb, int stage) {
     uint8_t* buf = smem + stage * Cfg::kStage;
     const int64_t k_off = (int64_t)kb * 128;
     load_slabs128<Cfg::kASlabs>(A, lda, m0, M - 1, k_off, buf, wave * Cfg::kASlabs, lane);
-    load_slabs128<Cfg::kWSlabs>(W, K, n0, N - 1, k_off, buf + Cfg::kABytes, wave * Cfg::kWSlabs,
-                                lane);
+    load_slabs128<Cfg::kWSlabs>(W, K, w_row0, N - 1, k_off, buf + Cfg::kABytes,
+                                wave * Cfg::kWSlabs, lane, w_hi_shift);
     // token scales of the tile for this block, beside its operands: lane i of
     // wave w loads the scale of tile row w * kSaPerWave + i into slot
     // w * 64 + i (lanes past kSaPerWave repeat a row into unused slots)
@@ -695,23 +713,60 @@ __global__ __launch_bounds__(64 * WAVES_N * WAVES_M) void gemm_fp8_k128_kernel(
     }
   }
   __syncthreads();
-  constexpr int kRowsPerOp = 64 / kChunks;
   constexpr int kRowsPerWave = BM / Cfg::kWaves;
-  const bool wide = ((ldc & 7) == 0) && ((reinterpret_cast<uintptr_t>(C) & 15) == 0);
-  const int c = lane % kChunks;
+  if constexpr (SWIGLU) {
+    // 16 lanes per tile row, 8 gate and 8 up values each (the SiLU-quant
+    // kernel's grouping: one 128-column quant group per 16 lanes)
+    static_assert(BN == 256 && kRowsPerWave % 4 == 0, "128 gate + 128 up columns per tile");
+    const int j0 = n0 >> 1;
+    const int seg = lane & 15;
 #pragma unroll
-  for (int i = 0; i < kRowsPerWave / kRowsPerOp; ++i) {
-    const int row = wave * kRowsPerWave + i * kRowsPerOp + lane / kChunks;
-    const int m = m0 + row;
-    const uint4 v = *reinterpret_cast<const uint4*>(smem + row * kRowBytes + c * 16);
-    if (m < M) {
-      uint16_t* dst = C + (int64_t)m * ldc + n0 + c * 8;
-      if (wide) {
-        const v4i w = {(int)v.x, (int)v.y, (int)v.z, (int)v.w};
-        __builtin_nontemporal_store(w, reinterpret_cast<v4i*>(dst));
-      } else {
-        reinterpret_cast<uint2*>(dst)[0] = make_uint2(v.x, v.y);
-        reinterpret_cast<uint2*>(dst)[1] = make_uint2(v.z, v.w);
+    for (int i = 0; i < kRowsPerWave / 4; ++i) {
+      const int row = wave * kRowsPerWave + i * 4 + (lane >> 4);
+      const int m = m0 + row;
+      const uint8_t* lrow = smem + row * kRowBytes;
+      const uint4 g = *reinterpret_cast<const uint4*>(lrow + seg * 16);
+      const uint4 u = *reinterpret_cast<const uint4*>(lrow + 256 + seg * 16);
+      const uint32_t gw[4] = {g.x, g.y, g.z, g.w}, uw[4] = {u.x, u.y, u.z, u.w};
+      float y[8];
+      float amax = 0.0f;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        y[2 * k] = silu_mul(lo_bf16(gw[k]), lo_bf16(uw[k]));
+        y[2 * k + 1] = silu_mul(hi_bf16(gw[k]), hi_bf16(uw[k]));
+      }
+#pragma unroll
+      for (int k = 0; k < 8; ++k) amax = fmaxf(amax, fabsf(y[k]));
+      amax = group_max<16>(amax);
+      const float scale = fp8_scale(amax);
+      const float rs = recip(scale);
+      if (m < M) {
+        const v2i o = {(int)pack4_fp8(div_by(y[0], scale, rs), div_by(y[1], scale, rs),
+                                      div_by(y[2], scale, rs), div_by(y[3], scale, rs)),
+                       (int)pack4_fp8(div_by(y[4], scale, rs), div_by(y[5], scale, rs),
+                                      div_by(y[6], scale, rs), div_by(y[7], scale, rs))};
+        __builtin_nontemporal_store(o, reinterpret_cast<v2i*>(Q + (int64_t)m * q_ld + j0 + seg * 8));
+        if (seg == 0) Qs[(int64_t)(j0 >> 7) * qs_ld + m] = scale;
+      }
+    }
+  } else {
+    constexpr int kRowsPerOp = 64 / kChunks;
+    const bool wide = ((ldc & 7) == 0) && ((reinterpret_cast<uintptr_t>(C) & 15) == 0);
+    const int c = lane % kChunks;
+#pragma unroll
+    for (int i = 0; i < kRowsPerWave / kRowsPerOp; ++i) {
+      const int row = wave * kRowsPerWave + i * kRowsPerOp + lane / kChunks;
+      const int m = m0 + row;
+      const uint4 v = *reinterpret_cast<const uint4*>(smem + row * kRowBytes + c * 16);
+      if (m < M) {
+        uint16_t* dst = C + (int64_t)m * ldc + n0 + c * 8;
+        if (wide) {
+          const v4i w = {(int)v.x, (int)v.y, (int)v.z, (int)v.w};
+          __builtin_nontemporal_store(w, reinterpret_cast<v4i*>(dst));
+        } else {
+          reinterpret_cast<uint2*>(dst)[0] = make_uint2(v.x, v.y);
+          reinterpret_cast<uint2*>(dst)[1] = make_uint2(v.z, v.w);
+        }
       }
     }
   }
@@ -728,7 +783,21 @@ int launch128(const void* A, const float* sA, const void* W, const float* sW, vo
   hipLaunchKernelGGL((gemm_fp8_k128_kernel<BM, BN, WN, WM, ST, WARM>), dim3(total),
                      dim3(Cfg::kThreads), 0, stream, (const uint8_t*)A, sA, (const uint8_t*)W, sW,
                      (uint16_t*)C, M, N, K, lda, ldc, sa_ld, tiles_m, tiles_n,
-                     group_m < 1 ? 1 : group_m);
+                     group_m < 1 ? 1 : group_m, nullptr, 0, nullptr, 0);
+  QX_LAUNCH_STATUS();
+}
+
+// the gate_up GEMM with the SiLU-quant epilogue (N = 2 x intermediate)
+int launch128_swiglu(const void* A, const float* sA, const void* W, const float* sW, void* Q,
+                     int64_t q_ld, float* Qs, int64_t qs_ld, int M, int N, int K, int64_t lda,
+                     int64_t sa_ld, hipStream_t stream) {
+  using Cfg = Cfg128<256, 256, 2, 4, 2>;
+  const int tiles_m = (M + 255) / 256;
+  const int tiles_n = N / 256;
+  hipLaunchKernelGGL((gemm_fp8_k128_kernel<256, 256, 2, 4, 2, false, true>),
+                     dim3(tiles_m * tiles_n), dim3(Cfg::kThreads), 0, stream, (const uint8_t*)A,
+                     sA, (const uint8_t*)W, sW, nullptr, M, N, K, lda, (int64_t)0, sa_ld, tiles_m,
+                     tiles_n, 4, (uint8_t*)Q, q_ld, Qs, qs_ld);
   QX_LAUNCH_STATUS();
 }
 
@@ -1462,6 +1531,29 @@ extern "C" {
 // 256x128, 4 waves; 12: 128x128; 13: 10 with L2 warming; 14, 15: 128x256;
 // 16, 17: persistent 256x256 / 256x128; 18, 19: 256x256 ping-pong (group 0
 // loads / every wave loads); 20: ping-pong over four 64-K stages.
+// gate_up projection + SiLU-gated product + per-128 FP8 quant in one launch:
+// W / sW are the gate_up weight (2I x K, rows [gate | up]) and its scales;
+// I = intermediate width.
+int qx_gemm_fp8_swiglu_quant(const void* A, const float* sA, const void* W, const float* sW,
+                             void* Q, int64_t q_ld, float* Qs, int64_t qs_ld, int64_t M,
+                             int64_t I, int64_t K, int64_t lda, int64_t sa_ld,
+                             hipStream_t stream) {
+  QX_CHECK(A && sA && W && sW && Q && Qs, "gemm_swiglu: null pointer");
+  QX_CHECK(M >= 0 && I > 0 && K > 0, "gemm_swiglu: bad shape M=%lld I=%lld K=%lld",
+           (long long)M, (long long)I, (long long)K);
+  QX_CHECK(K % 128 == 0 && I % 128 == 0, "gemm_swiglu: K=%lld, I=%lld not multiples of 128",
+           (long long)K, (long long)I);
+  QX_CHECK(lda >= K && lda % 16 == 0, "gemm_swiglu: lda=%lld", (long long)lda);
+  QX_CHECK(q_ld >= I && q_ld % 8 == 0 && ((uintptr_t)Q & 7) == 0, "gemm_swiglu: q_ld=%lld",
+           (long long)q_ld);
+  QX_CHECK(qs_ld >= M && sa_ld >= M, "gemm_swiglu: scale strides");
+  QX_CHECK(M < (1LL << 31) && 2 * I < (1LL << 31) && K < (1LL << 31), "gemm_swiglu: dims");
+  QX_CHECK(((uintptr_t)A & 15) == 0 && ((uintptr_t)W & 15) == 0, "gemm_swiglu: alignment");
+  if (M == 0) return QX_OK;
+  return qx::launch128_swiglu(A, sA, W, sW, Q, q_ld, Qs, qs_ld, (int)M, (int)(2 * I), (int)K, lda,
+                              sa_ld, stream);
+}
+
 int qx_gemm_fp8_blockscaled(const void* A, const float* sA, const void* W, const float* sW,
                             void* C, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldc,
                             int64_t sa_ld, int config, hipStream_t stream) {

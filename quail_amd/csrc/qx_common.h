@@ -18,6 +18,7 @@ constexpr float kFp8Max = 448.0f;
 constexpr float kScaleFloor = 1e-10f;  // attention.py:781 `max(amax, 1e-10)`
 constexpr int kGroup = 128;            // per-token FP8 group (attention.py GROUP)
 
+typedef int v2i __attribute__((ext_vector_type(2)));
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v8i __attribute__((ext_vector_type(8)));
 typedef float v4f __attribute__((ext_vector_type(4)));
@@ -188,6 +189,16 @@ __device__ __forceinline__ float div_by(float y, float s, float r) {
 __device__ __forceinline__ float recip(float s) {
   const float r = __builtin_amdgcn_rcpf(s);
   return fmaf(fmaf(-r, s, 1.0f), r, r);
+}
+
+// silu(g) * u in fp32 (attention.py:771-793): sigmoid(g) = 1 / (1 + e^-g),
+// e^-g = 2^(-g log2 e) on v_exp_f32; past |g| ~ 88 the exponential
+// saturates to 0 or inf and sigmoid to 1 or 0. Shared by the SiLU-quant
+// kernel and the gate_up GEMM's fused epilogue so both give the same bits.
+__device__ __forceinline__ float silu_mul(float g, float u) {
+  constexpr float kLog2e = 1.4426950408889634f;
+  const float d = 1.0f + __builtin_amdgcn_exp2f(-g * kLog2e);
+  return g * recip(d) * u;
 }
 
 // Per-group FP8 scale: max(amax, 1e-10) / 448 (attention.py:780-781).

@@ -319,16 +319,10 @@ __global__ __launch_bounds__(256) void group_quant_kernel(const uint16_t* __rest
     if (SILU) {
       uint4 u = *reinterpret_cast<const uint4*>(xrow + I + col);
       uint32_t uw[4] = {u.x, u.y, u.z, u.w};
-      // sigmoid(g) = 1 / (1 + e^-g), e^-g = 2^(-g log2 e) on v_exp_f32; past
-      // |g| ~ 88 the exponential saturates to 0 or inf and sigmoid to 1 or 0
-      constexpr float kLog2e = 1.4426950408889634f;
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
-        const float g0 = lo_bf16(gw[k]), g1 = hi_bf16(gw[k]);
-        const float d0 = 1.0f + __builtin_amdgcn_exp2f(-g0 * kLog2e);
-        const float d1 = 1.0f + __builtin_amdgcn_exp2f(-g1 * kLog2e);
-        y[2 * k] = g0 * recip(d0) * lo_bf16(uw[k]);
-        y[2 * k + 1] = g1 * recip(d1) * hi_bf16(uw[k]);
+        y[2 * k] = silu_mul(lo_bf16(gw[k]), lo_bf16(uw[k]));
+        y[2 * k + 1] = silu_mul(hi_bf16(gw[k]), hi_bf16(uw[k]));
       }
     } else {
 #pragma unroll

@@ -89,6 +89,7 @@ class Engine:
         self.use_ue8m0 = False
         # a list to receive (M, N, K, start event, end event) per GEMM launch,
         # recorded on the launch stream; None (the default) records nothing
+        # when a list: (M, N, K, start event, end event, SwiGLU epilogue) per GEMM
         self.gemm_timer = None
 
     # ---- weights and quant --------------------------------------------
@@ -132,8 +133,39 @@ class Engine:
                   self._scale_ld(input_scale), gemm_config(n, k, m), _stream())
         if timer is not None:
             end.record()
-            timer.append((m, n, k, start, end))
+            timer.append((m, n, k, start, end, False))
         return out
+
+    def gate_up_activation_quant(self, q_input, input_scale, linear):
+        """The gate_up projection and the quantized SiLU-gated product in one
+        launch: `activation_quant(gemm(q_input, input_scale, linear))`
+        (qwen3.py:66-67), bit for bit, without writing the bf16 gate_up rows.
+        `linear` is the checkpoint's gate_up projection as it is."""
+        w = linear.weight
+        sw = self.weight_scale(linear)
+        m, k = q_input.shape
+        n = w.shape[0]
+        if w.shape[1] != k:
+            raise ValueError(f"gate_up: input width {k} vs weight {tuple(w.shape)}")
+        if n % 256:
+            raise ValueError(f"gate_up: width {n} is not a multiple of 256")
+        if input_scale.shape != (m, k // GROUP) or input_scale.stride(0) != 1:
+            raise ValueError("gate_up: activation scales must be the (tokens, K/128) view of "
+                             "column-major storage")
+        half = n // 2
+        q = torch.empty((m, half), dtype=self.fp8, device=q_input.device)
+        scales = self._col_major_scales(m, half, q_input.device)
+        timer = self.gemm_timer
+        if timer is not None:
+            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            start.record()
+        _lib.call("qx_gemm_fp8_swiglu_quant", _ptr(q_input), _ptr(input_scale), _ptr(w),
+                  _ptr(sw), _ptr(q), q.stride(0), _ptr(scales), self._scale_ld(scales), m, half,
+                  k, q_input.stride(0), self._scale_ld(input_scale), _stream())
+        if timer is not None:
+            end.record()
+            timer.append((m, n, k, start, end, True))
+        return q, scales
 
     def quant(self, x, *, output=None):
         """Per-token 128-group FP8 of bf16 rows: (e4m3 rows, col-major scales)."""

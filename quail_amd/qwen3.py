@@ -7,9 +7,10 @@ per-head Q/K RMSNorm with rotary, paged attention, output projection,
 post-attention RMSNorm, gate_up projection, SiLU-gated product, down
 projection; the final norm runs on `chunk.final_indices` only.
 
-Two launches are fused relative to the reference's sequence, with identical
-results: the embedding gather with layer 0's norm_quant, and the final-row
-gather with the final fused_add_rms_norm.
+Launches are fused relative to the reference's sequence, with identical
+results: the embedding gather with layer 0's norm_quant; the gate_up
+projection with the SiLU-gated product and its quant (the bf16 gate_up rows
+are never written); the final-row gather with the final fused_add_rms_norm.
 """
 
 from quail_amd.engine import Engine
@@ -42,6 +43,11 @@ class Qwen3Pipeline:
                          layer.mlp.gate_up_proj.weight.shape[0]) for layer in self.layers)
         self.max_chunk_tokens = (2**31 - 1) // widest
         self.spec = spec
+        # gate_up + SiLU-quant in one launch when the engine has it (an engine
+        # class with the reference's primitives only runs them separately)
+        self.fuse_swiglu = (hasattr(self.engine, "gate_up_activation_quant") and
+                            all(layer.mlp.gate_up_proj.weight.shape[0] % 256 == 0
+                                for layer in self.layers))
 
     def _check_bounds(self, chunk):
         """Token ids index the embedding and positions the rotary cache; the
@@ -85,8 +91,11 @@ class Qwen3Pipeline:
         engine = self.engine
         hidden = engine.gemm(o_in, o_scale, layer.self_attn.o_proj)
         g_in, g_scale = engine.norm_quant(hidden, layer.post_attention_layernorm, residual)
-        gate_up = engine.gemm(g_in, g_scale, layer.mlp.gate_up_proj)
-        d_in, d_scale = engine.activation_quant(gate_up)
+        if self.fuse_swiglu:
+            d_in, d_scale = engine.gate_up_activation_quant(g_in, g_scale, layer.mlp.gate_up_proj)
+        else:
+            gate_up = engine.gemm(g_in, g_scale, layer.mlp.gate_up_proj)
+            d_in, d_scale = engine.activation_quant(gate_up)
         return engine.gemm(d_in, d_scale, layer.mlp.down_proj)
 
     def forward_chunk(self, chunk):

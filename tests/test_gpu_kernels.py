@@ -135,6 +135,36 @@ def test_gemm_persistent_configs_with_several_tiles_per_workgroup(monkeypatch):
     _bf16_close(outs[16], ref.gemm(q, s, ref.RefLinear(wq, ws)))
 
 
+@pytest.mark.parametrize("m,i,k,zero_blocks", [(700, 768, 512, False), (333, 1536, 256, True),
+                                               (2000, 9728, 2560, False)])
+def test_gate_up_swiglu_quant_equals_gemm_then_activation_quant(m, i, k, zero_blocks):
+    """qx_gemm_fp8_swiglu_quant (gate_up GEMM with the SiLU-quant epilogue)
+    against the two launches it replaces, bit for bit: a partial token tile,
+    the Qwen3-4B gate_up shape (I = 9728, K = 2560) and weight blocks whose
+    scale is 0 (skipped by the GEMM) in both halves."""
+    eng = _engine()
+    g = _gen(m + i + k)
+    a = torch.randn(m, k, generator=g)
+    q, s = ofp8.group_quant(a)
+    w = torch.randn(2 * i, k, generator=g) * 0.02
+    wq, ws = ofp8.quantize_weight_blocks(w)
+    if zero_blocks:
+        ws[1, 0] = 0.0                 # a gate block
+        ws[i // 128 + 2, 1] = 0.0      # an up block
+    lin = type("L", (), {})()
+    lin.weight = wq.to(DEV)
+    lin.weight_scale_inv = ws.to(DEV)
+    scales = torch.empty((k // 128, m), dtype=torch.float32, device=DEV)
+    scales.copy_(s.T)
+    q_in = q.to(DEV)
+    sv = scales.permute(1, 0)
+    want_q, want_s = eng.activation_quant(eng.gemm(q_in, sv, lin))
+    got_q, got_s = eng.gate_up_activation_quant(q_in, sv, lin)
+    assert got_q.shape == (m, i) and got_s.shape == (m, i // 128)
+    assert torch.equal(got_q.view(torch.uint8), want_q.view(torch.uint8))
+    assert torch.equal(got_s, want_s)
+
+
 @pytest.mark.parametrize("k,n", [(2560, 6144), (4096, 2560), (2560, 19456), (9728, 2560)])
 def test_gemm_qwen3_4b_shapes_at_8192_tokens(k, n):
     """The GEMM-alone config: M=8192 at the four Qwen3-4B projection shapes,
