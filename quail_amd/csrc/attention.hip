@@ -48,6 +48,9 @@ typedef __attribute__((address_space(3))) void lds_void;
 constexpr int kBK = 64;          // keys per KV tile
 constexpr int kPage = 16;        // tokens per arena page
 constexpr int kMaxPages = 2048;  // page-table entries staged in LDS per sequence
+// a row's reference max moves when a tile raises its max by more than this
+// many powers of two (probabilities then stay below 2^8 in fp16)
+constexpr float kLazyLog2 = 8.0f;
 
 typedef short v4s __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) v4s lds_v4s;
@@ -247,20 +250,33 @@ __global__ __launch_bounds__(HPB * QSUB * 64) void paged_attention_kernel(
 #pragma unroll
       for (int i = 0; i < 16; ++i) tmax = fmaxf(tmax, sacc[ks][i]);
     tmax = max_halves(tmax);
-    const float m_new = fmaxf(m_run, tmax);
-    const float m_use = m_new == -INFINITY ? 0.f : m_new * scale_log2;
-    // exactly 1 while the max holds, so a tile that adds nothing to a row
-    // (wholly masked for it) leaves its state bit for bit: a row's result
-    // then does not depend on how many such tiles its workgroup visits
-    const float alpha =
-        m_run == m_new ? 1.0f : __builtin_amdgcn_exp2f((m_run - m_new) * scale_log2);
+    // Lazy rescale: the reference max m_run, against which p and O are kept,
+    // moves only when a tile raises the row max by more than kLazyLog2 (log2
+    // units, so p < 2^kLazyLog2, well inside fp16), and O is rescaled only
+    // when some row of the wave moved: VALU work on the MFMA accumulators
+    // stalls the matrix core, and after a row's first tiles its max rarely
+    // jumps that far. A tile that adds nothing to a row (wholly masked for
+    // it, max -inf) never moves it and leaves its state bit for bit, so a
+    // row's result does not depend on how many such tiles its workgroup
+    // visits. (m_cand - m_run is NaN, so "no move", while both are -inf.)
+    const float m_cand = fmaxf(m_run, tmax);
+    const bool move = (m_cand - m_run) * scale_log2 > kLazyLog2;
+    const float alpha = move ? __builtin_amdgcn_exp2f((m_run - m_cand) * scale_log2) : 1.0f;
+    m_run = move ? m_cand : m_run;
+    const float m_use = m_run == -INFINITY ? 0.f : m_run * scale_log2;
+    if (__builtin_amdgcn_ballot_w64(move)) {  // wave-uniform; alpha is 1 where a row did not move
+#pragma unroll
+      for (int d = 0; d < NDS; ++d)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) o[d][e] *= alpha;
+    }
     float psum = 0.f;
     v8h pf[4];
 #pragma unroll
     for (int kc = 0; kc < 4; ++kc) {
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        // arguments are <= 0, so v_exp_f32's range is all that is needed
+        // arguments are <= kLazyLog2, inside v_exp_f32's range
         const float pv =
             __builtin_amdgcn_exp2f(fmaf(sacc[kc >> 1][(kc & 1) * 8 + j], scale_log2, -m_use));
         psum += pv;
@@ -269,13 +285,7 @@ __global__ __launch_bounds__(HPB * QSUB * 64) void paged_attention_kernel(
     }
     psum = sum_halves(psum);
     l_run = l_run * alpha + psum;
-    // alpha is 1 where the max did not move; rescaling unconditionally keeps
-    // this step one basic block
-#pragma unroll
-    for (int d = 0; d < NDS; ++d)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) o[d][e] *= alpha;
-    m_run = m_new;
+
     // O^T += V^T P^T: MFMA kc covers keys kc/2*32 + (kc&1)*16 +
     // {4*half + 0..3, 8 + 4*half + 0..3} in its k slots half*8 + 0..7, the
     // order in which P^T's lanes hold them

@@ -87,9 +87,9 @@ class Engine:
         self.fp8 = torch.float8_e4m3fn
         self.is_fp8 = True
         self.use_ue8m0 = False
-        # a list to receive (M, N, K, start event, end event) per GEMM launch,
-        # recorded on the launch stream; None (the default) records nothing
-        # when a list: (M, N, K, start event, end event, SwiGLU epilogue) per GEMM
+        # a list to receive (M, N, K, start event, end event, SwiGLU epilogue)
+        # per GEMM launch, recorded on the launch stream; None (the default)
+        # records nothing
         self.gemm_timer = None
 
     # ---- weights and quant --------------------------------------------
