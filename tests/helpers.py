@@ -57,3 +57,72 @@ def run_stage(model, workload, readout_kind="margins", num_pages=None, use_tree=
     results = run.run()
     torch.cuda.synchronize()
     return results, run
+
+
+def write_hf_checkpoint(model, cfg, path, shards=2):
+    """Write a model with the pipeline's module surface as a Hugging Face
+    Qwen3 FP8 checkpoint: q/k/v and gate/up split back into their own
+    tensors (with their weight_scale_inv row blocks), tensors spread over
+    `shards` safetensors files with a model.safetensors.index.json, and a
+    config.json carrying the FP8 quantization_config."""
+    import json
+    from pathlib import Path
+
+    from safetensors.torch import save_file
+
+    path = Path(path)
+    path.mkdir(parents=True, exist_ok=True)
+    d, hq, hk, inter = cfg.head_dim, cfg.heads, cfg.kv_heads, cfg.intermediate
+    tensors = {}
+
+    def put(name, t):
+        tensors[name] = t.detach().to("cpu").contiguous()
+
+    def split(prefix, linear, parts):
+        w, s = linear.weight, linear.weight_scale_inv
+        row = 0
+        for name, n in parts:
+            put(f"{prefix}.{name}.weight", w[row:row + n])
+            put(f"{prefix}.{name}.weight_scale_inv", s[row // 128:(row + n) // 128])
+            row += n
+
+    for i, layer in enumerate(model.model.layers):
+        a, m = f"model.layers.{i}.self_attn", f"model.layers.{i}.mlp"
+        attn = layer.self_attn
+        split(a, attn.qkv_proj, (("q_proj", hq * d), ("k_proj", hk * d), ("v_proj", hk * d)))
+        split(a, attn.o_proj, (("o_proj", cfg.hidden),))
+        put(f"{a}.q_norm.weight", attn.q_norm.weight)
+        put(f"{a}.k_norm.weight", attn.k_norm.weight)
+        split(m, layer.mlp.gate_up_proj, (("gate_proj", inter), ("up_proj", inter)))
+        split(m, layer.mlp.down_proj, (("down_proj", cfg.hidden),))
+        put(f"model.layers.{i}.input_layernorm.weight", layer.input_layernorm.weight)
+        put(f"model.layers.{i}.post_attention_layernorm.weight",
+            layer.post_attention_layernorm.weight)
+    put("model.embed_tokens.weight", model.model.embed_tokens.weight)
+    put("model.norm.weight", model.model.norm.weight)
+    if not cfg.tied_head:
+        put("lm_head.weight", model.lm_head.weight)
+    names = sorted(tensors)
+    weight_map = {}
+    for k in range(shards):
+        file = f"model-{k + 1:05d}-of-{shards:05d}.safetensors"
+        part = {n: tensors[n] for n in names[k::shards]}
+        save_file(part, str(path / file), metadata={"format": "pt"})
+        weight_map.update({n: file for n in part})
+    with open(path / "model.safetensors.index.json", "w") as f:
+        json.dump({"metadata": {}, "weight_map": weight_map}, f)
+    config = {
+        "architectures": ["Qwen3ForCausalLM"], "model_type": "qwen3",
+        "hidden_size": cfg.hidden, "intermediate_size": inter,
+        "num_attention_heads": hq, "num_key_value_heads": hk, "head_dim": d,
+        "num_hidden_layers": len(model.model.layers), "vocab_size": cfg.vocab,
+        "rms_norm_eps": cfg.eps, "rope_theta": cfg.theta, "rope_scaling": None,
+        "max_position_embeddings": cfg.max_positions, "hidden_act": "silu",
+        "tie_word_embeddings": cfg.tied_head, "torch_dtype": "bfloat16",
+        "use_sliding_window": False, "attention_bias": False,
+        "quantization_config": {"activation_scheme": "dynamic", "fmt": "e4m3",
+                                "quant_method": "fp8", "weight_block_size": [128, 128]},
+    }
+    with open(path / "config.json", "w") as f:
+        json.dump(config, f, indent=1)
+    return path
