@@ -136,6 +136,23 @@ int qx_gemm_fp8_swiglu_quant(const void* A, const float* sA, const void* W, cons
                              hipStream_t stream);
 
 /*
+ * Full-vocabulary log probabilities of t label tokens (t <= 16) for n rows:
+ * out[r * out_ld + j] = bf16logit(r, targets[j]) - logsumexp_v bf16logit(r, v)
+ * with bf16logit = bf16(normed[r] . head[v]) over all V head rows (bf16,
+ * h_ld), in fp32 — the normalize=True path of AsyncLabelLogprobs.logprobs
+ * (readout.py:164-200: F.linear over the whole head in blocks of rows,
+ * logsumexp, the targets' columns). targets: int64 on the device, each in
+ * [0, V). workspace: caller-allocated device memory of at least
+ * qx_vocab_logprobs_workspace(n, V, t) bytes (per-block partial sums and
+ * the target logits); H a multiple of 64.
+ */
+int64_t qx_vocab_logprobs_workspace(int64_t n, int64_t V, int64_t t);
+int qx_vocab_logprobs(const void* normed, int64_t n_ld, const void* head, int64_t h_ld,
+                      const int64_t* targets, int64_t t, float* out, int64_t out_ld, int64_t n,
+                      int64_t V, int64_t H, void* workspace, int64_t workspace_bytes,
+                      hipStream_t stream);
+
+/*
  * Per-token 128-group e4m3 quant of bf16 rows. Replaces Engine.quant ->
  * vLLM per_token_group_quant_fp8 (attention.py:517-532).
  */

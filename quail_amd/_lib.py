@@ -36,6 +36,9 @@ SIGNATURES = {
     "qx_silu_mul_quant": [_p, _i64, _p, _i64, _p, _i64, _i64, _i64, _p],
     "qx_gemm_fp8_swiglu_quant": [_p, _p, _p, _p, _p, _i64, _p, _i64, _i64, _i64, _i64, _i64,
                                  _i64, _p],
+    "qx_vocab_logprobs_workspace": [_i64, _i64, _i64],
+    "qx_vocab_logprobs": [_p, _i64, _p, _i64, _p, _i64, _p, _i64, _i64, _i64, _i64, _p, _i64,
+                          _p],
     "qx_group_quant": [_p, _i64, _p, _i64, _p, _i64, _i64, _i64, _p],
     "qx_kv_scatter": [_p, _i64, _p, _i64, _p, _p, _p, _p, _i64, _i64, _i32, _p],
     "qx_embed": [_p, _i64, _p, _p, _i64, _i64, _i64, _p],
@@ -49,7 +52,7 @@ SIGNATURES = {
 
 
 # entry points returning a count (>= 0) or -1 instead of a status
-RETURNS_COUNT = {"qx_paged_attention_work"}
+RETURNS_COUNT = {"qx_paged_attention_work", "qx_vocab_logprobs_workspace"}
 
 
 class QxUnavailable(RuntimeError):

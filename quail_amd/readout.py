@@ -11,9 +11,10 @@ never stalls the stream. The head itself is one gfx950 kernel
                               bf16 logits (readout.py:22-92)
   AsyncScores                 AI.SCORE: sigmoid((yes - no) / T), fp32 logits
                               (readout.py:314-339)
-  AsyncLabelLogprobs          AI.CLASSIFY with one-token labels and
-                              normalize=False: bf16 logits -> fp32
-                              (readout.py:143-226)
+  AsyncLabelLogprobs          AI.CLASSIFY label scores: normalize=True
+                              full-vocabulary log probabilities
+                              (qx_vocab_logprobs), normalize=False bf16
+                              logits -> fp32 (readout.py:143-226)
 """
 
 import numpy as np
@@ -143,38 +144,95 @@ class AsyncScores(_HostReadout):
         return super().result(handle, copy=False)
 
 
-class AsyncLabelLogprobs(_HostReadout):
-    """Unnormalized logits of one-token labels (AI.CLASSIFY, normalize=False).
+def answer_rows(rows_per_answer):
+    """Each read row's answer and its row within that answer
+    (readout.py:95-107)."""
+    counts = np.asarray(rows_per_answer, dtype=np.int64)
+    starts = np.repeat(np.cumsum(counts) - counts, counts)
+    return (np.repeat(np.arange(len(counts)), counts),
+            np.arange(int(counts.sum())) - starts)
 
-    targets are the label token ids in column order; rows of the full head
-    are gathered once. normalize=True (full-vocabulary log-softmax) is not
-    part of this engine.
+
+class AsyncLabelLogprobs(_HostReadout):
+    """AI.CLASSIFY label scores (readout.py:143-226).
+
+    normalize=True: each target token's log probability over the full
+    vocabulary at temperature 1 (bf16 logits of every head row, as F.linear
+    gives them, and their logsumexp in fp32): one qx_vocab_logprobs pass per
+    block of rows, which streams the head once per 128 rows and keeps no
+    (rows x vocabulary) logits. normalize=False: the targets' rows of the
+    head only, unnormalized bf16 logits as fp32 (qx_answer_head).
+
+    rows > 1 holds up to `rows` read rows per answer, unused rows NaN.
     """
 
-    def __init__(self, head, targets, rows=1, normalize=False):
+    BLOCK_ROWS = 1024
+
+    def __init__(self, head, targets, rows=1, normalize=True):
         super().__init__()
-        if normalize:
-            raise NotImplementedError("full-vocabulary normalized label scores")
-        if rows != 1:
-            raise NotImplementedError("one row per answer")
-        self.targets = list(targets)
-        idx = torch.tensor(self.targets, dtype=torch.long, device=head.device)
-        self.head_rows = head.index_select(0, idx).to(torch.bfloat16).contiguous()
+        self.targets = [int(t) for t in targets]
+        vocab, hidden = head.shape
+        if not 1 <= len(self.targets) <= 16:
+            raise ValueError(f"{len(self.targets)} label tokens; 1..16 are supported")
+        if any(not 0 <= t < vocab for t in self.targets):
+            raise ValueError(f"label token ids outside the vocabulary of {vocab}")
+        if rows < 1:
+            raise ValueError("rows must be positive")
         self.rows = rows
         self.normalize = normalize
-        self.dtype = np.dtype((np.float32, (len(self.targets),)))
-        self._none = torch.full((len(self.targets),), -1, dtype=torch.int32, device=head.device)
+        t = len(self.targets)
+        self.dtype = np.dtype((np.float32, (rows, t) if rows > 1 else (t,)))
+        idx = torch.tensor(self.targets, dtype=torch.long, device=head.device)
+        if normalize:
+            self.head = head if head.dtype == torch.bfloat16 else head.to(torch.bfloat16)
+            self.head = self.head.contiguous()
+            self.target_ids = idx
+            self.head_rows = None
+        else:
+            self.head = None
+            self.head_rows = head.index_select(0, idx).to(torch.bfloat16).contiguous()
 
     def logprobs(self, normed):
+        """(rows, targets) fp32 on the device: log probabilities with
+        normalize, logits without."""
         n, h = normed.shape
         t = len(self.targets)
         out = torch.empty((n, t), dtype=torch.float32, device=normed.device)
-        _lib.call("qx_answer_head", normed.data_ptr(), normed.stride(0),
-                  self.head_rows.data_ptr(), self.head_rows.stride(0), t, n, h, 0, None, 1.0,
-                  out.data_ptr(), None, None, None, _stream())
+        if n == 0:
+            return out
+        if not self.normalize:
+            _lib.call("qx_answer_head", normed.data_ptr(), normed.stride(0),
+                      self.head_rows.data_ptr(), self.head_rows.stride(0), t, n, h, 0, None, 1.0,
+                      out.data_ptr(), None, None, None, _stream())
+            return out
+        vocab = self.head.shape[0]
+        if normed.dtype != torch.bfloat16 or normed.stride(1) != 1:
+            normed = normed.to(torch.bfloat16).contiguous()
+        for start in range(0, n, self.BLOCK_ROWS):
+            block = normed[start:start + self.BLOCK_ROWS]
+            rows = block.shape[0]
+            size = _lib.count("qx_vocab_logprobs_workspace", rows, vocab, t)
+            work = torch.empty(size, dtype=torch.uint8, device=normed.device)
+            _lib.call("qx_vocab_logprobs", block.data_ptr(), block.stride(0),
+                      self.head.data_ptr(), self.head.stride(0), self.target_ids.data_ptr(), t,
+                      out[start:].data_ptr(), out.stride(0), rows, vocab, h, work.data_ptr(),
+                      size, _stream())
         return out
 
     def submit(self, normed, rows_per_answer=None):
-        if rows_per_answer is not None and any(r != 1 for r in rows_per_answer):
+        values = self.logprobs(normed)
+        if self.rows > 1:
+            if rows_per_answer is None:
+                rows_per_answer = [1] * values.shape[0]
+            if max(rows_per_answer) > self.rows:
+                raise ValueError(f"a suffix has {max(rows_per_answer)} rows to read; "
+                                 f"the readout holds {self.rows}")
+            answers = torch.full((len(rows_per_answer), self.rows, values.shape[1]),
+                                 float("nan"), dtype=torch.float32, device=values.device)
+            answer_index, row_index = (torch.from_numpy(i).to(values.device)
+                                       for i in answer_rows(rows_per_answer))
+            answers[answer_index, row_index] = values
+            values = answers
+        elif rows_per_answer is not None and any(r != 1 for r in rows_per_answer):
             raise ValueError("this readout holds one row per answer")
-        return self._copy(self.logprobs(normed))
+        return self._copy(values)
