@@ -44,7 +44,7 @@ int qx_device_is_gfx950(void);
  * (quail/backends/quail/executor/attention.py:479-490); weight scales are the
  * checkpoint's weight_scale_inv (attention.py:471-477).
  * K and N multiples of 128 (N of 256 for configs 0, 1, 3, 7, 10, 13-16,
- * 18-20). config selects the tile shape, tokens x weights, and the K depth
+ * 18-21). config selects the tile shape, tokens x weights, and the K depth
  * of a pipeline stage: 0: 256x256 (8 waves), 1: 256x256, 2: 128x128,
  * 3: 128x256, 4-6: 256x128 (3, 2, 4 stages of 64 K); 7-9: 256x256, 256x128,
  * 128x128 with fragments prefetched from LDS; 10-12: 256x256 (8 waves),
@@ -52,7 +52,9 @@ int qx_device_is_gfx950(void);
  * 14, 15: 128x256 (8 waves, two arrangements) with two stages of 128 K;
  * 16, 17: persistent 256x256 and 256x128 (one workgroup per CU);
  * 18, 19: 256x256 with two wave groups a phase apart (group 0 loads / every
- * wave loads); 20: as 19 over four stages of 64 K. Every config computes
+ * wave loads); 20: as 19 over four stages of 64 K; 21: 10 with each
+ * block's rescale issued four MFMAs away from the MFMAs on either side of
+ * it. Every config computes
  * each element with the same operations in the same order: the results are
  * bit-identical.
  */

@@ -516,6 +516,110 @@ struct Cfg128 {
   static_assert(STAGES >= 2 && (STAGES - 2) * kOpsPerStage < 64, "stages");
 };
 
+// Epilogue of the 128-K-stage tile kernels (acc in units of the last
+// block's scale s_prev): stage the bf16 tile in LDS and write it back.
+template <int BM, int BN, int WAVES_N, int WAVES_M, int LDS_BYTES, bool SWIGLU, int TN, int TM>
+__device__ __forceinline__ void tile_epilogue(uint8_t* smem, const v16f (&acc)[TN][TM],
+                                              const float (&s_prev)[TM], int lane, int wave, int m0,
+                                              int n0, int M, uint16_t* __restrict__ C,
+                                              int64_t ldc, uint8_t* __restrict__ Q, int64_t q_ld,
+                                              float* __restrict__ Qs, int64_t qs_ld) {
+  constexpr int kWaves = WAVES_N * WAVES_M;
+  const int wn = wave % WAVES_N;
+  const int wm = wave / WAVES_N;
+  // Epilogue through LDS. A lane's accumulators are one token's values at
+  // 4 runs of 4 columns, so storing them directly makes every store
+  // instruction touch 32 rows of C (8 bytes each); the bf16 tile is staged
+  // in LDS instead (rows = tokens, each row padded by 16 bytes so the 32
+  // rows one write instruction touches spread over the banks) and written
+  // back one whole tile row per BN/8 lanes, 16 bytes per lane.
+  // The stores are non-temporal: C is not read again by this launch, and
+  // keeping it out of L2 leaves L2 to the operand rows other workgroups
+  // are about to read (measured 1-8% faster per Qwen3-4B shape).
+  constexpr int kRowBytes = BN * 2 + 16;
+  constexpr int kChunks = BN / 8;
+  static_assert(BM * kRowBytes <= LDS_BYTES, "epilogue tile fits the stage buffers");
+  static_assert(64 % kChunks == 0 && BM % kWaves == 0 &&
+                    (BM / kWaves) % (64 / kChunks) == 0,
+                "epilogue rows");
+  __syncthreads();  // every wave is done with the last stage's operands
+#pragma unroll
+  for (int b = 0; b < TM; ++b) {
+    const int row = wm * TM * 32 + b * 32 + (lane & 31);
+    const float s = s_prev[b];
+    uint8_t* lrow = smem + row * kRowBytes;
+#pragma unroll
+    for (int a = 0; a < TN; ++a) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int off = (wn * TN * 32 + a * 32 + (lane >> 5) * 4 + g * 8) * 2;
+        uint2 v;
+        v.x = pack2_bf16(acc[a][b][g * 4 + 0] * s, acc[a][b][g * 4 + 1] * s);
+        v.y = pack2_bf16(acc[a][b][g * 4 + 2] * s, acc[a][b][g * 4 + 3] * s);
+        *reinterpret_cast<uint2*>(lrow + off) = v;
+      }
+    }
+  }
+  __syncthreads();
+  constexpr int kRowsPerWave = BM / kWaves;
+  if constexpr (SWIGLU) {
+    // 16 lanes per tile row, 8 gate and 8 up values each (the SiLU-quant
+    // kernel's grouping: one 128-column quant group per 16 lanes)
+    static_assert(BN == 256 && kRowsPerWave % 4 == 0, "128 gate + 128 up columns per tile");
+    const int j0 = n0 >> 1;
+    const int seg = lane & 15;
+#pragma unroll
+    for (int i = 0; i < kRowsPerWave / 4; ++i) {
+      const int row = wave * kRowsPerWave + i * 4 + (lane >> 4);
+      const int m = m0 + row;
+      const uint8_t* lrow = smem + row * kRowBytes;
+      const uint4 g = *reinterpret_cast<const uint4*>(lrow + seg * 16);
+      const uint4 u = *reinterpret_cast<const uint4*>(lrow + 256 + seg * 16);
+      const uint32_t gw[4] = {g.x, g.y, g.z, g.w}, uw[4] = {u.x, u.y, u.z, u.w};
+      float y[8];
+      float amax = 0.0f;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        y[2 * k] = silu_mul(lo_bf16(gw[k]), lo_bf16(uw[k]));
+        y[2 * k + 1] = silu_mul(hi_bf16(gw[k]), hi_bf16(uw[k]));
+      }
+#pragma unroll
+      for (int k = 0; k < 8; ++k) amax = fmaxf(amax, fabsf(y[k]));
+      amax = group_max<16>(amax);
+      const float scale = fp8_scale(amax);
+      const float rs = recip(scale);
+      if (m < M) {
+        const v2i o = {(int)pack4_fp8(div_by(y[0], scale, rs), div_by(y[1], scale, rs),
+                                      div_by(y[2], scale, rs), div_by(y[3], scale, rs)),
+                       (int)pack4_fp8(div_by(y[4], scale, rs), div_by(y[5], scale, rs),
+                                      div_by(y[6], scale, rs), div_by(y[7], scale, rs))};
+        __builtin_nontemporal_store(o, reinterpret_cast<v2i*>(Q + (int64_t)m * q_ld + j0 + seg * 8));
+        if (seg == 0) Qs[(int64_t)(j0 >> 7) * qs_ld + m] = scale;
+      }
+    }
+  } else {
+    constexpr int kRowsPerOp = 64 / kChunks;
+    const bool wide = ((ldc & 7) == 0) && ((reinterpret_cast<uintptr_t>(C) & 15) == 0);
+    const int c = lane % kChunks;
+#pragma unroll
+    for (int i = 0; i < kRowsPerWave / kRowsPerOp; ++i) {
+      const int row = wave * kRowsPerWave + i * kRowsPerOp + lane / kChunks;
+      const int m = m0 + row;
+      const uint4 v = *reinterpret_cast<const uint4*>(smem + row * kRowBytes + c * 16);
+      if (m < M) {
+        uint16_t* dst = C + (int64_t)m * ldc + n0 + c * 8;
+        if (wide) {
+          const v4i w = {(int)v.x, (int)v.y, (int)v.z, (int)v.w};
+          __builtin_nontemporal_store(w, reinterpret_cast<v4i*>(dst));
+        } else {
+          reinterpret_cast<uint2*>(dst)[0] = make_uint2(v.x, v.y);
+          reinterpret_cast<uint2*>(dst)[1] = make_uint2(v.z, v.w);
+        }
+      }
+    }
+  }
+}
+
 // WARM: with each stage's loads, also touch one 4-byte word of every
 // 128-byte row segment of the block one stage further ahead (into a small
 // LDS sink nothing reads), so that block's rows are on their way into L2
@@ -679,97 +783,214 @@ __global__ __launch_bounds__(64 * WAVES_N * WAVES_M) void gemm_fp8_k128_kernel(
     }
   }
 
-  // Epilogue through LDS. A lane's accumulators are one token's values at
-  // 4 runs of 4 columns, so storing them directly makes every store
-  // instruction touch 32 rows of C (8 bytes each); the bf16 tile is staged
-  // in LDS instead (rows = tokens, each row padded by 16 bytes so the 32
-  // rows one write instruction touches spread over the banks) and written
-  // back one whole tile row per BN/8 lanes, 16 bytes per lane.
-  // The stores are non-temporal: C is not read again by this launch, and
-  // keeping it out of L2 leaves L2 to the operand rows other workgroups
-  // are about to read (measured 1-8% faster per Qwen3-4B shape).
-  constexpr int kRowBytes = BN * 2 + 16;
-  constexpr int kChunks = BN / 8;
-  static_assert(BM * kRowBytes <= Cfg::kLds, "epilogue tile fits the stage buffers");
-  static_assert(64 % kChunks == 0 && BM % Cfg::kWaves == 0 &&
-                    (BM / Cfg::kWaves) % (64 / kChunks) == 0,
-                "epilogue rows");
-  __syncthreads();  // every wave is done with the last stage's operands
-#pragma unroll
-  for (int b = 0; b < TM; ++b) {
-    const int row = wm * TM * 32 + b * 32 + (lane & 31);
-    const float s = s_prev[b];
-    uint8_t* lrow = smem + row * kRowBytes;
-#pragma unroll
-    for (int a = 0; a < TN; ++a) {
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int off = (wn * TN * 32 + a * 32 + (lane >> 5) * 4 + g * 8) * 2;
-        uint2 v;
-        v.x = pack2_bf16(acc[a][b][g * 4 + 0] * s, acc[a][b][g * 4 + 1] * s);
-        v.y = pack2_bf16(acc[a][b][g * 4 + 2] * s, acc[a][b][g * 4 + 3] * s);
-        *reinterpret_cast<uint2*>(lrow + off) = v;
-      }
-    }
+  tile_epilogue<BM, BN, WAVES_N, WAVES_M, Cfg::kLds, SWIGLU>(smem, acc, s_prev, lane, wave, m0,
+                                                            n0, M, C, ldc, Q, q_ld, Qs, qs_ld);
+}
+
+// ---- staggered rescale ---------------------------------------------------------
+// gemm_fp8_k128_kernel<256, 256, 2, 4, 2> with the block-scale rescale moved
+// away from the MFMAs that produce and consume each accumulator. VALU work
+// on an accumulator right after the MFMA that wrote it, or right before the
+// MFMA that reads it, serialises with the matrix core; a few MFMAs between
+// them and it overlaps. A wave's 8 tiles are two token halves b = 0, 1 of 4
+// weight tiles each; per block the MFMAs run h0 b0 | h0 b1 | h1 b0 | h1 b1
+// (4 each), the b1 tiles are rescaled for block kb while the h0 b0 MFMAs of
+// kb issue, and the b0 tiles for block kb + 1 while the h1 b1 MFMAs of kb
+// issue, so four MFMAs separate every rescale from the MFMAs on either side.
+// The rescale of the b0 tiles needs block kb + 1's scales during block kb:
+// each lane loads its two tokens' scales two blocks ahead into registers,
+// and the weight scale is loaded with the stage. Per output element the
+// operations and their order are unchanged (rescale, then the block's MFMAs
+// in K order): bit-identical to the other configurations.
+template <bool SWIGLU>
+__global__ __launch_bounds__(512) void gemm_fp8_k128s_kernel(
+    const uint8_t* __restrict__ A, const float* __restrict__ sA, const uint8_t* __restrict__ W,
+    const float* __restrict__ sW, uint16_t* __restrict__ C, int M, int N, int K, int64_t lda,
+    int64_t ldc, int64_t sa_ld, int tiles_m, int tiles_n, int group_m, uint8_t* __restrict__ Q,
+    int64_t q_ld, float* __restrict__ Qs, int64_t qs_ld) {
+  constexpr int BM = 256, BN = 256, WAVES_N = 2, WAVES_M = 4, STAGES = 2;
+  using Cfg = Cfg128<BM, BN, WAVES_N, WAVES_M, STAGES>;
+  constexpr int TN = Cfg::kTN, TM = Cfg::kTM;
+  static_assert(TN == 4 && TM == 2, "two token halves of four weight tiles");
+  constexpr int kStage = Cfg::kABytes + Cfg::kWBytes;
+  // the stage buffers, or the epilogue's padded bf16 tile, whichever is larger
+  constexpr int kEpilogueBytes = BM * (BN * 2 + 16);
+  constexpr int kLds = STAGES * kStage > kEpilogueBytes ? STAGES * kStage : kEpilogueBytes;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[kLds];
+
+  const int total = tiles_m * tiles_n;
+  int id = blockIdx.x;
+  {
+    const int per = (total + 7) / 8;
+    const int xcd = id & 7, local = id >> 3;
+    const int full = total - (per - 1) * 8;
+    id = xcd < full ? xcd * per + local : full * per + (xcd - full) * (per - 1) + local;
   }
-  __syncthreads();
-  constexpr int kRowsPerWave = BM / Cfg::kWaves;
-  if constexpr (SWIGLU) {
-    // 16 lanes per tile row, 8 gate and 8 up values each (the SiLU-quant
-    // kernel's grouping: one 128-column quant group per 16 lanes)
-    static_assert(BN == 256 && kRowsPerWave % 4 == 0, "128 gate + 128 up columns per tile");
-    const int j0 = n0 >> 1;
-    const int seg = lane & 15;
+  const int width = group_m * tiles_n;
+  const int first_m = (id / width) * group_m;
+  const int gsize = min(tiles_m - first_m, group_m);
+  const int m0 = (first_m + (id % width) % gsize) * BM;
+  const int n0 = ((id % width) / gsize) * BN;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wn = wave % WAVES_N;
+  const int wm = wave / WAVES_N;
+  const int KT = K >> 7;
+  const int w_row0 = SWIGLU ? (n0 >> 1) : n0;
+  const int w_hi_shift = SWIGLU ? (N >> 1) - 128 : 0;
+  const float* sw_row =
+      sW + (int64_t)((SWIGLU ? w_row0 + wn * (N >> 1) : n0 + wn * TN * 32) >> 7) * KT;
+  // this lane's two token rows (tail rows read the last row's scales)
+  const int t0 = min(m0 + wm * TM * 32 + (lane & 31), M - 1);
+  const int t1 = min(m0 + wm * TM * 32 + 32 + (lane & 31), M - 1);
+
+  v16f acc[TN][TM];
 #pragma unroll
-    for (int i = 0; i < kRowsPerWave / 4; ++i) {
-      const int row = wave * kRowsPerWave + i * 4 + (lane >> 4);
-      const int m = m0 + row;
-      const uint8_t* lrow = smem + row * kRowBytes;
-      const uint4 g = *reinterpret_cast<const uint4*>(lrow + seg * 16);
-      const uint4 u = *reinterpret_cast<const uint4*>(lrow + 256 + seg * 16);
-      const uint32_t gw[4] = {g.x, g.y, g.z, g.w}, uw[4] = {u.x, u.y, u.z, u.w};
-      float y[8];
-      float amax = 0.0f;
+  for (int a = 0; a < TN; ++a)
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        y[2 * k] = silu_mul(lo_bf16(gw[k]), lo_bf16(uw[k]));
-        y[2 * k + 1] = silu_mul(hi_bf16(gw[k]), hi_bf16(uw[k]));
-      }
+    for (int b = 0; b < TM; ++b)
 #pragma unroll
-      for (int k = 0; k < 8; ++k) amax = fmaxf(amax, fabsf(y[k]));
-      amax = group_max<16>(amax);
-      const float scale = fp8_scale(amax);
-      const float rs = recip(scale);
-      if (m < M) {
-        const v2i o = {(int)pack4_fp8(div_by(y[0], scale, rs), div_by(y[1], scale, rs),
-                                      div_by(y[2], scale, rs), div_by(y[3], scale, rs)),
-                       (int)pack4_fp8(div_by(y[4], scale, rs), div_by(y[5], scale, rs),
-                                      div_by(y[6], scale, rs), div_by(y[7], scale, rs))};
-        __builtin_nontemporal_store(o, reinterpret_cast<v2i*>(Q + (int64_t)m * q_ld + j0 + seg * 8));
-        if (seg == 0) Qs[(int64_t)(j0 >> 7) * qs_ld + m] = scale;
-      }
-    }
-  } else {
-    constexpr int kRowsPerOp = 64 / kChunks;
-    const bool wide = ((ldc & 7) == 0) && ((reinterpret_cast<uintptr_t>(C) & 15) == 0);
-    const int c = lane % kChunks;
+      for (int e = 0; e < 16; ++e) acc[a][b][e] = 0.0f;
+  float s_prev[TM] = {0.0f, 0.0f};
+  float sw_ring[STAGES];
+
+  auto issue = [&](int kb, int stage) __attribute__((always_inline)) {
+    uint8_t* buf = smem + stage * kStage;
+    const int64_t k_off = (int64_t)kb * 128;
+    load_slabs128<Cfg::kASlabs>(A, lda, m0, M - 1, k_off, buf, wave * Cfg::kASlabs, lane);
+    load_slabs128<Cfg::kWSlabs>(W, K, w_row0, N - 1, k_off, buf + Cfg::kABytes,
+                                wave * Cfg::kWSlabs, lane, w_hi_shift);
+    sw_ring[stage] = __builtin_nontemporal_load(sw_row + kb);
+  };
+  // token scales of blocks kb (cur), kb + 1 (nxt), kb + 2 (nxt2), by half
+  float ta_cur[2], ta_nxt[2], ta_nxt2[2];
+  auto load_ta = [&](int kb, float (&dst)[2]) __attribute__((always_inline)) {
+    const float* row = sA + (int64_t)min(kb, KT - 1) * sa_ld;  // wave-uniform
+    dst[0] = row[t0];
+    dst[1] = row[t1];
+  };
+
+  issue(0, 0);
+  load_ta(0, ta_cur);
+  load_ta(1, ta_nxt);
+  // block 0's scale of the b0 tiles (their rescale by 0 / s of zero
+  // accumulators is a no-op); a zero weight-scale block keeps s_prev
+  {
+    const float sw0 = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(sw_ring[0])));
+    if (sw0 != 0.0f) s_prev[0] = ta_cur[0] * sw0;
+  }
+
+  for (int base = 0; base < KT; base += STAGES) {
 #pragma unroll
-    for (int i = 0; i < kRowsPerWave / kRowsPerOp; ++i) {
-      const int row = wave * kRowsPerWave + i * kRowsPerOp + lane / kChunks;
-      const int m = m0 + row;
-      const uint4 v = *reinterpret_cast<const uint4*>(smem + row * kRowBytes + c * 16);
-      if (m < M) {
-        uint16_t* dst = C + (int64_t)m * ldc + n0 + c * 8;
-        if (wide) {
-          const v4i w = {(int)v.x, (int)v.y, (int)v.z, (int)v.w};
-          __builtin_nontemporal_store(w, reinterpret_cast<v4i*>(dst));
-        } else {
-          reinterpret_cast<uint2*>(dst)[0] = make_uint2(v.x, v.y);
-          reinterpret_cast<uint2*>(dst)[1] = make_uint2(v.z, v.w);
+    for (int stage = 0; stage < STAGES; ++stage) {
+      const int kb = base + stage;
+      if (kb < KT) {
+        wait_vmcnt<0>();  // block kb's operands (and older scale loads) are in
+        lds_barrier();
+        if (kb + 1 < KT) issue(kb + 1, stage ^ 1);
+        load_ta(kb + 2, ta_nxt2);
+        const float sw = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(sw_ring[stage])));
+        const bool run = sw != 0.0f;  // wave-uniform
+        const uint8_t* a_lds = smem + stage * kStage;
+        const uint8_t* w_lds = a_lds + Cfg::kABytes;
+        // the b1 tiles' factor for block kb
+        float r1 = 1.0f;
+        if (run) {
+          const float s_cur = ta_cur[1] * sw;
+          r1 = s_prev[1] / s_cur;
+          s_prev[1] = s_cur;
+        }
+        // the b0 tiles' factor for block kb + 1 (1 if there is none or it adds nothing)
+        float r0 = 1.0f;
+        if (kb + 1 < KT) {
+          const float swn =
+              __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(sw_ring[stage ^ 1])));
+          if (swn != 0.0f) {
+            const float s_cur = ta_nxt[0] * swn;
+            r0 = s_prev[0] / s_cur;
+            s_prev[0] = s_cur;
+          }
+        }
+        // A block whose weight scale is 0 adds nothing: its MFMAs run on
+        // zero token fragments (acc + 0 leaves acc's bits: the accumulators
+        // start at +0 and never hold -0), so every block is one instruction
+        // stream and skipping it would give the same result.
+        const v8i zero = {0, 0, 0, 0, 0, 0, 0, 0};
+        {
+          v8i wf[TN], af[TM];
+#pragma unroll
+          for (int a = 0; a < TN; ++a)
+            wf[a] = read_frag128(w_lds, wn * TN * 32 + a * 32 + (lane & 31), 0, lane);
+#pragma unroll
+          for (int b = 0; b < TM; ++b)
+            af[b] = run ? read_frag128(a_lds, wm * TM * 32 + b * 32 + (lane & 31), 0, lane) : zero;
+          // h0 b0, with the b1 rescale
+#pragma unroll
+          for (int a = 0; a < TN; ++a) {
+            acc[a][0] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(wf[a], af[0], acc[a][0],
+                                                                       0, 0, 0, 0, 0, 0);
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[a][1][e] *= r1;
+          }
+#pragma unroll
+          for (int a = 0; a < TN; ++a) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, 16, 0);
+          }
+          // h0 b1
+#pragma unroll
+          for (int a = 0; a < TN; ++a)
+            acc[a][1] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(wf[a], af[1], acc[a][1],
+                                                                       0, 0, 0, 0, 0, 0);
+#pragma unroll
+          for (int a = 0; a < TN; ++a)
+            wf[a] = read_frag128(w_lds, wn * TN * 32 + a * 32 + (lane & 31), 1, lane);
+#pragma unroll
+          for (int b = 0; b < TM; ++b)
+            af[b] = run ? read_frag128(a_lds, wm * TM * 32 + b * 32 + (lane & 31), 1, lane) : zero;
+          // h1 b0
+#pragma unroll
+          for (int a = 0; a < TN; ++a)
+            acc[a][0] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(wf[a], af[0], acc[a][0],
+                                                                       0, 0, 0, 0, 0, 0);
+          // h1 b1, with the b0 rescale for block kb + 1
+#pragma unroll
+          for (int a = 0; a < TN; ++a) {
+            acc[a][1] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(wf[a], af[1], acc[a][1],
+                                                                       0, 0, 0, 0, 0, 0);
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[a][0][e] *= r0;
+          }
+#pragma unroll
+          for (int a = 0; a < TN; ++a) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, 16, 0);
+          }
+        }
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          ta_cur[h] = ta_nxt[h];
+          ta_nxt[h] = ta_nxt2[h];
         }
       }
     }
   }
+
+  tile_epilogue<BM, BN, WAVES_N, WAVES_M, kLds, SWIGLU>(
+      smem, acc, s_prev, lane, wave, m0, n0, M, C, ldc, Q, q_ld, Qs, qs_ld);
+}
+
+template <bool SWIGLU>
+int launch128s(const void* A, const float* sA, const void* W, const float* sW, void* C, int M,
+               int N, int K, int64_t lda, int64_t ldc, int64_t sa_ld, void* Q, int64_t q_ld,
+               float* Qs, int64_t qs_ld, hipStream_t stream) {
+  const int tiles_m = (M + 255) / 256;
+  const int tiles_n = N / 256;
+  hipLaunchKernelGGL((gemm_fp8_k128s_kernel<SWIGLU>), dim3(tiles_m * tiles_n), dim3(512), 0,
+                     stream, (const uint8_t*)A, sA, (const uint8_t*)W, sW, (uint16_t*)C, M, N, K,
+                     lda, ldc, sa_ld, tiles_m, tiles_n, 4, (uint8_t*)Q, q_ld, Qs, qs_ld);
+  QX_LAUNCH_STATUS();
 }
 
 template <int BM, int BN, int WN, int WM, int ST, bool WARM = false>
@@ -1530,7 +1751,8 @@ extern "C" {
 // stages (one scale block each): 10: 256x256, 8 waves (the default); 11:
 // 256x128, 4 waves; 12: 128x128; 13: 10 with L2 warming; 14, 15: 128x256;
 // 16, 17: persistent 256x256 / 256x128; 18, 19: 256x256 ping-pong (group 0
-// loads / every wave loads); 20: ping-pong over four 64-K stages.
+// loads / every wave loads); 20: ping-pong over four 64-K stages; 21: 10
+// with the rescale staggered away from the MFMAs.
 // gate_up projection + SiLU-gated product + per-128 FP8 quant in one launch:
 // W / sW are the gate_up weight (2I x K, rows [gate | up]) and its scales;
 // I = intermediate width.
@@ -1632,6 +1854,10 @@ int qx_gemm_fp8_blockscaled(const void* A, const float* sA, const void* W, const
     case 19:
       QX_CHECK(n % 256 == 0, "gemm config 19 needs N %% 256 == 0 (N=%d)", n);
       return qx::launch_pp<256, 256, 8>(A, sA, W, sW, C, m, n, k, lda, ldc, sa_ld, 4, stream);
+    case 21:
+      QX_CHECK(n % 256 == 0, "gemm config 21 needs N %% 256 == 0 (N=%d)", n);
+      return qx::launch128s<false>(A, sA, W, sW, C, m, n, k, lda, ldc, sa_ld, nullptr, 0, nullptr,
+                                   0, stream);
     case 20:
       QX_CHECK(n % 256 == 0, "gemm config 20 needs N %% 256 == 0 (N=%d)", n);
       return qx::launch_pp64<256, 256>(A, sA, W, sW, C, m, n, k, lda, ldc, sa_ld, 4, stream);

@@ -98,7 +98,7 @@ def test_gemm_small_shapes_match_dequantized_matmul(m, n, k):
     _bf16_close(out, want)
 
 
-@pytest.mark.parametrize("config", list(range(21)))
+@pytest.mark.parametrize("config", list(range(22)))
 def test_gemm_tile_configs_agree(config, monkeypatch):
     q, s, wq, ws = _gemm_case(300, 512, 512, seed=9)
     monkeypatch.setenv("QUAIL_GEMM_CONFIG", str(config))
@@ -113,7 +113,7 @@ def test_gemm_configs_are_bit_identical(monkeypatch):
     row's result must not depend on it)."""
     q, s, wq, ws = _gemm_case(700, 1024, 1024, seed=11)
     outs = []
-    for config in range(21):
+    for config in range(22):
         monkeypatch.setenv("QUAIL_GEMM_CONFIG", str(config))
         outs.append(_run_gemm(q, s, wq, ws).cpu())
     for config, out in enumerate(outs):
@@ -127,12 +127,35 @@ def test_gemm_persistent_configs_with_several_tiles_per_workgroup(monkeypatch):
     configuration bit for bit, and the oracle to the bf16 tolerance."""
     q, s, wq, ws = _gemm_case(2125, 4096, 384, seed=13)
     outs = {}
-    for config in (10, 5, 16, 17, 18, 19, 20):
+    for config in (10, 5, 16, 17, 18, 19, 20, 21):
         monkeypatch.setenv("QUAIL_GEMM_CONFIG", str(config))
         outs[config] = _run_gemm(q, s, wq, ws).cpu()
-    for config in (5, 16, 17, 18, 19, 20):
+    for config in (5, 16, 17, 18, 19, 20, 21):
         assert torch.equal(outs[config], outs[10]), config
     _bf16_close(outs[16], ref.gemm(q, s, ref.RefLinear(wq, ws)))
+
+
+def test_gemm_configs_agree_with_zero_weight_blocks(monkeypatch):
+    """Weight blocks whose scale is 0 add nothing; configurations skip them
+    or run them on zero fragments, and all must agree bit for bit: zero
+    blocks at the first and last K block, two in a row, and a whole
+    128-row weight block column."""
+    q, s, wq, ws = _gemm_case(520, 768, 1024, seed=17)
+    ws = ws.clone()
+    ws[0, 0] = 0.0
+    ws[1, 7] = 0.0
+    ws[2, 3] = ws[2, 4] = 0.0
+    ws[5, :] = 0.0
+    outs = {}
+    for config in range(22):
+        if config in (0, 1, 3, 7, 10, 13, 14, 15, 16, 18, 19, 20, 21) and 768 % 256:
+            continue
+        monkeypatch.setenv("QUAIL_GEMM_CONFIG", str(config))
+        outs[config] = _run_gemm(q, s, wq, ws).cpu()
+    for config, out in outs.items():
+        assert torch.equal(out, outs[10]), config
+    _bf16_close(outs[10], ref.gemm(q, s, ref.RefLinear(wq, ws)))
+    assert torch.all(outs[10][:, 5 * 128:6 * 128] == 0)
 
 
 @pytest.mark.parametrize("m,i,k,zero_blocks", [(700, 768, 512, False), (333, 1536, 256, True),
