@@ -240,6 +240,80 @@ int qx_answer_head(const void* normed, int64_t n_ld, const void* rows, int64_t r
 int qx_prefix_tree(const int64_t* tokens, const int64_t* offsets, int64_t n,
                    int64_t page_tokens, int64_t* order, int64_t* parent, int64_t* shared);
 
+/*
+ * Host functions (no device work): page accounting of the paged KV arena.
+ * Replace PageArena (quail/backends/quail/executor/pages.py:8-275), which
+ * KVArena (arena.py:106-147,347-437,522-563) drives. A pool is an opaque
+ * handle; keys are caller-chosen int64 ids (> 0; the packer's temporary
+ * keys are < 0). Besides QX_OK / -1 (argument error), the calls return
+ * -2 for a key that is not resident and -3 for one that already is.
+ *
+ * qx_pages_create: num_pages pages of page_tokens tokens; the free stack
+ *   hands out 0, 1, 2, ... first (pages.py:26).
+ * qx_pages_alloc (pages.py:63-81): pages for ceil(capacity / page) minus the
+ *   borrowed ones; *allocated = their count, or -1 (nothing changed) when
+ *   the free stack is short.
+ * qx_pages_shared (pages.py:83-92): the parent's table pages holding its
+ *   tokens [start, shared), both multiples of the page.
+ * qx_pages_table: the key's table (borrowed, then owned pages) when cap
+ *   holds it, and info = {tokens, borrowed, owned, pinned, retained,
+ *   allocation order}.
+ * qx_pages_stats: {free pages, retained pages, resident tokens, retained
+ *   tokens, resident keys}.
+ * qx_pages_keys: the resident keys in allocation order.
+ * qx_pages_free_key / drop_leading / rewind / grow (pages.py:100-154):
+ *   *out = pages freed (grow: pages added, or -1 when short).
+ * qx_pages_pin / retain / pop_victim (pages.py:168-250): retained keys are
+ *   evicted lowest priority first, ties in retention order; the default
+ *   priority is tokens per page the key alone holds. victim = {found, key,
+ *   pages it alone held, tokens}; the victim stays resident.
+ * qx_pages_free_list: the free stack, bottom first.
+ */
+int qx_pages_create(int64_t num_pages, int64_t page_tokens, void** pool);
+int qx_pages_destroy(void* pool);
+int qx_pages_alloc(void* pool, int64_t key, int64_t tokens, int64_t capacity_tokens,
+                   const int32_t* borrowed, int64_t n_borrowed, int64_t* allocated);
+int qx_pages_shared(void* pool, int64_t parent, int64_t shared, int64_t start, int32_t* pages,
+                    int64_t cap, int64_t* n);
+int qx_pages_table(void* pool, int64_t key, int32_t* pages, int64_t cap, int64_t* info);
+int qx_pages_stats(void* pool, int64_t* stats);
+int qx_pages_keys(void* pool, int64_t* keys, int64_t cap, int64_t* n);
+int qx_pages_free_key(void* pool, int64_t key, int64_t* freed);
+int qx_pages_drop_leading(void* pool, int64_t key, int64_t pages, int64_t* freed);
+int qx_pages_rewind(void* pool, int64_t key, int64_t tokens, int64_t* freed);
+int qx_pages_grow(void* pool, int64_t key, int64_t capacity_tokens, int64_t* added);
+int qx_pages_set_tokens(void* pool, int64_t key, int64_t tokens);
+int qx_pages_pin(void* pool, int64_t key);
+int qx_pages_retain(void* pool, int64_t key, int has_priority, double priority);
+int qx_pages_pop_victim(void* pool, const int64_t* keep, int64_t n_keep, int64_t* victim);
+int qx_pages_free_list(void* pool, int32_t* pages, int64_t cap, int64_t* n);
+
+/*
+ * Host function (no device work): one pack of the unified causal path.
+ * Replaces pack_chunk with attention_mode="unified"
+ * (quail/backends/quail/executor/chunk.py:505-1160; group loop :606-684,
+ * unified pools :913-1054, _PoolBuilder :407-502). groups holds 8 int64 per
+ * group: {key, fresh, f, start, prefix tokens, suffixes, suffix tokens kept
+ * in the key's pages, every suffix row answers}; prefix_ids concatenates
+ * the fresh groups' prefixes, suffix_lens and suffix_ids every group's
+ * suffixes. A suffix that does not fit its key's pages gets a temporary key
+ * (id < 0) in `pool`. On success *pack holds the arrays until
+ * qx_pack_destroy; qx_pack_array(which) points at one of them:
+ *   0 input ids, 1 positions, 2 final rows, 3 cu_a (int32), 4 rows per
+ *   answer (empty unless some group answers on every row), 5 src, 6 dst,
+ *   7 tail_src, 8 tail_dst, 9 cu_q (int32), 10 used (int32), 11 block table
+ *   (int32, rows of `width`), 12 pages per sequence, 13 temporary keys,
+ *   14 (row0, prefix end, row1) per group, 15 suffixes per group, 16 fresh
+ *   keys, 17 {rows, max_q, max_used, multi-row, tail copies, width}.
+ * On failure nothing stays allocated and *failed_group names the group;
+ * -4 means the temporaries do not fit the free pages.
+ */
+int qx_pack_unified(void* pool, const int64_t* groups, int64_t n_groups,
+                    const int64_t* prefix_ids, const int64_t* suffix_lens,
+                    const int64_t* suffix_ids, void** pack, int64_t* failed_group);
+int qx_pack_array(void* pack, int64_t which, const void** data, int64_t* count);
+int qx_pack_destroy(void* pack);
+
 #ifdef __cplusplus
 }
 #endif

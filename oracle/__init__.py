@@ -9,4 +9,6 @@ Modules:
   fp8.py        e4m3fn rounding and per-token group quantization
   qwen3_ref.py  the torch fp32 "dequantized path" of the Qwen3 forward pass
   packing_ref.py brute-force checks of pack layouts (prefix tree, pages, KV reads)
+  pages_ref.py  the page accounting of the KV arena, in plain Python
+  pack_ref.py   the unified pack layout, in plain Python
 """

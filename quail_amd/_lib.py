@@ -46,6 +46,25 @@ SIGNATURES = {
                            _i64, _i64, _f32, _i32, _p, _p, _i64, _p, _i64, _p, _i64, _p],
     "qx_paged_attention_work": [_p, _p, _i64, _i64, _i64, _i64, _i32, _p, _i64],
     "qx_prefix_tree": [_p, _p, _i64, _i64, _p, _p, _p],
+    "qx_pages_create": [_i64, _i64, _p],
+    "qx_pages_destroy": [_p],
+    "qx_pages_alloc": [_p, _i64, _i64, _i64, _p, _i64, _p],
+    "qx_pages_shared": [_p, _i64, _i64, _i64, _p, _i64, _p],
+    "qx_pages_table": [_p, _i64, _p, _i64, _p],
+    "qx_pages_stats": [_p, _p],
+    "qx_pages_keys": [_p, _p, _i64, _p],
+    "qx_pages_free_key": [_p, _i64, _p],
+    "qx_pages_drop_leading": [_p, _i64, _i64, _p],
+    "qx_pages_rewind": [_p, _i64, _i64, _p],
+    "qx_pages_grow": [_p, _i64, _i64, _p],
+    "qx_pages_set_tokens": [_p, _i64, _i64],
+    "qx_pages_pin": [_p, _i64],
+    "qx_pages_retain": [_p, _i64, _i32, ctypes.c_double],
+    "qx_pages_pop_victim": [_p, _p, _i64, _p],
+    "qx_pages_free_list": [_p, _p, _i64, _p],
+    "qx_pack_unified": [_p, _p, _i64, _p, _p, _p, _p, _p],
+    "qx_pack_array": [_p, _i64, _p, _p],
+    "qx_pack_destroy": [_p],
     "qx_answer_head": [_p, _i64, _p, _i64, _i64, _i64, _i64, _i32, _p, _f32, _p, _p, _p, _p,
                        _p],
 }

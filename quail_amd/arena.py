@@ -46,7 +46,6 @@ class KVArena:
         # V pages hold fp16 (same 16-bit slots): the attention's PV product
         # runs in fp16, so V is converted once, when it is written
         self.v = [p.view(torch.float16).view(rows, heads, dim) for p in parts[1::2]]
-        self._capacity_rows = {}
         self._holds = {}
         self._deferred = set()
 
@@ -77,26 +76,23 @@ class KVArena:
     # ---- residency ---------------------------------------------------------
 
     def is_resident(self, key) -> bool:
-        return key in self.accounting.owned
+        return self.accounting.is_resident(key)
 
     def resident_keys(self):
-        return list(self.accounting.owned)
+        return self.accounting.resident_keys()
 
     def owned_pages(self, key) -> list:
         """The page ids the key's block table reads: borrowed, then its own."""
         return self.accounting.table_pages(key)
 
     def tokens(self, key) -> int:
-        return self.accounting.tokens[key]
-
-    def _refresh_rows(self, key):
-        pages = np.asarray(self.accounting.table_pages(key), dtype=np.int64)
-        t = self.page_tokens
-        self._capacity_rows[key] = (pages[:, None] * t + np.arange(t, dtype=np.int64)).reshape(-1)
+        return self.accounting.key_tokens(key)
 
     def capacity_rows(self, key) -> np.ndarray:
         """Pool row of every row in the key's pages, in logical order (host int64)."""
-        return self._capacity_rows[key]
+        pages = np.asarray(self.accounting.table_pages(key), dtype=np.int64)
+        t = self.page_tokens
+        return (pages[:, None] * t + np.arange(t, dtype=np.int64)).reshape(-1)
 
     # ---- allocation ----------------------------------------------------------
 
@@ -108,18 +104,14 @@ class KVArena:
 
     def can_borrow(self, parent, shared: int) -> bool:
         acct = self.accounting
-        return parent in acct.owned and shared <= acct.tokens[parent]
+        return acct.is_resident(parent) and shared <= acct.key_tokens(parent)
 
     def alloc(self, key, tokens: int, capacity_tokens=None, base_tokens=None, borrow=None):
         """Pages for a fresh key, or None when the free list is short.
         borrow = (parent key, shared tokens): the key reads the parent's
         first pages as its own leading pages."""
-        pages = self.accounting.alloc(key, tokens, capacity_tokens,
-                                      borrowed=self._borrow_plan(borrow))
-        if pages is None:
-            return None
-        self._refresh_rows(key)
-        return pages
+        return self.accounting.alloc(key, tokens, capacity_tokens,
+                                     borrowed=self._borrow_plan(borrow))
 
     def _evict_for_pages(self, need: int) -> None:
         acct = self.accounting
@@ -131,22 +123,20 @@ class KVArena:
             self.evicted_keys += 1
             self.evicted_prefix_tokens += tokens
             self.evicted_pages += acct.free_key(key)
-            self._capacity_rows.pop(key, None)
 
     def activate(self, key, tokens: int, capacity_tokens=None, base_tokens=None, borrow=None):
         """Make a prefix active (pinned), evicting retained KV when needed."""
         acct = self.accounting
         capacity = tokens if capacity_tokens is None else capacity_tokens
-        if key in acct.owned:
+        if acct.is_resident(key):
             acct.pin(key)
             need = max(0, acct.pages_needed(capacity) - len(acct.table_pages(key)))
             self._evict_for_pages(need)
             if need > acct.free_pages:
                 return None
             acct.grow(key, capacity)
-            acct.tokens[key] = tokens
-            self._refresh_rows(key)
-            return acct.owned[key]
+            acct.set_tokens(key, tokens)
+            return acct.owned_pages(key)
         borrowed = self._borrow_plan(borrow)
         self._evict_for_pages(acct.pages_needed(capacity) - len(borrowed))
         pages = self.alloc(key, tokens, capacity, base_tokens, borrow=borrow)
@@ -164,7 +154,6 @@ class KVArena:
         if self._holds.get(key):
             self._deferred.add(key)
             return 0
-        self._capacity_rows.pop(key, None)
         return self.accounting.free_key(key)
 
     def pin(self, key) -> None:
@@ -210,5 +199,5 @@ class KVArena:
 
     def block_table(self, keys, pad_to=None):
         table = self.block_table_rows([self.owned_pages(k) for k in keys], pad_to)
-        used = np.asarray([self.accounting.tokens[k] for k in keys], dtype=np.int32)
+        used = np.asarray([self.accounting.key_tokens(k) for k in keys], dtype=np.int32)
         return table, used

@@ -24,10 +24,13 @@ For the one paged causal attention call every group becomes sequences:
 Outputs match the reference's field for field: input_ids, positions,
 final_indices (last row of each suffix), cu_a, and meta["unified"] =
 {cu_q, used, table, src, dst, tail_src, tail_dst, max_q, max_used, causal,
-cu_q_host, used_host, page_rows}. Host arrays are numpy; `upload` moves
-them to the device in one pinned staging copy per array.
+cu_q_host, used_host, page_rows}. The layout is computed in C++
+(csrc/host_pack.cpp, qx_pack_unified) against the arena's page accounting,
+also C++; host arrays are numpy; `upload` moves them to the device in one
+pinned staging copy per array.
 """
 
+import ctypes
 import time
 from dataclasses import dataclass, field
 from typing import Any
@@ -69,147 +72,112 @@ def _cat(parts, dtype=np.int64):
     return np.concatenate(parts) if parts else np.empty(0, dtype=dtype)
 
 
+# qx_pack_array indices (include/quail_mi355x.h)
+(_IDS, _POSITIONS, _FINALS, _CU_A, _ROWS_PER_ANSWER, _SRC, _DST, _TAIL_SRC, _TAIL_DST, _CU_Q,
+ _USED, _TABLE, _SEQ_PAGES, _TEMPORARIES, _ROW_SPANS, _SUFFIX_COUNTS, _FRESH_KEYS,
+ _SCALARS) = range(18)
+_EFULL = -4
+
+
+def _pack_arrays(handle):
+    """Copy a qx_pack_unified result into numpy arrays (int32 where noted)."""
+    from quail_amd import _lib
+    lib = _lib.load()
+    data, count = ctypes.c_void_p(), ctypes.c_int64()
+    out = []
+    for which in range(18):
+        rc = lib.qx_pack_array(handle, which, ctypes.byref(data), ctypes.byref(count))
+        if rc:
+            raise _lib.QxError(f"qx_pack_array: {lib.qx_last_error().decode()}")
+        ctype = ctypes.c_int32 if which in (_CU_A, _CU_Q, _USED, _TABLE) else ctypes.c_int64
+        dtype = np.int32 if ctype is ctypes.c_int32 else np.int64
+        n = count.value
+        if n:
+            buf = (ctype * n).from_address(data.value)
+            out.append(np.frombuffer(buf, dtype=dtype).copy())
+        else:
+            out.append(np.empty(0, dtype=dtype))
+    return out
+
+
 def pack_chunk(arena, groups, *, attention_mode="unified", mask="causal", timing=None,
                attention_heads=None):
     """Pack groups for one unified causal forward pass (host arrays only).
+
+    The layout runs in C++ (qx_pack_unified) against the arena's page
+    accounting; this function flattens the groups, calls it, and wraps the
+    arrays.
 
     attention_heads: (HQ, HK, D) of the model; with it the attention
     metadata also carries the work list of the paged calls (one item per
     query tile that holds rows, heaviest first, qx_paged_attention_work).
 
     Raises ValueError for layouts this path does not run and ArenaFullError
-    when the suffixes' temporary pages do not fit (temporaries allocated so
-    far are freed first).
+    when the suffixes' temporary pages do not fit (nothing stays allocated).
     """
+    from quail_amd import _lib
+
     if attention_mode != "unified":
         raise ValueError("this engine packs the unified attention path")
     if mask != "causal":
         raise ValueError("this engine packs the causal mask")
     t0 = time.perf_counter()
-    id_parts, pos_parts, finals, cu_a = [], [], [], [0]
-    rows_per_answer, multi = [], False
-    layout, row_spans, fresh_keys, specs = [], [], [], []
-    n_tok = 0
+    acct = arena.accounting
+    keys, desc, prefixes, suffix_lens, suffix_ids = [], [], [], [], []
     for g in groups:
         key = g["key"]
-        fresh = g.get("prefix") is not None
-        f = int(g["f"])
-        start = int(g.get("start", 0))
-        paged = arena.is_resident(key)
-        if not paged:
+        if not acct.is_resident(key):
             raise ValueError(f"group {key!r}: the paged unified path needs arena pages")
-        row0 = n_tok
+        keys.append(key)
+        fresh = g.get("prefix") is not None
+        prefix = np.asarray(g["prefix"], dtype=np.int64) if fresh else None
         sids, slen = _as_suffixes(g["suffixes"])
-        n = len(slen)
         if fresh:
-            prefix = np.asarray(g["prefix"], dtype=np.int64)
-            id_parts.append(prefix)
-            pos_parts.append(np.arange(start, start + len(prefix), dtype=np.int64))
-            n_tok += len(prefix)
-            cu_a.append(n_tok)
-        prefix_end = n_tok
-        s_row0 = n_tok
-        read_all = bool(g.get("read_all_rows"))
-        total = int(slen.sum())
-        ends = np.cumsum(slen)
-        begins = ends - slen
-        if n:
-            id_parts.append(sids)
-            within = np.arange(total, dtype=np.int64) - np.repeat(begins, slen)
-            pos_parts.append(f + within)
-            cu_a.extend((s_row0 + ends).tolist())
-            if read_all:
-                finals.append(np.arange(s_row0, s_row0 + total, dtype=np.int64))
-                rows_per_answer.append(slen)
-                multi = True
-            else:
-                finals.append(s_row0 + ends - 1)
-                rows_per_answer.append(np.ones(n, dtype=np.int64))
-            n_tok += total
-        layout.append((key, n))
-        row_spans.append((key, row0, prefix_end, n_tok))
-        specs.append(dict(key=key, fresh=fresh, f=f, start=start, row0=row0,
-                          prefix_end=prefix_end, row1=n_tok,
-                          begins=s_row0 + begins, ends=s_row0 + ends,
-                          keeps=int(g.get("write_suffix_tokens") or 0)))
+            prefixes.append(prefix)
+        suffix_lens.append(slen)
+        suffix_ids.append(sids)
+        desc.append((acct.key_id(key), int(fresh), int(g["f"]), int(g.get("start", 0)),
+                     len(prefix) if fresh else 0, len(slen),
+                     int(g.get("write_suffix_tokens") or 0), int(bool(g.get("read_all_rows")))))
+    desc = np.asarray(desc, dtype=np.int64).reshape(-1, 8)
+    prefix_ids = _cat(prefixes)
+    lens = _cat(suffix_lens)
+    sids = _cat(suffix_ids)
     t1 = time.perf_counter()
 
-    page = arena.page_tokens
-    src, dst, tail_src, tail_dst = [], [], [], []
-    seq_pages, seq_used, cu_q = [], [], [0]
-    temporary_keys = []
+    lib = _lib.load()
+    handle, failed = ctypes.c_void_p(), ctypes.c_int64(-1)
+    ptr = lambda a: a.ctypes.data if a.size else None  # noqa: E731
+    rc = lib.qx_pack_unified(acct.handle, ptr(desc), len(desc), ptr(prefix_ids), ptr(lens),
+                             ptr(sids), ctypes.byref(handle), ctypes.byref(failed))
+    if rc:
+        msg = lib.qx_last_error().decode(errors="replace")
+        where = f"group {keys[failed.value]!r}: " if 0 <= failed.value < len(keys) else ""
+        if rc == _EFULL:
+            raise ArenaFullError(msg)
+        raise ValueError(where + msg)
     try:
-        for spec in specs:
-            key, f = spec["key"], spec["f"]
-            r0, r1 = spec["row0"], spec["row1"]
-            begins, ends = spec["begins"], spec["ends"]
-            logical = spec["start"] if spec["fresh"] else f
-            if spec["fresh"]:
-                fresh_keys.append(key)
-            count = r1 - r0
-            rows = arena.capacity_rows(key)
-            pages = arena.owned_pages(key)
-            suffix_total = int((ends - begins).sum())
-            direct = len(begins) == 1 and logical + count <= rows.size
-            if spec["keeps"] and not direct:
-                raise ValueError(f"group {key!r} keeps suffix KV but its pages hold "
-                                 f"{rows.size} rows, not {logical + count}")
-            if direct:
-                src.append(np.arange(r0, r1, dtype=np.int64))
-                dst.append(rows[logical:logical + count])
-                seq_pages.append(list(pages))
-                seq_used.append(f + suffix_total)
-                cu_q.append(cu_q[-1] + count)
-                continue
-            n_prefix = spec["prefix_end"] - r0
-            if n_prefix:
-                src.append(np.arange(r0, spec["prefix_end"], dtype=np.int64))
-                dst.append(rows[spec["start"]:spec["start"] + n_prefix])
-                seq_pages.append(list(pages[:arena.pages_needed(f)]))
-                seq_used.append(f)
-                cu_q.append(cu_q[-1] + n_prefix)
-            remainder = f % page
-            for s0, s1 in zip(begins.tolist(), ends.tolist()):
-                got = arena.alloc_temporary(remainder + (s1 - s0))
-                if got is None:
-                    raise ArenaFullError(
-                        f"unified suffix pages exceed the free KV arena (asked "
-                        f"{remainder + s1 - s0} rows, free pages {arena.free_pages})")
-                temp, _ = got
-                temporary_keys.append(temp)
-                trows = arena.capacity_rows(temp)
-                src.append(np.arange(s0, s1, dtype=np.int64))
-                dst.append(trows[remainder:remainder + (s1 - s0)])
-                if remainder:
-                    base = pages[f // page] * page
-                    tail_src.append(np.arange(base, base + remainder, dtype=np.int64))
-                    tail_dst.append(trows[:remainder])
-                seq_pages.append(list(pages[:f // page]) + arena.owned_pages(temp))
-                seq_used.append(f + (s1 - s0))
-                cu_q.append(cu_q[-1] + (s1 - s0))
-    except Exception:
-        for temp in temporary_keys:
-            arena.free_key(temp)
-        raise
-
-    used = np.asarray(seq_used, dtype=np.int32)
-    table = arena.block_table_rows(seq_pages) if seq_pages else np.zeros((0, 1), np.int32)
-    cu_q_arr = np.asarray(cu_q, dtype=np.int32)
+        (ids, positions, final, cu_a, rows_per_answer, src, dst, tail_src, tail_dst, cu_q, used,
+         table, seq_pages, temporaries, row_spans, suffix_counts, fresh_ids,
+         scalars) = _pack_arrays(handle)
+    finally:
+        lib.qx_pack_destroy(handle)
+    n_tok, max_q, max_used, multi, has_tail, width = (int(v) for v in scalars)
+    temporary_keys = tuple(acct.adopt(int(t)) for t in temporaries)
+    table = table.reshape(-1, width)
+    key_of = {acct.key_id(k): k for k in keys}
+    spans = row_spans.reshape(-1, 3).tolist()
     unified = dict(
-        src=_cat(src), dst=_cat(dst),
-        tail_src=_cat(tail_src) if tail_src else None,
-        tail_dst=_cat(tail_dst) if tail_dst else None,
-        used=used, table=table, cu_q=cu_q_arr, cu_q_host=list(cu_q),
-        used_host=used.tolist(), page_rows=seq_pages,
-        max_q=int(np.diff(cu_q_arr).max()) if len(cu_q) > 1 else 0,
-        max_used=int(used.max()) if len(used) else 0, causal=True)
-    cu_a_arr = np.asarray(cu_a, dtype=np.int32)
-    ids = _cat(id_parts)
-    positions = _cat(pos_parts)
-    final = _cat(finals)
-    meta = dict(layer=0, unified=unified, cu_a=cu_a_arr,
-                max_a=int(np.diff(cu_a_arr).max()) if len(cu_a) > 1 else 0,
-                final_query=_final_query(cu_q_arr, used, table, final))
+        src=src, dst=dst,
+        tail_src=tail_src if has_tail else None,
+        tail_dst=tail_dst if has_tail else None,
+        used=used, table=table, cu_q=cu_q, cu_q_host=cu_q.tolist(),
+        used_host=used.tolist(),
+        page_rows=[table[i, :c].tolist() for i, c in enumerate(seq_pages.tolist())],
+        max_q=max_q, max_used=max_used, causal=True)
+    meta = dict(layer=0, unified=unified, cu_a=cu_a,
+                max_a=int(np.diff(cu_a).max()) if len(cu_a) > 1 else 0,
+                final_query=_final_query(cu_q, used, table, final))
     if attention_heads is not None:
         for tables in (unified, meta["final_query"]):
             if tables is not None:
@@ -218,10 +186,12 @@ def pack_chunk(arena, groups, *, attention_mode="unified", mask="causal", timing
         timing["pack_py"] = timing.get("pack_py", 0.0) + (t1 - t0)
         timing["pack_unified"] = timing.get("pack_unified", 0.0) + (time.perf_counter() - t1)
     return Chunk(input_ids=ids, positions=positions, final_indices=final, meta=meta,
-                 attention_mode="unified", tokens=n_tok, layout=layout,
-                 row_spans=tuple(row_spans), temporary_keys=tuple(temporary_keys),
-                 fresh_keys=tuple(fresh_keys),
-                 rows_per_answer=np.concatenate(rows_per_answer) if multi else None,
+                 attention_mode="unified", tokens=n_tok,
+                 layout=list(zip(keys, suffix_counts.tolist())),
+                 row_spans=tuple((k, *span) for k, span in zip(keys, spans)),
+                 temporary_keys=temporary_keys,
+                 fresh_keys=tuple(key_of[int(i)] for i in fresh_ids),
+                 rows_per_answer=rows_per_answer if multi else None,
                  host_ids=ids, host_positions=positions)
 
 
