@@ -169,7 +169,9 @@ int qx_group_quant(const void* x, int64_t x_ld, void* q, int64_t q_ld, float* sc
  * even) as they are written; without it (the pool-to-pool tail copy) rows
  * are copied unchanged. Replaces the Triton kv_row_scatter
  * (attention.py:885-897) of Engine.kv_row_scatter / write_kv
- * (attention.py:1165-1195), including its pool-to-pool tail copy.
+ * (attention.py:1165-1195), including its pool-to-pool tail copy. With src
+ * and dst both NULL, row i goes to row i (a contiguous copy, V converted:
+ * the tree path's call A reads the pack's own rows that way).
  */
 int qx_kv_scatter(const void* k, int64_t k_ld, const void* v, int64_t v_ld, void* k_pool,
                   void* v_pool, const int64_t* src, const int64_t* dst, int64_t count,
@@ -211,6 +213,44 @@ int qx_paged_attention(const void* q, int64_t q_ld, const void* k_pool, const vo
 int64_t qx_paged_attention_work(const int* cu_q, const int* used, int64_t seqs, int64_t HQ,
                                 int64_t HK, int64_t D, int causal, int* work,
                                 int64_t capacity);
+
+/*
+ * The tree attention path's two calls (Engine.attention_tree,
+ * attention.py:1395-1441): each is flash_attn_varlen_func with
+ * return_softmax_lse=True (attention.py:1280-1306). Writes bf16 out
+ * (rows of o_ld elements, row i = query i in cu_q order) and
+ * lse[h*lse_ld + i] = ln(sum_j exp(scale * q_i . k_j)) (-inf for a row that
+ * sees no key).
+ *   table != NULL, cu_k == NULL: call B, keys [0, used[s]) read through the
+ *     block table as in qx_paged_attention (K bf16, V fp16 pools);
+ *   table == NULL, cu_k != NULL: call A, key j of sequence s is row
+ *     cu_k[s] + j of k (bf16) and v (fp16), rows of HK * D elements, and
+ *     used[s] <= cu_k[s+1] - cu_k[s].
+ * q_index (may be NULL): query i reads Q row q_index[i] (the reference's
+ * q3.index_select(0, reads["rows"]), without the copy). causal aligns
+ * bottom-right as in qx_paged_attention. work/n_work as there.
+ */
+int qx_attention_lse(const void* q, int64_t q_ld, const int64_t* q_index, const void* k,
+                     const void* v, const int* cu_q, const int* used, const int* table,
+                     int64_t table_ld, const int* cu_k, int64_t seqs, int64_t max_q,
+                     int64_t max_used, int64_t HQ, int64_t HK, int64_t D, float scale, int causal,
+                     void* out_bf16, int64_t o_ld, float* lse, int64_t lse_ld, const int* work,
+                     int64_t n_work, hipStream_t stream);
+
+/*
+ * Replaces Engine.merge_attn_quant / the merge_attn_quant Triton kernel
+ * (attention.py:902-948, QUANT on, UE8M0 off): for row t with
+ * source[t] >= 0, w = bf16(sigmoid(lb[h*lb_ld + source[t]] - la[h*la_ld + t])),
+ * y = bf16(a + (b[source[t]] - a) * w); otherwise y = a. Then per head
+ * (D == 128, one 128-group) scale = max(amax|y|, 1e-10) / 448 and
+ * e4m3(clamp(y / scale, +-448)) into q, scale into scales[h*s_ld + t].
+ * With scales == NULL (QUANT off, any D in {64, 128}) the bf16 y goes to q.
+ * q_ld is in elements of q; a, b, q rows hold HQ * D values.
+ */
+int qx_merge_attn_quant(const void* a, int64_t a_ld, const void* b, int64_t b_ld,
+                        const float* la, int64_t la_ld, const float* lb, int64_t lb_ld,
+                        const int* source, int64_t n, int64_t HQ, int64_t D, void* q,
+                        int64_t q_ld, float* scales, int64_t s_ld, hipStream_t stream);
 
 /*
  * Last-token answer head over the retained head rows (t <= 16):

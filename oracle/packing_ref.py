@@ -80,3 +80,54 @@ def check_pack(chunk, page, pool: PoolModel, prompt_of_key):
                                  f"{got[:4]}...{got[-2:]} (len {len(got)}), want len {len(want)}")
             checked += 1
     return checked
+
+
+def check_pack_tree(chunk, page, pool: PoolModel, prompt_of_key):
+    """The tree layout's reads (attention.py:1395-1441): the pack's KV writes
+    land in the pool first (kv_src -> kv_dst); a row then reads, in call B,
+    its reader sequence's `used` keys through that sequence's table (not
+    causal) when source[row] >= 0, and in call A the rows of its own cu_a
+    segment up to itself. Together, in that order, they must be exactly its
+    document's tokens at positions 0..its own position. Returns the number
+    of rows checked; raises AssertionError naming the first bad row."""
+    meta = chunk.meta
+    host = chunk.host or {}
+    ids = np.asarray(chunk.host_ids)
+    positions = np.asarray(chunk.host_positions)
+    kv_src = host.get("kv_src", meta.get("kv_src"))
+    kv_dst = host.get("kv_dst", meta.get("kv_dst"))
+    if kv_src is not None:
+        pool.apply(ids, positions, dict(src=kv_src, dst=kv_dst))
+    reads = host.get("reads", meta.get("reads"))
+    cu_a = np.asarray(host.get("segments", meta.get("segments"))["cu_q"], dtype=np.int64)
+    b_keys = {}
+    if reads is not None:
+        rows = np.asarray(reads["rows"], dtype=np.int64)
+        cu = np.asarray(reads["cu_q"], dtype=np.int64)
+        used = np.asarray(reads["used"], dtype=np.int64)
+        table = np.asarray(reads["table"], dtype=np.int64)
+        source = np.asarray(reads["source"], dtype=np.int64)
+        for s in range(len(used)):
+            keys = [pool.rows.get(int(table[s, j // page]) * page + j % page, ("unwritten", j))
+                    for j in range(int(used[s]))]
+            for i in range(int(cu[s]), int(cu[s + 1])):
+                b_keys[int(rows[i])] = keys
+        for r in range(len(ids)):
+            assert (source[r] >= 0) == (r in b_keys), f"row {r}: source map"
+            if source[r] >= 0:
+                assert rows[source[r]] == r, f"row {r}: source {source[r]}"
+    seg_of = np.searchsorted(cu_a, np.arange(len(ids)), side="right") - 1
+    checked = 0
+    for key, row0, _, row1 in chunk.row_spans:
+        prompt = list(prompt_of_key(key))
+        for r in range(row0, row1):
+            pos = int(positions[r])
+            assert ids[r] == prompt[pos], f"row {r}: token {ids[r]} != prompt[{pos}]"
+            a0 = int(cu_a[seg_of[r]])
+            got = list(b_keys.get(r, [])) + [(int(ids[j]), int(positions[j]))
+                                             for j in range(a0, r + 1)]
+            want = [(int(t), p) for p, t in enumerate(prompt[:pos + 1])]
+            assert got == want, (f"row {r} of {key!r} at position {pos} reads "
+                                 f"{got[:4]}...{got[-2:]} (len {len(got)}), want len {len(want)}")
+            checked += 1
+    return checked

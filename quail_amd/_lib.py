@@ -45,6 +45,10 @@ SIGNATURES = {
     "qx_paged_attention": [_p, _i64, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64,
                            _i64, _i64, _f32, _i32, _p, _p, _i64, _p, _i64, _p, _i64, _p],
     "qx_paged_attention_work": [_p, _p, _i64, _i64, _i64, _i64, _i32, _p, _i64],
+    "qx_attention_lse": [_p, _i64, _p, _p, _p, _p, _p, _p, _i64, _p, _i64, _i64, _i64, _i64,
+                         _i64, _i64, _f32, _i32, _p, _i64, _p, _i64, _p, _i64, _p],
+    "qx_merge_attn_quant": [_p, _i64, _p, _i64, _p, _i64, _p, _i64, _p, _i64, _i64, _i64, _p,
+                            _i64, _p, _i64, _p],
     "qx_prefix_tree": [_p, _p, _i64, _i64, _p, _p, _p],
     "qx_pages_create": [_i64, _i64, _p],
     "qx_pages_destroy": [_p],

@@ -148,6 +148,7 @@ class StageAdmission:
             self.admitted_order.append(d)
             room -= rows
             groups.append((d, dict(key=self.keys[d], prefix=prefix[shared:], f=f,
-                                   start=shared, suffixes=self.suffixes[d])))
+                                   start=shared, suffixes=self.suffixes[d],
+                                   borrow_key=None if borrow is None else borrow[0])))
         self.pending.extendleft(reversed(held))
         return groups

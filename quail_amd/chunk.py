@@ -117,10 +117,12 @@ def pack_chunk(arena, groups, *, attention_mode="unified", mask="causal", timing
     """
     from quail_amd import _lib
 
-    if attention_mode != "unified":
-        raise ValueError("this engine packs the unified attention path")
     if mask != "causal":
         raise ValueError("this engine packs the causal mask")
+    if attention_mode == "tree":
+        return _pack_tree(arena, groups, timing=timing, attention_heads=attention_heads)
+    if attention_mode != "unified":
+        raise ValueError(f"attention_mode must be 'unified' or 'tree', got {attention_mode!r}")
     t0 = time.perf_counter()
     acct = arena.accounting
     keys, desc, prefixes, suffix_lens, suffix_ids = [], [], [], [], []
@@ -192,6 +194,166 @@ def pack_chunk(arena, groups, *, attention_mode="unified", mask="causal", timing
                  temporary_keys=temporary_keys,
                  fresh_keys=tuple(key_of[int(i)] for i in fresh_ids),
                  rows_per_answer=rows_per_answer if multi else None,
+                 host_ids=ids, host_positions=positions)
+
+
+_TREE_UNSUPPORTED = ("canvas", "paths", "read_mask", "read_rows", "questions")
+
+
+def _pack_tree(arena, groups, *, timing=None, attention_heads=None):
+    """The tree attention layout (chunk.py:580-912, the reads of :1010-1054
+    and the KV writes of :1060-1079 with attention_mode="tree").
+
+    Call A is causal over the pack's own rows in `cu_a` segments: a fresh
+    group's prefix is a segment (unless the group is `whole`, one segment
+    with its suffix, or `stacked`), and each suffix is one. Call B reads
+    resident KV, not causally: a borrowing prefix reads its key's pages
+    before `start`; a suffix reads its key's pages [0, f); a stacked
+    group (one suffix, a `read_key`) reads the read key's pages before
+    `start` with all its rows, siblings with the same read key and start
+    in one sequence. Fresh rows of paged keys (and kept suffix rows) are
+    written to the key's pages first (kv_src -> kv_dst), so a later suffix
+    or a child can read them.
+    """
+    t0 = time.perf_counter()
+    id_parts, pos_parts, finals, cu_a = [], [], [], [0]
+    rows_per_answer, multi = [], False
+    layout, row_spans, fresh_keys = [], [], []
+    kv_writes, reader_rows, read_keys, read_used, cu_q = [], [], [], [], [0]
+    # the pages each read sequence goes through: its read key's table; a
+    # stacked run whose read key has left the arena (its last borrower was
+    # admitted) reads its first document's table, whose leading pages are
+    # the read key's borrowed ones
+    table_keys = []
+    max_q = 0
+    n_tok = 0
+    for g in groups:
+        key = g["key"]
+        for name in _TREE_UNSUPPORTED:
+            if g.get(name) is not None:
+                raise ValueError(f"group {key!r}: this engine has no {name} rows")
+        fresh = g.get("prefix") is not None
+        f = int(g["f"])
+        start = int(g.get("start", 0))
+        paged = arena.is_resident(key)
+        row0 = n_tok
+        sids, slen = _as_suffixes(g["suffixes"])
+        n = len(slen)
+        borrowing = fresh and start > 0
+        stacked = borrowing and n == 1 and g.get("read_key") is not None
+        whole = fresh and paged and not start and n == 1 and bool(g.get("single"))
+        prefix_len = 0
+        if fresh:
+            if not paged and n > 1:
+                raise ValueError(f"group {key!r}: an unpaged fresh group packs [prefix | suffix] "
+                                 f"as one causal segment, which only one suffix may join")
+            if start and not paged:
+                raise ValueError(f"group {key!r}: a borrowed prefix needs arena pages")
+            prefix = np.asarray(g["prefix"], dtype=np.int64)
+            prefix_len = len(prefix)
+            id_parts.append(prefix)
+            pos_parts.append(np.arange(start, start + prefix_len, dtype=np.int64))
+            n_tok += prefix_len
+            if (paged or not n) and not stacked and not whole:
+                cu_a.append(n_tok)
+            if borrowing and not stacked:
+                reader_rows.append(np.arange(row0, n_tok, dtype=np.int64))
+                cu_q.append(cu_q[-1] + prefix_len)
+                read_keys.append(key)
+                table_keys.append(key)
+                read_used.append(start)
+                max_q = max(max_q, prefix_len)
+            if paged:
+                kv_writes.append((key, row0, n_tok, start))
+                fresh_keys.append(key)
+        elif not paged:
+            raise ValueError(f"group {key!r}: a kept group needs its arena pages")
+        prefix_end = n_tok
+        s_row0 = n_tok
+        total = int(slen.sum())
+        ends = np.cumsum(slen)
+        begins = ends - slen
+        if n:
+            id_parts.append(sids)
+            within = np.arange(total, dtype=np.int64) - np.repeat(begins, slen)
+            pos_parts.append(f + within)
+            if g.get("read_all_rows"):
+                finals.append(np.arange(s_row0, s_row0 + total, dtype=np.int64))
+                rows_per_answer.append(slen)
+                multi = True
+            else:
+                finals.append(s_row0 + ends - 1)
+                rows_per_answer.append(np.ones(n, dtype=np.int64))
+            cu_a.extend((s_row0 + ends).tolist())
+            n_tok += total
+            keep = int(g.get("write_suffix_tokens") or 0)
+            if keep and paged:
+                kv_writes.append((key, s_row0, s_row0 + keep, start + prefix_len if fresh else f))
+        num_s = n_tok - s_row0
+        layout.append((key, n))
+        row_spans.append((key, row0, prefix_end, n_tok))
+        if stacked:
+            count = n_tok - row0
+            reader_rows.append(np.arange(row0, n_tok, dtype=np.int64))
+            read_key = g["read_key"]
+            if read_keys and read_keys[-1] == read_key and read_used[-1] == start:
+                cu_q[-1] += count
+                max_q = max(max_q, cu_q[-1] - cu_q[-2])
+            else:
+                cu_q.append(cu_q[-1] + count)
+                read_keys.append(read_key)
+                table_keys.append(read_key if arena.is_resident(read_key) else key)
+                read_used.append(start)
+                max_q = max(max_q, count)
+        elif num_s and f and paged and not whole:
+            reader_rows.append(np.arange(s_row0, n_tok, dtype=np.int64))
+            cu_q.append(cu_q[-1] + num_s)
+            read_keys.append(key)
+            table_keys.append(key)
+            read_used.append(f)
+            max_q = max(max_q, num_s)
+    t1 = time.perf_counter()
+
+    reads = None
+    if read_keys:
+        table = arena.block_table_rows([arena.owned_pages(k) for k in table_keys])
+        rows = _cat(reader_rows)
+        source = np.full(n_tok, -1, dtype=np.int32)
+        source[rows] = np.arange(len(rows), dtype=np.int32)
+        used = np.asarray(read_used, dtype=np.int32)
+        reads = dict(rows=rows, cu_q=np.asarray(cu_q, dtype=np.int32), max_q=max_q, used=used,
+                     max_used=int(used.max()), table=table, source=source, causal=False)
+    kv_src = kv_dst = None
+    if kv_writes:
+        src, dst = [], []
+        for key, r0, r1, dest in kv_writes:
+            rows = arena.capacity_rows(key)[dest:dest + (r1 - r0)]
+            if len(rows) != r1 - r0:
+                raise ValueError(f"group {key!r}: KV write of {r1 - r0} rows at {dest} exceeds "
+                                 f"its reserved rows")
+            src.append(np.arange(r0, r1, dtype=np.int64))
+            dst.append(rows)
+        kv_src, kv_dst = _cat(src), _cat(dst)
+    cu_a_arr = np.asarray(cu_a, dtype=np.int32)
+    segments = dict(cu_q=cu_a_arr, used=np.diff(cu_a_arr).astype(np.int32),
+                    max_q=int(np.diff(cu_a_arr).max()) if len(cu_a) > 1 else 0, causal=True)
+    segments["max_used"] = segments["max_q"]
+    if attention_heads is not None:
+        for tables in (segments, reads):
+            if tables is not None:
+                tables["work"], tables["n_work"] = _work_list(tables, attention_heads)
+    ids = _cat(id_parts)
+    positions = _cat(pos_parts)
+    final = _cat(finals)
+    meta = dict(layer=0, unified=None, kv_src=kv_src, kv_dst=kv_dst, reads=reads,
+                segments=segments, cu_a=cu_a_arr, max_a=segments["max_q"])
+    if timing is not None:
+        timing["pack_py"] = timing.get("pack_py", 0.0) + (t1 - t0)
+        timing["pack_reads"] = timing.get("pack_reads", 0.0) + (time.perf_counter() - t1)
+    return Chunk(input_ids=ids, positions=positions, final_indices=final, meta=meta,
+                 attention_mode="tree", tokens=n_tok, layout=layout, row_spans=tuple(row_spans),
+                 fresh_keys=tuple(fresh_keys),
+                 rows_per_answer=np.concatenate(rows_per_answer) if multi else None,
                  host_ids=ids, host_positions=positions)
 
 
@@ -268,10 +430,12 @@ class InputStaging:
 def upload(chunk: Chunk, staging: InputStaging) -> Chunk:
     """Move a packed chunk's index arrays to the device (int64 ids/rows, int32 tables)."""
     import torch
-    u = chunk.meta["unified"]
     chunk.input_ids = staging.copy("tokens", chunk.host_ids, torch.int64)
     chunk.positions = staging.copy("positions", chunk.host_positions, torch.int64)
     chunk.final_indices = staging.copy("finals", chunk.final_indices, torch.int64)
+    if chunk.attention_mode == "tree":
+        return _upload_tree(chunk, staging)
+    u = chunk.meta["unified"]
     dev = dict(u)
     dev["src"] = staging.copy("unified_src", u["src"], torch.int64)
     dev["dst"] = staging.copy("unified_dst", u["dst"], torch.int64)
@@ -296,4 +460,32 @@ def upload(chunk: Chunk, staging: InputStaging) -> Chunk:
             chunk.meta["final_query"]["work"] = staging.copy("final_work", fq["work"],
                                                              torch.int32)
     chunk.meta["cu_a"] = staging.copy("cu_a", chunk.meta["cu_a"], torch.int32)
+    return chunk
+
+
+def _upload_tree(chunk: Chunk, staging: InputStaging) -> Chunk:
+    import torch
+    meta = chunk.meta
+    chunk.host["segments"], chunk.host["reads"] = meta["segments"], meta["reads"]
+    chunk.host["kv_src"], chunk.host["kv_dst"] = meta["kv_src"], meta["kv_dst"]
+    if meta["kv_src"] is not None:
+        meta["kv_src"] = staging.copy("kv_src", meta["kv_src"], torch.int64)
+        meta["kv_dst"] = staging.copy("kv_dst", meta["kv_dst"], torch.int64)
+    seg = meta["segments"]
+    dev = dict(seg, cu_q=staging.copy("cu_a", seg["cu_q"], torch.int32),
+               used=staging.copy("segment_lengths", seg["used"], torch.int32))
+    if seg.get("work") is not None and seg["n_work"]:
+        dev["work"] = staging.copy("segment_work", seg["work"], torch.int32)
+    meta["segments"] = dev
+    meta["cu_a"] = dev["cu_q"]
+    reads = meta["reads"]
+    if reads is not None:
+        dev = dict(reads, rows=staging.copy("read_rows", reads["rows"], torch.int64),
+                   cu_q=staging.copy("read_cu_q", reads["cu_q"], torch.int32),
+                   used=staging.copy("read_used", reads["used"], torch.int32),
+                   table=staging.copy("read_table", reads["table"], torch.int32),
+                   source=staging.copy("read_source", reads["source"], torch.int32))
+        if reads.get("work") is not None and reads["n_work"]:
+            dev["work"] = staging.copy("read_work", reads["work"], torch.int32)
+        meta["reads"] = dev
     return chunk

@@ -65,14 +65,18 @@ __device__ __forceinline__ int kswz(int key) { return D == 128 ? (key & 15) : ((
 template <int D>
 __device__ __forceinline__ int vswz(int key) { return D == 128 ? ((key & 3) << 2) : (((key >> 1) & 1) << 2); }
 
-template <int D, int HPB, int QSUB, bool QUANT>
+// CONTIG: keys are contiguous rows, key j of sequence s at row cu_k[s] + j
+// (no block table). q_index (optional): query row i reads Q row q_index[i].
+// lse (optional): lse[h * lse_ld + i] = ln(sum_j exp(scale * s_ij)) of row i.
+template <int D, int HPB, int QSUB, bool QUANT, bool CONTIG>
 __global__ __launch_bounds__(HPB * QSUB * 64) void paged_attention_kernel(
-    const uint16_t* __restrict__ q, int64_t q_ld, const uint16_t* __restrict__ kp,
-    const uint16_t* __restrict__ vp, const int* __restrict__ cu_q, const int* __restrict__ used,
-    const int* __restrict__ table, int64_t table_ld, int max_used, int HQ, int HK,
+    const uint16_t* __restrict__ q, int64_t q_ld, const int64_t* __restrict__ q_index,
+    const uint16_t* __restrict__ kp, const uint16_t* __restrict__ vp,
+    const int* __restrict__ cu_q, const int* __restrict__ used, const int* __restrict__ table,
+    int64_t table_ld, const int* __restrict__ cu_k, int max_used, int HQ, int HK,
     float scale_log2, int causal, uint16_t* __restrict__ out16, uint8_t* __restrict__ out8,
-    int64_t o_ld, float* __restrict__ scales, int64_t s_ld, const int* __restrict__ work,
-    int zgroups, int seqs) {
+    int64_t o_ld, float* __restrict__ scales, int64_t s_ld, float* __restrict__ lse,
+    int64_t lse_ld, const int* __restrict__ work, int zgroups, int seqs) {
   constexpr int NW = HPB * QSUB;
   constexpr int NT = NW * 64;
   constexpr int BQ = 32 * QSUB;  // query rows per workgroup
@@ -132,15 +136,21 @@ __global__ __launch_bounds__(HPB * QSUB * 64) void paged_attention_kernel(
   const int ntiles = (kv_end + kBK - 1) / kBK;
 
   // stage the page-table row
-  const int* trow = table + (int64_t)s * table_ld;
-  const int npages = (kv_end + kPage - 1) / kPage;
-  for (int i = tid; i < npages; i += NT) pages_lds[i] = trow[i];
+  int kv0 = 0;
+  if (CONTIG) {
+    kv0 = cu_k[s];
+  } else {
+    const int* trow = table + (int64_t)s * table_ld;
+    const int npages = (kv_end + kPage - 1) / kPage;
+    for (int i = tid; i < npages; i += NT) pages_lds[i] = trow[i];
+  }
 
   // Q^T fragments (B operand): lane holds query `col`, d = c*16 + half*8 .. +8
   v8s qf[ND16];
   {
     const int rr = r_ok ? r : q_len - 1;
-    const uint16_t* qrow = q + (int64_t)(q0 + rr) * q_ld + head * D;
+    const int64_t qr = q_index ? q_index[q0 + rr] : (int64_t)(q0 + rr);
+    const uint16_t* qrow = q + qr * q_ld + head * D;
 #pragma unroll
     for (int c = 0; c < ND16; ++c) qf[c] = *reinterpret_cast<const v8s*>(qrow + c * 16 + half * 8);
     // consume the Q fragments here, before any KV load is issued: the
@@ -168,7 +178,8 @@ __global__ __launch_bounds__(HPB * QSUB * 64) void paged_attention_kernel(
       const int p = lane % KCH;
       int kidx = t * kBK + key;
       kidx = kidx < kv_end ? kidx : kv_end - 1;
-      const int64_t prow = (int64_t)pages_lds[kidx / kPage] * kPage + (kidx % kPage);
+      const int64_t prow = CONTIG ? (int64_t)kv0 + kidx
+                                  : (int64_t)pages_lds[kidx / kPage] * kPage + (kidx % kPage);
       if (v) {
         lds_dma16(vbase + prow * kv_row + (p ^ vswz<D>(key)) * 8, v_buf(buf) + slab * 1024);
       } else {
@@ -338,6 +349,12 @@ __global__ __launch_bounds__(HPB * QSUB * 64) void paged_attention_kernel(
   // ---- epilogue: lane holds query `col`, d = dt*32 + (i/4)*8 + half*4 + i%4
   const float inv = l_run > 0.f ? 1.0f / l_run : 0.f;
   const int64_t row = q0 + r;
+  if (lse && r_ok && half == 0) {
+    // p was kept against m_run: ln(sum exp(scale * s)) = ln 2 * (log2 l + m_run * scale_log2)
+    const float m_use = m_run == -INFINITY ? 0.f : m_run * scale_log2;
+    lse[(int64_t)head * lse_ld + row] =
+        l_run > 0.f ? (__log2f(l_run) + m_use) * 0.6931471805599453f : -INFINITY;
+  }
   if (QUANT) {
     float amax = 0.f;
 #pragma unroll
@@ -379,10 +396,11 @@ __global__ __launch_bounds__(HPB * QSUB * 64) void paged_attention_kernel(
 }
 
 template <int D, int HPB, int QSUB>
-int launch_attn(const void* q, int64_t q_ld, const void* kp, const void* vp, const int* cu_q,
-                const int* used, const int* table, int64_t table_ld, int seqs, int max_q,
-                int max_used, int HQ, int HK, int page, float scale, int causal, void* out16,
-                void* out8, int64_t o_ld, float* scales, int64_t s_ld, const int* work,
+int launch_attn(const void* q, int64_t q_ld, const int64_t* q_index, const void* kp,
+                const void* vp, const int* cu_q, const int* used, const int* table,
+                int64_t table_ld, const int* cu_k, int seqs, int max_q, int max_used, int HQ,
+                int HK, int page, float scale, int causal, void* out16, void* out8, int64_t o_ld,
+                float* scales, int64_t s_ld, float* lse, int64_t lse_ld, const int* work,
                 int n_work, hipStream_t stream) {
   const int G = HQ / HK;
   constexpr int BQ = 32 * QSUB;
@@ -390,20 +408,92 @@ int launch_attn(const void* q, int64_t q_ld, const void* kp, const void* vp, con
   dim3 grid = work ? dim3((unsigned)n_work * zgroups, 1, 1)
                    : dim3((max_q + BQ - 1) / BQ, seqs, zgroups);
   const float scale_log2 = scale * 1.4426950408889634f;
+  const dim3 block(HPB * QSUB * 64);
+  const uint16_t* q16 = (const uint16_t*)q;
+  const uint16_t* k16 = (const uint16_t*)kp;
+  const uint16_t* v16 = (const uint16_t*)vp;
   if (out8) {
-    hipLaunchKernelGGL((paged_attention_kernel<D, HPB, QSUB, true>), grid, dim3(HPB * QSUB * 64),
-                       0, stream, (const uint16_t*)q, q_ld, (const uint16_t*)kp,
-                       (const uint16_t*)vp, cu_q, used, table, table_ld, max_used, HQ, HK,
-                       scale_log2, causal, nullptr, (uint8_t*)out8, o_ld, scales, s_ld, work,
-                       zgroups, seqs);
+    hipLaunchKernelGGL((paged_attention_kernel<D, HPB, QSUB, true, false>), grid, block, 0,
+                       stream, q16, q_ld, q_index, k16, v16, cu_q, used, table, table_ld, cu_k,
+                       max_used, HQ, HK, scale_log2, causal, nullptr, (uint8_t*)out8, o_ld,
+                       scales, s_ld, lse, lse_ld, work, zgroups, seqs);
+  } else if (cu_k) {
+    hipLaunchKernelGGL((paged_attention_kernel<D, HPB, QSUB, false, true>), grid, block, 0,
+                       stream, q16, q_ld, q_index, k16, v16, cu_q, used, table, table_ld, cu_k,
+                       max_used, HQ, HK, scale_log2, causal, (uint16_t*)out16, nullptr, o_ld,
+                       nullptr, 0, lse, lse_ld, work, zgroups, seqs);
   } else {
-    hipLaunchKernelGGL((paged_attention_kernel<D, HPB, QSUB, false>), grid, dim3(HPB * QSUB * 64),
-                       0, stream, (const uint16_t*)q, q_ld, (const uint16_t*)kp,
-                       (const uint16_t*)vp, cu_q, used, table, table_ld, max_used, HQ, HK,
-                       scale_log2, causal, (uint16_t*)out16, nullptr, o_ld, nullptr, 0, work,
-                       zgroups, seqs);
+    hipLaunchKernelGGL((paged_attention_kernel<D, HPB, QSUB, false, false>), grid, block, 0,
+                       stream, q16, q_ld, q_index, k16, v16, cu_q, used, table, table_ld, cu_k,
+                       max_used, HQ, HK, scale_log2, causal, (uint16_t*)out16, nullptr, o_ld,
+                       nullptr, 0, lse, lse_ld, work, zgroups, seqs);
   }
   QX_LAUNCH_STATUS();
+}
+
+// The tree path's merge (attention.py:902-948, merge_attn_quant with QUANT):
+// row t's result from call A (its own segment) and, when source[t] >= 0,
+// row source[t] of call B (its reads of resident pages) are combined by
+// their log-sum-exps, w = bf16(sigmoid(lse_b - lse_a)),
+// y = bf16(a + (b - a) * w), and y is quantized per head to e4m3 with
+// scale max(amax, 1e-10) / 448, as the o_proj input (QUANT, D = 128), or
+// stored as bf16 (QUANT off). One wave per (row, 512 columns): each lane
+// holds 8 consecutive values of one head.
+template <bool QUANT>
+__global__ __launch_bounds__(256) void merge_attn_quant_kernel(
+    const uint16_t* __restrict__ a, int64_t a_ld, const uint16_t* __restrict__ b, int64_t b_ld,
+    const float* __restrict__ la, int64_t la_ld, const float* __restrict__ lb, int64_t lb_ld,
+    const int* __restrict__ source, uint8_t* __restrict__ q, int64_t q_ld,
+    float* __restrict__ scales, int64_t s_ld, int n, int width, int blocks, int D) {
+  const int lane = threadIdx.x & 63;
+  const int wid = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (wid >= n * blocks) return;
+  const int row = wid / blocks;
+  const int col = (wid % blocks) * 512 + lane * 8;
+  if (col >= width) return;  // whole heads leave together
+  const int head = col / D;
+  const int src = source[row];
+  float y[8];
+  const uint4 av = *reinterpret_cast<const uint4*>(a + (int64_t)row * a_ld + col);
+  const uint32_t aw[4] = {av.x, av.y, av.z, av.w};
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    y[2 * k] = lo_bf16(aw[k]);
+    y[2 * k + 1] = hi_bf16(aw[k]);
+  }
+  if (src >= 0) {
+    const float x = lb[(int64_t)head * lb_ld + src] - la[(int64_t)head * la_ld + row];
+    const float w = round_bf16(1.0f / (1.0f + expf(-x)));
+    const uint4 bv = *reinterpret_cast<const uint4*>(b + (int64_t)src * b_ld + col);
+    const uint32_t bw[4] = {bv.x, bv.y, bv.z, bv.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      y[2 * k] = round_bf16(fmaf(lo_bf16(bw[k]) - y[2 * k], w, y[2 * k]));
+      y[2 * k + 1] = round_bf16(fmaf(hi_bf16(bw[k]) - y[2 * k + 1], w, y[2 * k + 1]));
+    }
+  }
+  if (!QUANT) {
+    uint4 o;
+    o.x = pack2_bf16(y[0], y[1]);
+    o.y = pack2_bf16(y[2], y[3]);
+    o.z = pack2_bf16(y[4], y[5]);
+    o.w = pack2_bf16(y[6], y[7]);
+    *reinterpret_cast<uint4*>(q + ((int64_t)row * q_ld + col) * 2) = o;
+    return;
+  }
+  float amax = 0.f;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) amax = fmaxf(amax, fabsf(y[k]));
+  amax = group_max<16>(amax);
+  const float scale = fp8_scale(amax);
+  const float rs = recip(scale);
+  uint2 o;
+  o.x = pack4_fp8(div_by(y[0], scale, rs), div_by(y[1], scale, rs), div_by(y[2], scale, rs),
+                  div_by(y[3], scale, rs));
+  o.y = pack4_fp8(div_by(y[4], scale, rs), div_by(y[5], scale, rs), div_by(y[6], scale, rs),
+                  div_by(y[7], scale, rs));
+  *reinterpret_cast<uint2*>(q + (int64_t)row * q_ld + col) = o;
+  if ((lane & 15) == 0) scales[(int64_t)head * s_ld + row] = scale;
 }
 
 // Query rows per workgroup of the configuration dispatched for (D, G):
@@ -417,7 +507,56 @@ inline int attn_query_tile(int64_t D, int64_t G) {
 }  // namespace
 }  // namespace qx
 
+namespace qx {
+namespace {
+
+int attention_impl(const void* q, int64_t q_ld, const int64_t* q_index, const void* k_pool,
+                   const void* v_pool, const int* cu_q, const int* used, const int* table,
+                   int64_t table_ld, const int* cu_k, int64_t seqs, int64_t max_q,
+                   int64_t max_used, int64_t HQ, int64_t HK, int64_t D, int64_t page, float scale,
+                   int causal, void* out_bf16, void* out_fp8, int64_t o_ld, float* scales,
+                   int64_t s_ld, float* lse, int64_t lse_ld, const int* work, int64_t n_work,
+                   hipStream_t stream) {
+  QX_CHECK(q && k_pool && v_pool && cu_q && used && (table || cu_k), "attention: null pointer");
+  QX_CHECK(out_bf16 || out_fp8, "attention: no output");
+  QX_CHECK(!(out_fp8 && (cu_k || lse || q_index)), "attention: fused quant is for the paged call");
+  QX_CHECK(D == 64 || D == 128, "attention: head_dim %lld", (long long)D);
+  QX_CHECK(HQ > 0 && HK > 0 && HQ % HK == 0, "attention: heads %lld/%lld", (long long)HQ,
+           (long long)HK);
+  QX_CHECK(page == kPage, "attention: page of %lld tokens (the arena uses 16)", (long long)page);
+  QX_CHECK(max_used >= 0 && (cu_k || max_used <= (int64_t)kMaxPages * page),
+           "attention: max_used %lld exceeds %d pages", (long long)max_used, kMaxPages);
+  QX_CHECK(q_ld % 8 == 0 && o_ld % 4 == 0, "attention: strides");
+  QX_CHECK(!out_fp8 || (D == 128 && scales), "attention: fused quant needs D=128 and scales");
+  QX_CHECK(seqs < 65536, "attention: %lld sequences exceed the grid", (long long)seqs);
+  QX_CHECK(!work || (n_work >= 0 && n_work * HK * 8 < (1LL << 31)), "attention: work items");
+  if (seqs == 0 || max_q == 0 || (work && n_work == 0)) return QX_OK;
+  const int G = (int)(HQ / HK);
+  const int hpb = G % 4 == 0 ? 4 : (G % 2 == 0 ? 2 : 1);
+  const int args_seqs = (int)seqs, args_mq = (int)max_q, args_mu = (int)max_used;
+#define QX_ATTN(DD, HPB_, QS_)                                                                 \
+  return launch_attn<DD, HPB_, QS_>(q, q_ld, q_index, k_pool, v_pool, cu_q, used, table,       \
+                                    table_ld, cu_k, args_seqs, args_mq, args_mu, (int)HQ,      \
+                                    (int)HK, (int)page, scale, causal, out_bf16, out_fp8,      \
+                                    o_ld, scales, s_ld, lse, lse_ld, work, (int)n_work,        \
+                                    stream)
+  if (D == 128) {
+    if (hpb == 4) QX_ATTN(128, 4, 2);
+    if (hpb == 2) QX_ATTN(128, 2, 4);
+    QX_ATTN(128, 1, 8);
+  } else {
+    if (hpb == 4) QX_ATTN(64, 4, 2);
+    if (hpb == 2) QX_ATTN(64, 2, 4);
+    QX_ATTN(64, 1, 8);
+  }
+#undef QX_ATTN
+}
+
+}  // namespace
+}  // namespace qx
+
 extern "C" {
+
 
 // out_fp8 != NULL: write the e4m3 o_proj input and its scales (D must be
 // 128); otherwise write bf16 to out_bf16. o_ld is in elements of the output.
@@ -429,37 +568,62 @@ int qx_paged_attention(const void* q, int64_t q_ld, const void* k_pool, const vo
                        int64_t D, int64_t page, float scale, int causal, void* out_bf16,
                        void* out_fp8, int64_t o_ld, float* scales, int64_t s_ld,
                        const int* work, int64_t n_work, hipStream_t stream) {
-  QX_CHECK(q && k_pool && v_pool && cu_q && used && table, "attention: null pointer");
-  QX_CHECK(out_bf16 || out_fp8, "attention: no output");
-  QX_CHECK(D == 64 || D == 128, "attention: head_dim %lld", (long long)D);
-  QX_CHECK(HQ > 0 && HK > 0 && HQ % HK == 0, "attention: heads %lld/%lld", (long long)HQ,
-           (long long)HK);
-  QX_CHECK(page == qx::kPage, "attention: page of %lld tokens (the arena uses 16)", (long long)page);
-  QX_CHECK(max_used >= 0 && max_used <= (int64_t)qx::kMaxPages * page,
-           "attention: max_used %lld exceeds %d pages", (long long)max_used, qx::kMaxPages);
-  QX_CHECK(q_ld % 8 == 0 && o_ld % 4 == 0, "attention: strides");
-  QX_CHECK(!out_fp8 || (D == 128 && scales), "attention: fused quant needs D=128 and scales");
-  QX_CHECK(seqs < 65536, "attention: %lld sequences exceed the grid", (long long)seqs);
-  QX_CHECK(!work || (n_work >= 0 && n_work * HK * 8 < (1LL << 31)), "attention: work items");
-  if (seqs == 0 || max_q == 0 || (work && n_work == 0)) return QX_OK;
-  const int G = (int)(HQ / HK);
-  const int hpb = G % 4 == 0 ? 4 : (G % 2 == 0 ? 2 : 1);
-  const int args_seqs = (int)seqs, args_mq = (int)max_q, args_mu = (int)max_used;
-#define QX_ATTN(DD, HPB_, QS_)                                                                  \
-  return qx::launch_attn<DD, HPB_, QS_>(q, q_ld, k_pool, v_pool, cu_q, used, table, table_ld,   \
-                                        args_seqs, args_mq, args_mu, (int)HQ, (int)HK,          \
-                                        (int)page, scale, causal, out_bf16, out_fp8, o_ld,      \
-                                        scales, s_ld, work, (int)n_work, stream)
-  if (D == 128) {
-    if (hpb == 4) QX_ATTN(128, 4, 2);
-    if (hpb == 2) QX_ATTN(128, 2, 4);
-    QX_ATTN(128, 1, 8);
+  QX_CHECK(table, "attention: null pointer");
+  return qx::attention_impl(q, q_ld, nullptr, k_pool, v_pool, cu_q, used, table, table_ld,
+                            nullptr, seqs, max_q, max_used, HQ, HK, D, page, scale, causal,
+                            out_bf16, out_fp8, o_ld, scales, s_ld, nullptr, 0, work, n_work,
+                            stream);
+}
+
+// The tree path's two calls: bf16 output plus each row's log-sum-exp.
+// table != NULL: paged keys as in qx_paged_attention; table == NULL: key j
+// of sequence s is row cu_k[s] + j of k and v (rows of HK * D elements, V
+// fp16). q_index (may be NULL): query row i reads Q row q_index[i].
+int qx_attention_lse(const void* q, int64_t q_ld, const int64_t* q_index, const void* k,
+                     const void* v, const int* cu_q, const int* used, const int* table,
+                     int64_t table_ld, const int* cu_k, int64_t seqs, int64_t max_q,
+                     int64_t max_used, int64_t HQ, int64_t HK, int64_t D, float scale, int causal,
+                     void* out_bf16, int64_t o_ld, float* lse, int64_t lse_ld, const int* work,
+                     int64_t n_work, hipStream_t stream) {
+  QX_CHECK(out_bf16 && lse, "attention_lse: null output");
+  QX_CHECK((table == nullptr) != (cu_k == nullptr), "attention_lse: give a table or cu_k");
+  return qx::attention_impl(q, q_ld, q_index, k, v, cu_q, used, table, table_ld, cu_k, seqs,
+                            max_q, max_used, HQ, HK, D, qx::kPage, scale, causal, out_bf16,
+                            nullptr, o_ld, nullptr, 0, lse, lse_ld, work, n_work, stream);
+}
+
+// The tree path's LSE merge fused with the o_proj input quantization
+// (attention.py:902-948): a (n, HQ*D) bf16 from the segment call with
+// lse_a at la[h*la_ld + t], b (rows, HQ*D) bf16 from the resident-page call
+// with lse_b at lb[h*lb_ld + j], source[t] = row of b for row t or -1.
+// scales != NULL: writes e4m3 (n, HQ*D) to q and scales[h*s_ld + t]
+// (D == 128, one quant group per head); scales == NULL: writes the bf16
+// merge to q (q_ld in elements of either).
+int qx_merge_attn_quant(const void* a, int64_t a_ld, const void* b, int64_t b_ld,
+                        const float* la, int64_t la_ld, const float* lb, int64_t lb_ld,
+                        const int* source, int64_t n, int64_t HQ, int64_t D, void* q,
+                        int64_t q_ld, float* scales, int64_t s_ld, hipStream_t stream) {
+  QX_CHECK(a && la && source && q, "merge_attn_quant: null pointer");
+  QX_CHECK((D == 64 || D == 128) && HQ > 0, "merge_attn_quant: heads %lld x %lld",
+           (long long)HQ, (long long)D);
+  QX_CHECK(!scales || D == 128, "merge_attn_quant: the fused quant needs one head per group");
+  QX_CHECK(a_ld % 8 == 0 && b_ld % 8 == 0 && q_ld % 8 == 0, "merge_attn_quant: strides");
+  QX_CHECK(la_ld >= n && (!scales || s_ld >= n), "merge_attn_quant: lse / scale strides");
+  if (n == 0) return QX_OK;
+  const int width = (int)(HQ * D);
+  const int blocks = (width + 511) / 512;
+  const int64_t waves = n * blocks;
+  const dim3 grid((unsigned)((waves + 3) / 4));
+  if (scales) {
+    hipLaunchKernelGGL(qx::merge_attn_quant_kernel<true>, grid, dim3(256), 0, stream,
+                       (const uint16_t*)a, a_ld, (const uint16_t*)b, b_ld, la, la_ld, lb, lb_ld,
+                       source, (uint8_t*)q, q_ld, scales, s_ld, (int)n, width, blocks, (int)D);
   } else {
-    if (hpb == 4) QX_ATTN(64, 4, 2);
-    if (hpb == 2) QX_ATTN(64, 2, 4);
-    QX_ATTN(64, 1, 8);
+    hipLaunchKernelGGL(qx::merge_attn_quant_kernel<false>, grid, dim3(256), 0, stream,
+                       (const uint16_t*)a, a_ld, (const uint16_t*)b, b_ld, la, la_ld, lb, lb_ld,
+                       source, (uint8_t*)q, q_ld, nullptr, 0, (int)n, width, blocks, (int)D);
   }
-#undef QX_ATTN
+  QX_LAUNCH_STATUS();
 }
 
 // Host function: the work list of a paged call, one (sequence, query tile)

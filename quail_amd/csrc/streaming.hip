@@ -350,7 +350,8 @@ __global__ __launch_bounds__(256) void group_quant_kernel(const uint16_t* __rest
 
 // ---------------------------------------------------------------------------
 // pool[dst[i]] = rows[src[i]] for K and V; dst < 0 writes nothing
-// (attention.py:885-897). One wave per pair; rows are row_elems bf16.
+// (attention.py:885-897); without src and dst, row i goes to row i. One
+// wave per pair; rows are row_elems bf16.
 // V_F16: V source rows are bf16 and the V pool holds fp16 (round to nearest
 // even, exact for |v| in [2^-14, 65504]); otherwise both are copied as they are
 template <bool V_F16>
@@ -361,9 +362,9 @@ __global__ __launch_bounds__(256) void kv_scatter_kernel(
   const int lane = threadIdx.x & 63;
   const int i = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (i >= count) return;
-  const int64_t d = dst[i];
+  const int64_t d = dst ? dst[i] : i;
   if (d < 0) return;
-  const int64_t s = src[i];
+  const int64_t s = src ? src[i] : i;
   const uint4* ks = reinterpret_cast<const uint4*>(k + s * k_ld);
   const uint4* vs = reinterpret_cast<const uint4*>(v + s * v_ld);
   uint4* kd = reinterpret_cast<uint4*>(kp + d * row_elems);
@@ -541,7 +542,8 @@ int qx_group_quant(const void* x, int64_t x_ld, void* q, int64_t q_ld, float* sc
 int qx_kv_scatter(const void* k, int64_t k_ld, const void* v, int64_t v_ld, void* k_pool,
                   void* v_pool, const int64_t* src, const int64_t* dst, int64_t count,
                   int64_t row_elems, int v_to_f16, hipStream_t stream) {
-  QX_CHECK(k && v && k_pool && v_pool && src && dst, "kv_scatter: null pointer");
+  QX_CHECK(k && v && k_pool && v_pool && (src != nullptr) == (dst != nullptr),
+           "kv_scatter: null pointer");
   QX_CHECK(row_elems > 0 && row_elems % 8 == 0, "kv_scatter: row %lld", (long long)row_elems);
   QX_CHECK(k_ld % 8 == 0 && v_ld % 8 == 0 && aligned16(k) && aligned16(v) && aligned16(k_pool) &&
                aligned16(v_pool),

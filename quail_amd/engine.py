@@ -314,15 +314,91 @@ class Engine:
         """
         n = q.shape[0]
         hq, hk, d = self.num_q_heads, self.num_kv_heads, self.head_dim
-        if chunk.attention_mode != "unified":
-            raise ValueError("this engine runs the unified attention path")
+        if chunk.attention_mode not in ("unified", "tree"):
+            raise ValueError(f"attention mode {chunk.attention_mode!r}")
         for key in ("shared", "canvas"):
             if chunk.meta.get(key) is not None:
                 raise ValueError(f"this engine has no {key}-row attention path")
         q3 = q.view(n, hq, d)
         k3 = k.view(n, hk, d)
         v3 = v.view(n, hk, d) if v.is_contiguous() else v
+        if chunk.attention_mode == "tree":
+            return self.attention_tree(q3, k3, v3, chunk.meta, output=output)
         return self.attention_unified(q3, k3, v3, chunk.meta, output=output)
+
+    def attention_tree(self, q3, k3, v3, meta, *, output=None, quantize=True):
+        """The tree attention path (attention.py:1395-1441): the pack's KV
+        writes into arena pages, then call A (causal over the pack's own rows
+        in `cu_a` segments), call B (the reader rows over resident pages, not
+        causal), each with its log-sum-exp, and one fused merge + o_proj
+        input quantization (attention.py:902-948). Returns (e4m3, scales),
+        or with quantize=False the merged bf16 rows (for tests)."""
+        n = q3.shape[0]
+        hq, hk, d = self.num_q_heads, self.num_kv_heads, self.head_dim
+        layer = meta["layer"]
+        dev = q3.device
+        if meta.get("kv_src") is not None and meta["kv_src"].numel():
+            self.kv_row_scatter(k3, v3, meta["kv_src"], meta["kv_dst"], layer)
+        # call A reads the pack's own K and V rows: contiguous, V in fp16 as
+        # the pages hold it (one identity scatter)
+        row = hk * d
+        k_rows = torch.empty((n, row), dtype=torch.bfloat16, device=dev)
+        v_rows = torch.empty((n, row), dtype=torch.float16, device=dev)
+        _lib.call("qx_kv_scatter", _ptr(k3), k3.stride(0), _ptr(v3), v3.stride(0), _ptr(k_rows),
+                  _ptr(v_rows), None, None, n, row, 1, _stream())
+        scale = float(d ** -0.5)
+        seg = meta["segments"]
+        out_a = torch.empty((n, hq * d), dtype=torch.bfloat16, device=dev)
+        lse_a = torch.empty((hq, max(n, 1)), dtype=torch.float32, device=dev)
+        self._lse_call(q3, None, k_rows, v_rows, seg, None, seg["cu_q"], scale, out_a, lse_a)
+        reads = meta["reads"]
+        if output is not None:
+            o_q, o_s = output
+        else:
+            o_q = torch.empty((n, hq * d), dtype=self.fp8, device=dev)
+            o_s = self._col_major_scales(n, hq * d, dev)
+        if reads is None:
+            meta["layer"] += 1
+            return self.quant(out_a, output=(o_q, o_s)) if quantize else out_a
+        nb = reads["rows"].shape[0]
+        k_pool, v_pool = self.arena.layer_kv(layer)
+        out_b = torch.empty((nb, hq * d), dtype=torch.bfloat16, device=dev)
+        lse_b = torch.empty((hq, max(nb, 1)), dtype=torch.float32, device=dev)
+        self._lse_call(q3, reads["rows"], k_pool, v_pool, reads, reads["table"], None, scale,
+                       out_b, lse_b)
+        args = (_ptr(out_a), out_a.stride(0), _ptr(out_b), out_b.stride(0), _ptr(lse_a),
+                lse_a.stride(0), _ptr(lse_b), lse_b.stride(0), _ptr(reads["source"]), n, hq, d)
+        if d == GROUP and quantize:
+            _lib.call("qx_merge_attn_quant", *args, _ptr(o_q), o_q.stride(0), _ptr(o_s),
+                      self._scale_ld(o_s), _stream())
+        else:
+            # a 128-column FP8 group spans several heads: bf16 merge, then quant
+            merged = torch.empty((n, hq * d), dtype=torch.bfloat16, device=dev)
+            _lib.call("qx_merge_attn_quant", *args, _ptr(merged), merged.stride(0), None, 0,
+                      _stream())
+            if not quantize:
+                meta["layer"] += 1
+                return merged
+            self.quant(merged, output=(o_q, o_s))
+        meta["layer"] += 1
+        return o_q, o_s
+
+    def _lse_call(self, q3, q_index, k, v, tables, table, cu_k, scale, out, lse):
+        """One qx_attention_lse call over `tables` (cu_q, used, max_q,
+        max_used, causal, work): paged through `table`, or over contiguous
+        rows at `cu_k`."""
+        hq, hk, d = self.num_q_heads, self.num_kv_heads, self.head_dim
+        work = tables.get("work")
+        if not torch.is_tensor(work):
+            work = None
+        n_work = int(tables.get("n_work", 0)) if work is not None else 0
+        seqs = tables["used"].shape[0]
+        _lib.call("qx_attention_lse", _ptr(q3), q3.stride(0), _ptr(q_index), _ptr(k), _ptr(v),
+                  _ptr(tables["cu_q"]), _ptr(tables["used"]), _ptr(table),
+                  table.stride(0) if table is not None else 0, _ptr(cu_k), seqs,
+                  int(tables["max_q"]), int(tables["max_used"]), hq, hk, d, scale,
+                  int(tables.get("causal", True)), _ptr(out), out.stride(0), _ptr(lse),
+                  lse.stride(0), _ptr(work), n_work, _stream())
 
     def attention_unified(self, q3, k3, v3, meta, *, softmax_scale=None, output=None):
         """Write the chunk's KV to its pages, then one paged causal call with

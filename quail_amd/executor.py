@@ -21,7 +21,7 @@ from quail_amd.prefix import PrefixIndex
 
 class StageRun:
     def __init__(self, pipeline, arena, readout, prefixes, suffixes, chunk_budget,
-                 use_tree=True, staging=None):
+                 use_tree=True, staging=None, attention_mode="unified"):
         self.pipeline = pipeline
         self.arena = arena
         self.readout = readout
@@ -29,6 +29,9 @@ class StageRun:
         self.suffixes = suffixes
         self.chunk_budget = min(chunk_budget, pipeline.max_chunk_tokens)
         self.use_tree = use_tree
+        if attention_mode not in ("unified", "tree"):
+            raise ValueError(f"attention_mode {attention_mode!r}")
+        self.attention_mode = attention_mode
         self.staging = staging or InputStaging()
         self.stats = dict(chunks=0, fresh_tokens=0, borrowed_tokens=0, pack_s=0.0,
                           admission_s=0.0)
@@ -68,7 +71,13 @@ class StageRun:
                 raise ArenaFullError("no document fits the free KV arena")
             t = time.perf_counter()
             engine = self.pipeline.engine
-            chunk = pack_chunk(self.arena, [g for _, g in groups],
+            specs = [g for _, g in groups]
+            if self.attention_mode == "tree":
+                # a borrowing document with one question reads its parent's
+                # pages stacked with its siblings (stage_executor.py:772-774)
+                specs = [dict(g, read_key=g.get("borrow_key") if g.get("start") else None,
+                              single=len(g["suffixes"]) == 1) for g in specs]
+            chunk = pack_chunk(self.arena, specs, attention_mode=self.attention_mode,
                                attention_heads=(engine.num_q_heads, engine.num_kv_heads,
                                                 engine.head_dim))
             upload(chunk, self.staging)

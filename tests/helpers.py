@@ -27,7 +27,8 @@ def ref_model(model) -> ref.RefModel:
         head=cpu(model.lm_head.weight))
 
 
-def run_stage(model, workload, readout_kind="margins", num_pages=None, use_tree=True):
+def run_stage(model, workload, readout_kind="margins", num_pages=None, use_tree=True,
+              attention_mode="unified"):
     """Run one stage of the workload through the GPU engine; returns
     (results per document, StageRun)."""
     from quail_amd.arena import KVArena
@@ -53,7 +54,7 @@ def run_stage(model, workload, readout_kind="margins", num_pages=None, use_tree=
                    "score": ro.AsyncScores}[readout_kind](rows)
     prefixes, suffixes = workload.groups_input()
     run = StageRun(pipe, arena, readout, prefixes, suffixes, workload.chunk_budget,
-                   use_tree=use_tree)
+                   use_tree=use_tree, attention_mode=attention_mode)
     results = run.run()
     torch.cuda.synchronize()
     return results, run

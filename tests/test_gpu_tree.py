@@ -1,0 +1,286 @@
+"""The tree attention path on the GPU (Engine.attention_tree,
+attention.py:1395-1441): its two attention calls with log-sum-exp
+(qx_attention_lse) against float32 attention, the fused LSE merge and
+o_proj quantization (qx_merge_attn_quant) against a float32 restatement of
+the reference's merge_attn_quant (attention.py:902-948), and whole packs
+in tree mode against the oracle and against the unified path.
+
+Tolerances: attention outputs are bf16 (one rounding, 2^-8 relative) and
+the PV product runs with fp16 probabilities, so outputs are compared at
+2e-2 absolute on O(1) values and log-sum-exps at 1e-3. The merge is the
+reference's sequence of fp32 operations with its two bf16 roundings; the
+kernel fuses a + (b - a) * w into one FMA, which moves a value across a
+bf16 rounding boundary now and then, so at least 99.9% of e4m3 codes must
+be identical and the rest one code apart. End to end the margins keep the
+bounds of the unified path (tests/test_gpu_forward.py).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import fp8 as ofp8
+from quail_amd import _lib
+from quail_amd.model import CONFIGS, build_synthetic
+from quail_amd.workload import make_workload
+from tests.helpers import run_stage
+from tests.test_gpu_forward import TOL, _check, _oracle_margins
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _p(t):
+    return None if t is None else t.data_ptr()
+
+
+def _stream():
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _ref_attention(q, k, v, scale, causal):
+    """float32 attention of one sequence: q (m, HQ, D), k, v (u, HK, D)."""
+    m, hq, d = q.shape
+    u, hk, _ = k.shape
+    g = hq // hk
+    kk = k.float().repeat_interleave(g, dim=1)
+    vv = v.float().repeat_interleave(g, dim=1)
+    s = torch.einsum("mhd,uhd->hmu", q.float(), kk) * scale
+    if causal:
+        i = torch.arange(m, device=q.device)[:, None]
+        j = torch.arange(u, device=q.device)[None, :]
+        s = s.masked_fill(j > u - m + i, float("-inf"))
+    lse = torch.logsumexp(s, dim=-1)                     # (h, m)
+    o = torch.einsum("hmu,uhd->mhd", torch.softmax(s, dim=-1), vv)
+    return o, lse
+
+
+def _lse_call(q, q_ld, q_index, k, v, cu_q, used, table, cu_k, seqs, max_q, max_used, hq, hk, d,
+              causal, out, lse):
+    _lib.call("qx_attention_lse", _p(q), q_ld, _p(q_index), _p(k), _p(v), _p(cu_q), _p(used),
+              _p(table), table.stride(0) if table is not None else 0, _p(cu_k), seqs, max_q,
+              max_used, hq, hk, d, float(d ** -0.5), int(causal), _p(out), out.stride(0),
+              _p(lse), lse.stride(0), None, 0, _stream())
+
+
+@pytest.mark.parametrize("hq,hk,d", [(32, 8, 128), (4, 2, 64)])
+def test_segments_call_matches_float32(hq, hk, d):
+    """Call A: causal over contiguous rows in cu_k segments (a zero-length one,
+    one shorter than a KV tile, several tiles long)."""
+    g = torch.Generator(device=DEV).manual_seed(hq + d)
+    lengths = [5, 0, 64, 1, 300, 129, 33]
+    cu = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int32)
+    n = int(cu[-1])
+    q = torch.randn(n, hq * d, generator=g, device=DEV).to(torch.bfloat16)
+    k = torch.randn(n, hk * d, generator=g, device=DEV).to(torch.bfloat16)
+    v = torch.randn(n, hk * d, generator=g, device=DEV).to(torch.float16)
+    cu_t = torch.tensor(cu, device=DEV)
+    used = torch.tensor(lengths, dtype=torch.int32, device=DEV)
+    out = torch.full((n, hq * d), float("nan"), dtype=torch.bfloat16, device=DEV)
+    lse = torch.full((hq, n), float("nan"), dtype=torch.float32, device=DEV)
+    _lse_call(q, q.stride(0), None, k, v, cu_t, used, None, cu_t, len(lengths), max(lengths),
+              max(lengths), hq, hk, d, True, out, lse)
+    torch.cuda.synchronize()
+    for s, length in enumerate(lengths):
+        if not length:
+            continue
+        r0, r1 = int(cu[s]), int(cu[s + 1])
+        o, l = _ref_attention(q[r0:r1].view(-1, hq, d), k[r0:r1].view(-1, hk, d),
+                              v[r0:r1].view(-1, hk, d), d ** -0.5, True)
+        torch.testing.assert_close(out[r0:r1].float().view(-1, hq, d), o, atol=2e-2, rtol=0)
+        torch.testing.assert_close(lse[:, r0:r1], l, atol=1e-3, rtol=0)
+
+
+def test_page_reads_with_row_index_match_float32():
+    """Call B: selected query rows (q_index), not causal, keys through block
+    tables over 16-row pages (used not a page multiple)."""
+    hq, hk, d, page = 32, 8, 128, 16
+    g = torch.Generator(device=DEV).manual_seed(7)
+    pages = 64
+    kp = torch.randn(pages * page, hk * d, generator=g, device=DEV).to(torch.bfloat16)
+    vp = torch.randn(pages * page, hk * d, generator=g, device=DEV).to(torch.float16)
+    n = 200
+    q = torch.randn(n, hq * d, generator=g, device=DEV).to(torch.bfloat16)
+    rng = np.random.default_rng(3)
+    q_lens = [3, 40, 1, 70]
+    used_h = [16, 100, 33, 250]
+    rows = rng.choice(n, sum(q_lens), replace=False).astype(np.int64)
+    width = max(-(-u // page) for u in used_h)
+    table_h = np.zeros((len(q_lens), width), dtype=np.int32)
+    for s, u in enumerate(used_h):
+        table_h[s, :-(-u // page)] = rng.choice(pages, -(-u // page), replace=False)
+    cu = np.concatenate([[0], np.cumsum(q_lens)]).astype(np.int32)
+    nb = int(cu[-1])
+    out = torch.empty(nb, hq * d, dtype=torch.bfloat16, device=DEV)
+    lse = torch.empty(hq, nb, dtype=torch.float32, device=DEV)
+    table = torch.tensor(table_h, device=DEV)
+    _lse_call(q, q.stride(0), torch.tensor(rows, device=DEV), kp, vp, torch.tensor(cu, device=DEV),
+              torch.tensor(used_h, dtype=torch.int32, device=DEV), table, None, len(q_lens),
+              max(q_lens), max(used_h), hq, hk, d, False, out, lse)
+    torch.cuda.synchronize()
+    for s in range(len(q_lens)):
+        keys = (torch.tensor(table_h[s], device=DEV).long()[:, None] * page
+                + torch.arange(page, device=DEV)).reshape(-1)[:used_h[s]]
+        sel = torch.tensor(rows[cu[s]:cu[s + 1]], device=DEV)
+        o, l = _ref_attention(q[sel].view(-1, hq, d), kp[keys].view(-1, hk, d),
+                              vp[keys].view(-1, hk, d), d ** -0.5, False)
+        torch.testing.assert_close(out[cu[s]:cu[s + 1]].float().view(-1, hq, d), o, atol=2e-2,
+                                   rtol=0)
+        torch.testing.assert_close(lse[:, cu[s]:cu[s + 1]], l, atol=1e-3, rtol=0)
+
+
+def _merge_reference(a, b, la, lb, source):
+    """merge_attn_quant (attention.py:902-948) in float32 torch ops."""
+    has = source >= 0
+    src = source.clamp_min(0).long()
+    af = a.float()
+    bf = b.float()[src]
+    hq = la.shape[0]
+    x = lb[:, src] - la                                       # (h, n)
+    w = torch.sigmoid(x).to(torch.bfloat16).float().t()      # (n, h)
+    n = a.shape[0]
+    a3 = af.view(n, hq, -1)
+    b3 = bf.view(n, hq, -1)
+    merged = (a3 + (b3 - a3) * w[:, :, None]).to(torch.bfloat16).float()
+    return torch.where(has[:, None, None], merged, a3).reshape(n, -1)
+
+
+def test_merge_matches_the_reference_merge():
+    hq, d = 32, 128
+    g = torch.Generator(device=DEV).manual_seed(11)
+    n, nb = 300, 180
+    a = torch.randn(n, hq * d, generator=g, device=DEV).to(torch.bfloat16)
+    b = torch.randn(nb, hq * d, generator=g, device=DEV).to(torch.bfloat16)
+    la = torch.randn(hq, n, generator=g, device=DEV) * 3
+    lb = torch.randn(hq, nb, generator=g, device=DEV) * 3
+    src = torch.full((n,), -1, dtype=torch.int32, device=DEV)
+    pick = torch.randperm(n, generator=g, device=DEV)[:nb]
+    src[pick] = torch.arange(nb, dtype=torch.int32, device=DEV)
+    q = torch.empty(n, hq * d, dtype=torch.float8_e4m3fn, device=DEV)
+    scales = torch.empty(n * hq, dtype=torch.float32, device=DEV)
+    _lib.call("qx_merge_attn_quant", _p(a), a.stride(0), _p(b), b.stride(0), _p(la), la.stride(0),
+              _p(lb), lb.stride(0), _p(src), n, hq, d, _p(q), q.stride(0), _p(scales), n,
+              _stream())
+    y = _merge_reference(a, b, la, lb, src)
+    want_q, want_s = ofp8.group_quant(y.cpu())
+    got_s = scales.view(hq, n).t().cpu()
+    codes = q.view(torch.uint8).cpu().numpy().astype(np.int32)
+    want_codes = want_q.view(torch.uint8).numpy().astype(np.int32)
+    same = codes == want_codes
+    assert same.mean() >= 0.999, same.mean()
+    # a differing code is an adjacent e4m3 value (same sign byte, code +-1)
+    assert np.abs(codes[~same] - want_codes[~same]).max(initial=0) <= 1
+    rel = ((got_s - want_s).abs() / want_s).numpy()
+    assert (rel == 0).mean() >= 0.99 and rel.max() <= 2 ** -7
+    # rows that read nothing resident are quantized a
+    keep = (src < 0).cpu().numpy()
+    plain_q, _ = ofp8.group_quant(a.float().cpu())
+    assert np.array_equal(codes[keep], plain_q.view(torch.uint8).numpy()[keep])
+
+
+def test_bf16_merge_for_narrow_heads():
+    hq, d = 4, 64
+    g = torch.Generator(device=DEV).manual_seed(12)
+    n = 50
+    a = torch.randn(n, hq * d, generator=g, device=DEV).to(torch.bfloat16)
+    b = torch.randn(n, hq * d, generator=g, device=DEV).to(torch.bfloat16)
+    la = torch.randn(hq, n, generator=g, device=DEV)
+    lb = torch.randn(hq, n, generator=g, device=DEV)
+    src = torch.arange(n, dtype=torch.int32, device=DEV)
+    src[::3] = -1
+    out = torch.empty(n, hq * d, dtype=torch.bfloat16, device=DEV)
+    _lib.call("qx_merge_attn_quant", _p(a), a.stride(0), _p(b), b.stride(0), _p(la), la.stride(0),
+              _p(lb), lb.stride(0), _p(src), n, hq, d, _p(out), out.stride(0), None, 0, _stream())
+    want = _merge_reference(a, b, la, lb, src)
+    diff = (out.float() - want).abs()
+    ulp = want.abs().clamp_min(1e-30) * 2 ** -7
+    assert (diff == 0).float().mean() >= 0.999 and bool((diff <= ulp).all())
+
+
+@pytest.mark.parametrize("seed", [0, 3])
+def test_tiny_tree_pass_matches_the_oracle_and_the_unified_pass(seed):
+    cfg = CONFIGS["tiny"]
+    wl = make_workload("tiny", seed=seed)
+    model = build_synthetic(cfg, seed=seed, device="cuda", gen_device="cpu", norm_init="random")
+    results, run = run_stage(model, wl, "margins", attention_mode="tree")
+    tree = np.array([r[0] - r[1] for r in results], dtype=np.float64)
+    results, _ = run_stage(model, wl, "margins")
+    unified = np.array([r[0] - r[1] for r in results], dtype=np.float64)
+    want, _ = _oracle_margins(model, wl)
+    assert run.stats["borrowed_tokens"] == 15 * 32
+    _check(tree, want, within=15 / 16)
+    assert np.abs(tree - unified).max() <= 2 * TOL
+
+
+def test_qwen3_4b_tree_attention_equals_the_unified_attention():
+    """Layer 0 of Qwen3-4B over the first two packs of 40 benchmark documents
+    (64-token shared prefix: children read their parent's pages stacked,
+    from the same pack and from the one before), packed both ways: every
+    row's attention output (bf16, before the o_proj quantization) agrees.
+    The tree result rounds call A, call B, the merge weight and the merge to
+    bf16 (attention.py:902-948): about 3 * 2^-9 of max(|a|, |b|), so the
+    bound is relative to the head's largest value (the o_proj input's FP8
+    group): 99.9% of elements within 2^-7 of it and every one within 2^-5
+    (measured 6.4e-3 and 1.7e-2; rows with no resident reads are
+    bit-identical)."""
+    import dataclasses
+
+    from quail_amd.admission import StageAdmission
+    from quail_amd.arena import KVArena
+    from quail_amd.chunk import InputStaging, pack_chunk, upload
+    from quail_amd.prefix import PrefixIndex
+    from quail_amd.qwen3 import Qwen3Pipeline
+
+    cfg = dataclasses.replace(CONFIGS["qwen3-4b"], layers=1)
+    wl = make_workload("qwen3-4b", seed=0)
+    prompts = wl.prompts[:40]
+    model = build_synthetic(cfg, seed=0, device="cuda", norm_init="random")
+    prefixes = [p[:-1] for p in prompts]
+    suffixes = [[p[-1:]] for p in prompts]
+    tree = PrefixIndex(prompts).tree(16)
+    runs = {}
+    for mode in ("unified", "tree"):
+        arena = KVArena(1, 2048, 16, cfg.kv_heads, cfg.head_dim)
+        pipe = Qwen3Pipeline(model, arena)
+        engine = pipe.engine
+        adm = StageAdmission(prefixes, suffixes, arena, 3000, tree=tree)
+        outs, stacked = [], 0
+        for _ in range(2):
+            specs = [g for _, g in adm.next_chunk()]
+            if mode == "tree":
+                specs = [dict(g, read_key=g["borrow_key"] if g["start"] else None, single=True)
+                         for g in specs]
+                stacked += sum(g["read_key"] is not None for g in specs)
+            chunk = pack_chunk(arena, specs, attention_mode=mode,
+                               attention_heads=(cfg.heads, cfg.kv_heads, cfg.head_dim))
+            upload(chunk, InputStaging())
+            layer = pipe.layers[0]
+            q_in, q_scale, _ = engine.embed_norm_quant(chunk.input_ids, pipe.embed.weight,
+                                                       layer.input_layernorm)
+            q, k, v = pipe._project_qkv(q_in, q_scale, chunk.positions, layer.self_attn)
+            n = q.shape[0]
+            q3 = q.view(n, cfg.heads, cfg.head_dim)
+            k3 = k.view(n, cfg.kv_heads, cfg.head_dim)
+            v3 = v.view(n, cfg.kv_heads, cfg.head_dim) if v.is_contiguous() else v
+            chunk.meta["layer"] = 0
+            if mode == "tree":
+                outs.append(engine.attention_tree(q3, k3, v3, chunk.meta, quantize=False))
+            else:
+                engine.write_kv(k3, v3, chunk.meta)
+                outs.append(engine.attention_bf16(q3, chunk.meta, 0))
+            for t in chunk.temporary_keys:
+                arena.free_key(t)
+        torch.cuda.synchronize()
+        runs[mode] = (outs, stacked)
+    assert runs["tree"][1] > 0
+    for got, want in zip(runs["tree"][0], runs["unified"][0]):
+        n = want.shape[0]
+        g3 = got.float().view(n, cfg.heads, cfg.head_dim)
+        w3 = want.float().view(n, cfg.heads, cfg.head_dim)
+        amax = w3.abs().amax(dim=-1, keepdim=True).clamp_min(1e-30)
+        rel = ((g3 - w3).abs() / amax).flatten()
+        qs = torch.quantile(rel[torch.randperm(rel.numel(), device=rel.device)[:1 << 20]],
+                            torch.tensor([0.5, 0.9, 0.99, 0.999], device=rel.device))
+        print("tree vs unified attention, |diff| / head amax: quantiles 50/90/99/99.9% "
+              + " ".join(f"{v:.2e}" for v in qs.tolist()) + f" max {rel.max().item():.2e}")
+        assert qs[3].item() <= 2 ** -7 and rel.max().item() <= 2 ** -5

@@ -1,0 +1,150 @@
+"""The tree attention layout (attention_mode="tree"): the reference's known
+answers (tests/engine/test_pack_chunk.py:16-51 and the retained-read counts
+of :58-100) and the structural read check over seeded corpora with shared
+prefixes (each row's call-B keys through its read table, then its call-A
+segment, must be exactly its document up to itself)."""
+
+import numpy as np
+import pytest
+
+from oracle.packing_ref import PoolModel, check_pack_tree
+from quail_amd.admission import StageAdmission
+from quail_amd.arena import KVArena
+from quail_amd.chunk import pack_chunk
+from quail_amd.prefix import PrefixIndex
+from tests.test_pack import _corpus
+
+
+def plain_arena(pages=64, page=16):
+    return KVArena(1, pages, page, 1, 8, device="cpu")
+
+
+def test_many_suffixes_and_a_kept_document():
+    # tests/engine/test_pack_chunk.py:16-51
+    arena = plain_arena()
+    key = ("d", 0)
+    arena.activate(key, 4, capacity_tokens=8, base_tokens=4)
+    sufs = [[10, 11], [12], [13, 14, 15]]
+    chunk = pack_chunk(arena, [dict(key=key, prefix=[1, 2, 3, 4], f=4, suffixes=sufs,
+                                    read_all_rows=True)], attention_mode="tree")
+    assert chunk.host_ids.tolist() == [1, 2, 3, 4, 10, 11, 12, 13, 14, 15]
+    assert chunk.host_positions.tolist() == [0, 1, 2, 3, 4, 5, 4, 4, 5, 6]
+    assert chunk.final_indices.tolist() == [4, 5, 6, 7, 8, 9]
+    assert chunk.rows_per_answer.tolist() == [2, 1, 3]
+    assert chunk.meta["cu_a"].tolist() == [0, 4, 6, 7, 10]
+    assert chunk.meta["max_a"] == 4
+    assert chunk.layout == [(key, 3)]
+    assert chunk.fresh_keys == (key,)
+    assert chunk.meta["kv_src"].tolist() == [0, 1, 2, 3]
+    # the suffix rows read the document's 4 tokens from its pages
+    reads = chunk.meta["reads"]
+    assert reads["rows"].tolist() == [4, 5, 6, 7, 8, 9]
+    assert reads["used"].tolist() == [4]
+    chunk = pack_chunk(arena, [dict(key=key, prefix=None, f=4, suffixes=sufs)],
+                       attention_mode="tree")
+    assert chunk.host_ids.tolist() == [10, 11, 12, 13, 14, 15]
+    assert chunk.final_indices.tolist() == [1, 2, 5]
+    assert chunk.rows_per_answer is None
+    assert chunk.meta["cu_a"].tolist() == [0, 2, 3, 6]
+    reads = chunk.meta["reads"]
+    assert reads["rows"].tolist() == [0, 1, 2, 3, 4, 5]
+    assert reads["cu_q"].tolist() == [0, 6]
+    assert reads["used"].tolist() == [4]
+    assert reads["source"].tolist() == [0, 1, 2, 3, 4, 5]
+    assert chunk.meta["kv_src"] is None
+
+
+@pytest.mark.parametrize("shared", [0, 16])
+def test_retained_reads_of_a_stacked_then_kept_document(shared):
+    # tests/engine/test_pack_chunk.py:58-100 with run = 2: the first pass
+    # reads the shared pages of the parent, the second the kept 35 tokens
+    arena = plain_arena()
+    parent, key = ("d", 0), ("d", 1)
+    arena.activate(parent, 32, capacity_tokens=40, base_tokens=32)
+    arena.activate(key, 32, capacity_tokens=40, base_tokens=32,
+                   borrow=(parent, shared) if shared else None)
+    retained = []
+    for first in (True, False):
+        chunk = pack_chunk(arena, [dict(
+            key=key, prefix=list(range(shared, 32)) if first else None,
+            f=32 if first else 35, start=shared if first else 0,
+            read_key=parent if first and shared else None,
+            suffixes=[[91, 92, 93]] if first else [[40, 41]],
+            write_suffix_tokens=3 if first else 2, single=True)], attention_mode="tree")
+        reads = chunk.meta["reads"]
+        retained.append(0 if reads is None else int(reads["used"].sum()))
+        if first:
+            # the prefix rows, then the 3 kept suffix rows after them
+            rows = arena.capacity_rows(key)
+            assert chunk.meta["kv_dst"].tolist() == rows[shared:35].tolist()
+            # whole document, one causal segment
+            assert chunk.meta["cu_a"].tolist() == [0, 32 - shared + 3]
+    assert retained == [shared, 35]
+
+
+def test_unpaged_and_unsupported_groups_are_refused():
+    arena = plain_arena()
+    with pytest.raises(ValueError, match="needs arena pages"):
+        pack_chunk(arena, [dict(key="x", prefix=[1, 2], f=2, start=16, suffixes=[[3]])],
+                   attention_mode="tree")
+    arena.activate("y", 4)
+    with pytest.raises(ValueError, match="canvas"):
+        pack_chunk(arena, [dict(key="y", prefix=[1, 2, 3, 4], f=4, suffixes=[[5]],
+                                canvas=[1, 2])], attention_mode="tree")
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2, 3, 7, 11, 100, 200])
+def test_tree_packs_read_exactly_their_documents(seed):
+    docs = _corpus(seed, 40)
+    arena = plain_arena(pages=48)
+    tree = PrefixIndex(docs).tree(16)
+    adm = StageAdmission([d[:-1] for d in docs], [[d[-1:]] for d in docs], arena,
+                         chunk_budget=256, tree=tree)
+    pool = PoolModel()
+    prompts = {adm.keys[i]: d for i, d in enumerate(docs)}
+    checked = packs = stacked = 0
+    live = []
+    while not adm.done():
+        groups = adm.next_chunk()
+        if not groups:
+            assert live
+            for d in live.pop(0):
+                arena.free_key(adm.keys[d])
+            continue
+        specs = [dict(g, read_key=g["borrow_key"] if g["start"] else None, single=True)
+                 for _, g in groups]
+        stacked += sum(1 for g in specs if g["read_key"] is not None)
+        chunk = pack_chunk(arena, specs, attention_mode="tree")
+        checked += check_pack_tree(chunk, 16, pool, prompts.__getitem__)
+        live.append([d for d, _ in groups])
+        packs += 1
+        if len(live) > 1:
+            for d in live.pop(0):
+                arena.free_key(adm.keys[d])
+    for left in live:
+        for d in left:
+            arena.free_key(adm.keys[d])
+    assert checked == sum(len(d) for d in docs) - adm.borrowing.borrowed_tokens
+    assert packs >= 2 and stacked > 0
+    assert arena.free_pages == arena.num_pages
+
+
+def test_siblings_share_one_stacked_read_of_their_parent():
+    prefix = list(range(32))
+    docs = [prefix + [100 + i] * (3 + i) for i in range(5)]
+    arena = plain_arena()
+    tree = PrefixIndex(docs).tree(16)
+    adm = StageAdmission([d[:-1] for d in docs], [[d[-1:]] for d in docs], arena,
+                         chunk_budget=1024, tree=tree)
+    groups = adm.next_chunk()
+    specs = [dict(g, read_key=g["borrow_key"] if g["start"] else None, single=True)
+             for _, g in groups]
+    chunk = pack_chunk(arena, specs, attention_mode="tree")
+    reads = chunk.meta["reads"]
+    # the root is one segment with no reads; its four children read the
+    # root's 32 tokens in one stacked sequence
+    assert reads["used"].tolist() == [32]
+    n_root = len(docs[0])
+    assert reads["rows"].tolist() == list(range(n_root, len(chunk.host_ids)))
+    assert chunk.meta["cu_a"].tolist()[:2] == [0, n_root]
+    check_pack_tree(chunk, 16, PoolModel(), {adm.keys[i]: d for i, d in enumerate(docs)}.__getitem__)
