@@ -14,6 +14,12 @@ GEMM launch of the timed region), and the CPU baseline: the oracle's torch
 restatement of the reference path timed on this host on a bounded sample.
 
   python bench.py [--steps K] [--warmup W] [--gpus 1] [--cpu-seconds S]
+                  [--attention unified|tree]
+                                          tree: the tree attention path (each
+                                          document one causal segment, the
+                                          shared prefix read from its parent's
+                                          pages, LSE merge) instead of the
+                                          unified paged call
   python bench.py --copy-mib 1024 ...     also run one plain copy of that size
                                           (qx_embed over identity ids) before
                                           the warmup, to calibrate HBM counters
@@ -52,6 +58,7 @@ def parse():
     p.add_argument("--warmup", type=int, default=1)
     p.add_argument("--workload", default=WORKLOAD)
     p.add_argument("--seed", type=int, default=0)
+    p.add_argument("--attention", choices=("unified", "tree"), default="unified")
     p.add_argument("--cpu-seconds", type=float, default=15.0,
                    help="target wall time of the CPU baseline sample (0 skips it)")
     p.add_argument("--copy-mib", type=int, default=0,
@@ -65,6 +72,14 @@ def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
+def describe(wl, cfg, attention) -> str:
+    """The workload line of the JSON record."""
+    text = (f"{cfg.name} FP8 AI.{wl.function.upper()} prefill: {wl.documents} documents, "
+            f"{wl.describe_lengths()}, {wl.prefix_tokens}-token shared prefix in the paged "
+            f"arena, {wl.chunk_budget}-row packs")
+    return text + ("" if attention == "unified" else ", tree attention path")
+
+
 def cpu_threads() -> int:
     share = len(os.sched_getaffinity(0))
     env = os.environ.get("OMP_NUM_THREADS")
@@ -72,14 +87,18 @@ def cpu_threads() -> int:
 
 
 def attention_pairs(run_packs):
-    """(q, k) pairs the causal paged calls evaluate, summed over packs."""
+    """(q, k) pairs the attention calls evaluate, summed over packs: each
+    entry is (cu_q, used, causal) of one call."""
     pairs = 0
-    for cu, used in run_packs:
+    for cu, used, causal in run_packs:
         for s in range(len(used)):
             q_len = cu[s + 1] - cu[s]
             u = used[s]
-            # query i sees u - q_len + i + 1 keys
-            pairs += q_len * (u - q_len) + q_len * (q_len + 1) // 2
+            if causal:
+                # query i sees u - q_len + i + 1 keys
+                pairs += q_len * (u - q_len) + q_len * (q_len + 1) // 2
+            else:
+                pairs += q_len * u
     return pairs
 
 
@@ -267,13 +286,17 @@ def main():
     t_build = time.perf_counter() - t_build
 
     def step(record=None):
-        run = StageRun(pipe, arena, readout, prefixes, suffixes, wl.chunk_budget)
+        run = StageRun(pipe, arena, readout, prefixes, suffixes, wl.chunk_budget,
+                       attention_mode=args.attention)
         if record is not None:
             orig = pipe.forward_chunk
 
             def forward(chunk):
-                u = chunk.host["unified"]
-                record.append(([int(x) for x in u["cu_q"]], [int(x) for x in u["used"]]))
+                calls = ([chunk.host["unified"]] if chunk.attention_mode == "unified" else
+                         [t for t in (chunk.host["segments"], chunk.host["reads"]) if t])
+                for u in calls:
+                    record.append(([int(x) for x in u["cu_q"]], [int(x) for x in u["used"]],
+                                   bool(u.get("causal", True))))
                 return orig(chunk)
             pipe.forward_chunk = forward
         try:
@@ -364,9 +387,7 @@ def main():
         "dtype": "fp8-e4m3 (fp32 accumulate), bf16 activations",
         "data": "synthetic (seeded random-init Qwen3-4B weights, uniform token ids)",
         "config": {
-            "workload": ("Qwen3-4B FP8 AI.IF prefill: 512 documents, lognormal(256, 0.8) "
-                         "clipped 32..2048 tokens, 64-token shared prefix in the paged arena, "
-                         "16384-row packs"),
+            "workload": describe(wl, cfg, args.attention),
             "documents": docs, "fresh_tokens": fresh, "packs": stats[0]["chunks"],
             "borrowed_tokens": stats[0]["borrowed_tokens"], "attention_pairs": pairs,
             "parallelism": "none (1 GPU)",

@@ -39,6 +39,14 @@ class Workload:
     def documents(self) -> int:
         return len(self.prompts)
 
+    def describe_lengths(self) -> str:
+        """The document length distribution of the workload, in words."""
+        kind = _SPECS[self.name]["lengths"]
+        if kind[0] == "uniform":
+            return f"lengths uniform {kind[1]}..{kind[2]} tokens"
+        _, median, sigma, lo, hi = kind
+        return f"lognormal({median}, {sigma}) clipped {lo}..{hi} tokens"
+
     def groups_input(self):
         """(prefixes, suffixes): the prompt less its last token, and that token."""
         prefixes = [p[:-1] for p in self.prompts]
