@@ -16,7 +16,9 @@
  *     128-column group g is at scales[g * s_ld + t] (attention.py:534-537).
  *   - Return value: 0 on success; -1 for an argument error, with the
  *     message in qx_last_error(); a positive hipError_t if the launch failed.
- *   - The library allocates no memory and keeps no state between calls.
+ *   - The device entry points allocate no memory and keep no state between
+ *     calls; the host packing functions (qx_pages_*, qx_pack_*) keep theirs
+ *     in host handles the caller creates and destroys.
  */
 #ifndef QUAIL_MI355X_H
 #define QUAIL_MI355X_H
