@@ -72,9 +72,14 @@ def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
+def model_name(cfg) -> str:
+    """qwen3-4b -> Qwen3-4B."""
+    return "Qwen3" + cfg.name[len("qwen3"):].upper() if cfg.name.startswith("qwen3") else cfg.name
+
+
 def describe(wl, cfg, attention) -> str:
     """The workload line of the JSON record."""
-    text = (f"{cfg.name} FP8 AI.{wl.function.upper()} prefill: {wl.documents} documents, "
+    text = (f"{model_name(cfg)} FP8 AI.{wl.function.upper()} prefill: {wl.documents} documents, "
             f"{wl.describe_lengths()}, {wl.prefix_tokens}-token shared prefix in the paged "
             f"arena, {wl.chunk_budget}-row packs")
     return text + ("" if attention == "unified" else ", tree attention path")
@@ -268,7 +273,7 @@ def main():
     from quail_amd.executor import StageRun
     from quail_amd.model import CONFIGS, build_synthetic, retain_answer_head
     from quail_amd.qwen3 import Qwen3Pipeline
-    from quail_amd.readout import AnswerRows, AsyncAnswers
+    from quail_amd.readout import AnswerRows, AsyncAnswers, AsyncLabelLogprobs, AsyncScores
     from quail_amd.workload import make_workload
 
     assert torch.cuda.is_available(), "bench needs a GPU"
@@ -276,11 +281,18 @@ def main():
     cfg = CONFIGS[wl.model]
     t_build = time.perf_counter()
     model = build_synthetic(cfg, seed=args.seed, device="cuda")
-    retain_answer_head(model, wl.label_ids[:2])
+    if wl.function != "classify":
+        retain_answer_head(model, wl.label_ids[:2])
     num_pages = 3 * wl.chunk_budget // wl.page_tokens + 64
     arena = KVArena(cfg.layers, num_pages, wl.page_tokens, cfg.kv_heads, cfg.head_dim)
     pipe = Qwen3Pipeline(model, arena)
-    readout = AsyncAnswers(AnswerRows(model, [wl.label_ids[0]], [wl.label_ids[1]]))
+    # the stage's AI function: AI.IF bits, AI.SCORE values, or the
+    # AI.CLASSIFY label logits at each document's last row
+    if wl.function == "classify":
+        readout = AsyncLabelLogprobs(model.lm_head.weight, list(wl.label_ids), normalize=False)
+    else:
+        rows = AnswerRows(model, [wl.label_ids[0]], [wl.label_ids[1]])
+        readout = (AsyncScores if wl.function == "score" else AsyncAnswers)(rows)
     prefixes, suffixes = wl.groups_input()
     torch.cuda.synchronize()
     t_build = time.perf_counter() - t_build
@@ -346,7 +358,8 @@ def main():
     gemm_bytes = sum(m * k + n * k + 4 * (m * k // 128 + n * k // 16384) +
                      (m * n // 2 + 4 * (m * n // 256) if swiglu else 2 * m * n)
                      for m, n, k, _, _, swiglu in timer)
-    traffic = load_traffic()
+    # the counter runs behind TRAFFIC_FILE are of the Qwen3-4B workload
+    traffic = load_traffic() if args.workload == WORKLOAD else None
 
     fresh = stats[0]["fresh_tokens"]
     docs = wl.documents
@@ -374,7 +387,9 @@ def main():
         log(f"cpu baseline: {cpu['sample']}")
 
     line = {
-        "metric": METRIC,
+        "metric": METRIC if args.workload == WORKLOAD else
+        f"AI.{wl.function.upper()} rows/sec + prefill tok/s, {model_name(cfg)} FP8, 1 MI355X; "
+        f"% FP8 MFMA peak",
         "value": round(rows_s, 2),
         "unit": "rows/s",
         "n_gpus": 1,
@@ -385,7 +400,7 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "fp8-e4m3 (fp32 accumulate), bf16 activations",
-        "data": "synthetic (seeded random-init Qwen3-4B weights, uniform token ids)",
+        "data": f"synthetic (seeded random-init {model_name(cfg)} weights, uniform token ids)",
         "config": {
             "workload": describe(wl, cfg, args.attention),
             "documents": docs, "fresh_tokens": fresh, "packs": stats[0]["chunks"],
@@ -396,7 +411,7 @@ def main():
         "e2e_roofline_frac": round(e2e_frac, 4),
         "roofline": {
             "bound": "mfma",
-            "kernel": "FP8 block-scaled GEMM, all four Qwen3-4B projections: "
+            "kernel": f"FP8 block-scaled GEMM, all four {model_name(cfg)} projections: "
                       "qx_gemm_fp8_blockscaled (qkv, o_proj, down) and "
                       "qx_gemm_fp8_swiglu_quant (gate_up with the SiLU-quant epilogue)",
             "achieved": round(gemm_tflops, 2),
