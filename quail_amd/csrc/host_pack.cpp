@@ -29,6 +29,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <new>
 #include <queue>
 #include <unordered_map>
 #include <unordered_set>
@@ -430,9 +431,9 @@ int qx_pages_free_list(void* pool, int32_t* pages, int64_t cap, int64_t* n) {
 // suffix_ids: every group's suffixes, concatenated. On success *pack holds
 // the arrays (qx_pack_array) until qx_pack_destroy. On failure every
 // temporary key allocated so far is freed and *failed_group names the group.
-int qx_pack_unified(void* pool, const int64_t* groups, int64_t n_groups,
-                    const int64_t* prefix_ids, const int64_t* suffix_lens,
-                    const int64_t* suffix_ids, void** pack, int64_t* failed_group) {
+static int pack_unified(void* pool, const int64_t* groups, int64_t n_groups,
+                        const int64_t* prefix_ids, const int64_t* suffix_lens,
+                        const int64_t* suffix_ids, void** pack, int64_t* failed_group) {
   PagePool* p = pool_of(pool);
   QX_CHECK(p && pack && failed_group && (n_groups == 0 || groups), "pack_unified: null pointer");
   *pack = nullptr;
@@ -616,6 +617,18 @@ int qx_pack_unified(void* pool, const int64_t* groups, int64_t n_groups,
                   (int64_t)width};
   *pack = out;
   return QX_OK;
+}
+
+int qx_pack_unified(void* pool, const int64_t* groups, int64_t n_groups,
+                    const int64_t* prefix_ids, const int64_t* suffix_lens,
+                    const int64_t* suffix_ids, void** pack, int64_t* failed_group) {
+  try {
+    return pack_unified(pool, groups, n_groups, prefix_ids, suffix_lens, suffix_ids, pack,
+                        failed_group);
+  } catch (const std::bad_alloc&) {
+    qx::set_error("pack_unified: out of host memory");
+    return QX_EINVAL;
+  }
 }
 
 int qx_pack_array(void* pack, int64_t which, const void** data, int64_t* count) {

@@ -11,6 +11,12 @@ if str(ROOT) not in sys.path:
 
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) GPU and the built library")
+    # the host-side tests call the library's C++ packing functions: build it
+    # in a fresh checkout (the .so is not versioned); an existing one is used
+    from quail_amd import _lib
+    if not _lib.LIB_PATH.exists():
+        from quail_amd import build
+        build.build(verbose=True)
 
 
 def gpu_available() -> bool:
