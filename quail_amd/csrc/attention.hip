@@ -93,7 +93,7 @@ __global__ __launch_bounds__(HPB * QSUB * 64) void paged_attention_kernel(
   __shared__ __attribute__((aligned(1024))) uint8_t kv_lds[2][2][T_BYTES];  // [buffer][K, V]
   auto k_buf = [&](int b) -> uint8_t* { return &kv_lds[b][0][0]; };
   auto v_buf = [&](int b) -> uint8_t* { return &kv_lds[b][1][0]; };
-  __shared__ int pages_lds[kMaxPages];
+  __shared__ int pages_lds[kMaxPages + 64];  // + one wave's DMA past the last page
 
   // the workgroup's (sequence, query tile, head group): from the work list
   // (one item per real query tile, heaviest first, head groups innermost),
@@ -104,15 +104,21 @@ __global__ __launch_bounds__(HPB * QSUB * 64) void paged_attention_kernel(
     zg = blockIdx.x % zgroups;
     s = work[2 * item];
     qt = work[2 * item + 1];
-    if (s < 0 || s >= seqs || qt < 0) return;  // not an item of this call
   } else {
     s = blockIdx.y;
     qt = gridDim.x - 1 - blockIdx.x;
     zg = blockIdx.z;
   }
-  const int q0 = cu_q[s];
-  const int q_len = cu_q[s + 1] - q0;
-  if (qt * BQ >= q_len) return;  // uniform over the workgroup
+  // the sequence's bounds in one round of loads (s clamped into range, so
+  // every load is in bounds), then the exits: each dependent load is a
+  // memory round trip before the first KV tile
+  const int sc = min(max(s, 0), seqs - 1);
+  const int q0 = cu_q[sc];
+  const int q_len = cu_q[sc + 1] - q0;
+  const int used_raw = used[sc];
+  const int kv_first = CONTIG ? cu_k[sc] : 0;
+  if (s < 0 || s >= seqs || qt < 0) return;  // not an item of this call
+  if (qt * BQ >= q_len) return;               // uniform over the workgroup
   const int G = HQ / HK;
   const int groups_per_kv = G / HPB;
   const int kvh = zg / groups_per_kv;
@@ -124,7 +130,7 @@ __global__ __launch_bounds__(HPB * QSUB * 64) void paged_attention_kernel(
   const int half = lane >> 5;
   const int col = lane & 31;
 
-  const int used_s = min(used[s], max_used);
+  const int used_s = min(used_raw, max_used);
   const int off = causal ? used_s - q_len : 0;
   const int r = qt * BQ + qsub * 32 + col;  // this lane's query row within the sequence
   const bool r_ok = r < q_len;
@@ -135,22 +141,32 @@ __global__ __launch_bounds__(HPB * QSUB * 64) void paged_attention_kernel(
   const int wave_end = causal ? min(used_s, off + wave_last + 1) : used_s;
   const int ntiles = (kv_end + kBK - 1) / kBK;
 
-  // stage the page-table row
-  int kv0 = 0;
-  if (CONTIG) {
-    kv0 = cu_k[s];
-  } else {
+  // this lane's Q row (through q_index, which only the tree path's reads of
+  // resident pages pass, before the table load so that its wait does not
+  // also wait for that)
+  const uint16_t* qrow;
+  {
+    const int rr = r_ok ? r : q_len - 1;
+    const int64_t* qi = QUANT ? nullptr : q_index;
+    const int64_t qr = qi ? qi[q0 + rr] : (int64_t)(q0 + rr);
+    qrow = q + qr * q_ld + head * D;
+  }
+
+  // stage the page-table row straight into LDS (no VGPR round trip), in
+  // flight together with the Q loads below: 64 entries per wave and pass,
+  // lanes past the row's last page re-read it (their LDS slots, inside the
+  // padding, are never read)
+  const int kv0 = kv_first;
+  if (!CONTIG) {
     const int* trow = table + (int64_t)s * table_ld;
     const int npages = (kv_end + kPage - 1) / kPage;
-    for (int i = tid; i < npages; i += NT) pages_lds[i] = trow[i];
+    for (int b = wave * 64; b < npages; b += NT)
+      lds_dma4(trow + min(b + lane, npages - 1), (const uint8_t*)&pages_lds[b]);
   }
 
   // Q^T fragments (B operand): lane holds query `col`, d = c*16 + half*8 .. +8
   v8s qf[ND16];
   {
-    const int rr = r_ok ? r : q_len - 1;
-    const int64_t qr = q_index ? q_index[q0 + rr] : (int64_t)(q0 + rr);
-    const uint16_t* qrow = q + qr * q_ld + head * D;
 #pragma unroll
     for (int c = 0; c < ND16; ++c) qf[c] = *reinterpret_cast<const v8s*>(qrow + c * 16 + half * 8);
     // consume the Q fragments here, before any KV load is issued: the
@@ -355,6 +371,22 @@ __global__ __launch_bounds__(HPB * QSUB * 64) void paged_attention_kernel(
     lse[(int64_t)head * lse_ld + row] =
         l_run > 0.f ? (__log2f(l_run) + m_use) * 0.6931471805599453f : -INFINITY;
   }
+  // The wave's 32 output rows go out through LDS (the K/V buffers: after
+  // the last step's barrier every wave's loads have landed and its reads of
+  // them are consumed) so that each global store writes whole rows: from
+  // the MFMA layout a lane holds 4-value runs of one row, and every store
+  // instruction would touch 32 rows.
+  // LDS rows hold their 16-byte chunks XOR-swizzled by the row (chunk
+  // c of row rr at c ^ (rr % CH)), which spreads a store's 32 rows over
+  // the banks without padding
+  constexpr int OUT_BYTES = QUANT ? D : 2 * D;  // bytes of one head's row
+  constexpr int CH = OUT_BYTES / 16;            // 16-byte chunks per row
+  static_assert(NW * 32 * OUT_BYTES <= 2 * 2 * T_BYTES, "epilogue staging");
+  uint8_t* stage = &kv_lds[0][0][0] + wave * 32 * OUT_BYTES;
+  // byte b of row rr in the staged tile
+  auto slot = [&](int rr, int b) { return rr * OUT_BYTES + (((b >> 4) ^ (rr % CH)) << 4) + (b & 15); };
+  const int wave_row0 = qt * BQ + qsub * 32;         // the wave's first row in the sequence
+  const int rows_here = min(32, q_len - wave_row0);  // of which exist
   if (QUANT) {
     float amax = 0.f;
 #pragma unroll
@@ -368,30 +400,42 @@ __global__ __launch_bounds__(HPB * QSUB * 64) void paged_attention_kernel(
     amax = max_halves(amax);
     const float sc = fp8_scale(amax);
     const float rsc = recip(sc);
-    if (r_ok) {
-      uint8_t* orow = out8 + row * o_ld + head * D;
-#pragma unroll
-      for (int d = 0; d < NDS; ++d)
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int dd = d * 32 + g * 8 + half * 4;
-          *reinterpret_cast<uint32_t*>(orow + dd) =
-              pack4_fp8(div_by(o[d][g * 4], sc, rsc), div_by(o[d][g * 4 + 1], sc, rsc),
-                        div_by(o[d][g * 4 + 2], sc, rsc), div_by(o[d][g * 4 + 3], sc, rsc));
-        }
-      if (half == 0) scales[(int64_t)head * s_ld + row] = sc;
-    }
-  } else if (r_ok) {
-    uint16_t* orow = out16 + row * o_ld + head * D;
 #pragma unroll
     for (int d = 0; d < NDS; ++d)
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         const int dd = d * 32 + g * 8 + half * 4;
-        *reinterpret_cast<uint2*>(orow + dd) =
+        *reinterpret_cast<uint32_t*>(stage + slot(col, dd)) =
+            pack4_fp8(div_by(o[d][g * 4], sc, rsc), div_by(o[d][g * 4 + 1], sc, rsc),
+                      div_by(o[d][g * 4 + 2], sc, rsc), div_by(o[d][g * 4 + 3], sc, rsc));
+      }
+    if (r_ok && half == 0) scales[(int64_t)head * s_ld + row] = sc;
+  } else {
+#pragma unroll
+    for (int d = 0; d < NDS; ++d)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int dd = d * 32 + g * 8 + half * 4;
+        *reinterpret_cast<uint2*>(stage + slot(col, 2 * dd)) =
             make_uint2(pack2_bf16(o[d][g * 4] * inv, o[d][g * 4 + 1] * inv),
                        pack2_bf16(o[d][g * 4 + 2] * inv, o[d][g * 4 + 3] * inv));
       }
+  }
+  // the wave reads back what its other lanes wrote
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  constexpr int RPP = 64 / CH;  // rows per store instruction
+  uint8_t* obase = QUANT ? out8 : reinterpret_cast<uint8_t*>(out16);
+  const int64_t orow_bytes = QUANT ? o_ld : 2 * o_ld;
+#pragma unroll
+  for (int pass = 0; pass < 32 / RPP; ++pass) {
+    const int rr = pass * RPP + lane / CH;
+    const int ch = lane % CH;
+    const v4i val = *reinterpret_cast<const v4i*>(stage + slot(rr, ch * 16));
+    if (rr < rows_here)
+      *reinterpret_cast<v4i*>(obase + (int64_t)(q0 + wave_row0 + rr) * orow_bytes +
+                              head * OUT_BYTES + ch * 16) = val;
   }
 }
 
