@@ -249,10 +249,22 @@ def copy_calibration(mib: int) -> None:
     dst = torch.empty_like(src)
     ids = torch.arange(rows, dtype=torch.int64, device="cuda")
     torch.cuda.synchronize()
-    _lib.call("qx_embed", src.data_ptr(), COPY_ROW_ELEMS, ids.data_ptr(), dst.data_ptr(),
-              COPY_ROW_ELEMS, rows, COPY_ROW_ELEMS, torch.cuda.current_stream().cuda_stream)
+
+    def copy():
+        _lib.call("qx_embed", src.data_ptr(), COPY_ROW_ELEMS, ids.data_ptr(), dst.data_ptr(),
+                  COPY_ROW_ELEMS, rows, COPY_ROW_ELEMS, torch.cuda.current_stream().cuda_stream)
+    copy()
     torch.cuda.synchronize()
     log(f"calibration copy: {rows} rows x {2 * COPY_ROW_ELEMS} B = {mib} MiB")
+    # the same copy timed: the practical bandwidth of a read + write stream
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(5):
+        copy()
+    end.record()
+    torch.cuda.synchronize()
+    seconds = start.elapsed_time(end) * 1e-3 / 5
+    log(f"copy bandwidth: {2 * mib * 2**20 / seconds / 1e12:.2f} TB/s (read + write)")
     del src, dst, ids
 
 
