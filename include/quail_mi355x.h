@@ -46,7 +46,7 @@ int qx_device_is_gfx950(void);
  * (quail/backends/quail/executor/attention.py:479-490); weight scales are the
  * checkpoint's weight_scale_inv (attention.py:471-477).
  * K and N multiples of 128 (N of 256 for configs 0, 1, 3, 7, 10, 13-16,
- * 18-21). config selects the tile shape, tokens x weights, and the K depth
+ * 18-22). config selects the tile shape, tokens x weights, and the K depth
  * of a pipeline stage: 0: 256x256 (8 waves), 1: 256x256, 2: 128x128,
  * 3: 128x256, 4-6: 256x128 (3, 2, 4 stages of 64 K); 7-9: 256x256, 256x128,
  * 128x128 with fragments prefetched from LDS; 10-12: 256x256 (8 waves),
@@ -56,7 +56,10 @@ int qx_device_is_gfx950(void);
  * 18, 19: 256x256 with two wave groups a phase apart (group 0 loads / every
  * wave loads); 20: as 19 over four stages of 64 K; 21: 10 with each
  * block's rescale issued four MFMAs away from the MFMAs on either side of
- * it. Every config computes
+ * it; 22: 256x256 tiles walked by one persistent workgroup per CU, the
+ * next tile's first block loaded during the last block of the current one
+ * and the epilogue staged in two passes through one stage buffer. Every
+ * config computes
  * each element with the same operations in the same order: the results are
  * bit-identical.
  */
@@ -132,11 +135,13 @@ int qx_silu_mul_quant(const void* gate_up, int64_t gu_ld, void* q, int64_t q_ld,
  * for qx_gemm_fp8_blockscaled. Output as qx_silu_mul_quant's: Q (M x I)
  * e4m3 with leading dimension q_ld, Qs column-major (Qs[g * qs_ld + m]).
  * Bit-identical to qx_gemm_fp8_blockscaled (any config) followed by
- * qx_silu_mul_quant; the bf16 gate_up rows are never written.
+ * qx_silu_mul_quant; the bf16 gate_up rows are never written. config: 10
+ * (one workgroup per 256x256 tile) or 22 (persistent, as config 22 of
+ * qx_gemm_fp8_blockscaled); both give the same bits.
  */
 int qx_gemm_fp8_swiglu_quant(const void* A, const float* sA, const void* W, const float* sW,
                              void* Q, int64_t q_ld, float* Qs, int64_t qs_ld, int64_t M,
-                             int64_t I, int64_t K, int64_t lda, int64_t sa_ld,
+                             int64_t I, int64_t K, int64_t lda, int64_t sa_ld, int config,
                              hipStream_t stream);
 
 /*

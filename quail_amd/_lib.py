@@ -35,7 +35,7 @@ SIGNATURES = {
                         _i64, _f32, _p],
     "qx_silu_mul_quant": [_p, _i64, _p, _i64, _p, _i64, _i64, _i64, _p],
     "qx_gemm_fp8_swiglu_quant": [_p, _p, _p, _p, _p, _i64, _p, _i64, _i64, _i64, _i64, _i64,
-                                 _i64, _p],
+                                 _i64, _i32, _p],
     "qx_vocab_logprobs_workspace": [_i64, _i64, _i64],
     "qx_vocab_logprobs": [_p, _i64, _p, _i64, _p, _i64, _p, _i64, _i64, _i64, _i64, _p, _i64,
                           _p],

@@ -1022,6 +1022,246 @@ int launch128_swiglu(const void* A, const float* sA, const void* W, const float*
   QX_LAUNCH_STATUS();
 }
 
+// ---- persistent tiles with the K pipeline running across them ---------------
+// Measured on the one-tile-per-workgroup kernel (config 10): a tile's time is
+// ~13 us plus 1.77 us per 128-K block (M = 16384, N = 6144, K = 640 .. 10240),
+// i.e. at K = 2560 a quarter of it is the pipeline fill and the epilogue,
+// which every CU reaches at the same moment (all tiles take equally long),
+// so the first-stage loads and the C stores of all CUs arrive in one burst
+// while the matrix cores wait. Here one workgroup per CU walks its tiles and
+// the next tile's first block is loaded during the current tile's last
+// block, so it is in LDS by the time the epilogue ends; the epilogue stages
+// the tile through the last block's stage buffer only (two passes of 128
+// rows), leaving the prefetched block alone, with LDS-only barriers (no wait
+// on the loads in flight). 256 x 256 tiles, 8 waves, two 128-K stages; the
+// same arithmetic as config 10 in the same order (bit-identical).
+__device__ __forceinline__ void lgkm_barrier() {
+  // lgkmcnt(0) with vmcnt and expcnt unconstrained, then the barrier
+  __builtin_amdgcn_s_waitcnt((15) | (7 << 4) | (0 << 8) | (3 << 14));
+  asm volatile("s_barrier" ::: "memory");
+}
+
+template <bool SWIGLU>
+__global__ __launch_bounds__(512) void gemm_fp8_k128q_kernel(
+    const uint8_t* __restrict__ A, const float* __restrict__ sA, const uint8_t* __restrict__ W,
+    const float* __restrict__ sW, uint16_t* __restrict__ C, int M, int N, int K, int64_t lda,
+    int64_t ldc, int64_t sa_ld, int tiles_m, int tiles_n, int group_m, uint8_t* __restrict__ Q,
+    int64_t q_ld, float* __restrict__ Qs, int64_t qs_ld) {
+  constexpr int BM = 256, BN = 256, WAVES_N = 2, WAVES_M = 4;
+  using Cfg = Cfg128<BM, BN, WAVES_N, WAVES_M, 2>;
+  constexpr int TN = Cfg::kTN, TM = Cfg::kTM;
+  constexpr int kRowBytes = BN * 2 + 16;   // padded staging row (bank spread)
+  constexpr int kPassRows = WAVES_M * 32;  // tile rows staged per epilogue pass
+  constexpr int kRowsPerWave = kPassRows / Cfg::kWaves;
+  static_assert(kPassRows * kRowBytes <= Cfg::kStage, "an epilogue pass fits one stage");
+  static_assert(TM * kPassRows == BM, "passes cover the tile");
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[Cfg::kLds];
+
+  // this workgroup's tiles: a contiguous band of tile ids per XCD (i mod 8),
+  // walked with stride (workgroups per XCD); ids map to tiles in groups of
+  // group_m token tiles, as in the one-tile-per-workgroup kernels
+  const int total = tiles_m * tiles_n;
+  const int xcd = blockIdx.x & 7;
+  const int per_xcd = gridDim.x >> 3;  // the grid is a multiple of 8
+  const int local = blockIdx.x >> 3;
+  const int per = (total + 7) / 8;
+  const int full = total - (per - 1) * 8;
+  const int band0 = xcd < full ? xcd * per : full * per + (xcd - full) * (per - 1);
+  const int band = xcd < full ? per : per - 1;
+  const int my_tiles = local < band ? (band - local + per_xcd - 1) / per_xcd : 0;
+  const int width = group_m * tiles_n;
+  auto origin = [&](int iter, int& m0_, int& n0_) {
+    const int id = band0 + local + iter * per_xcd;
+    const int first_m = (id / width) * group_m;
+    const int gsize = min(tiles_m - first_m, group_m);
+    m0_ = (first_m + (id % width) % gsize) * BM;
+    n0_ = ((id % width) / gsize) * BN;
+  };
+  const int KT = K >> 7;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wn = wave % WAVES_N;
+  const int wm = wave / WAVES_N;
+
+  float sw0 = 0.0f, sw1 = 0.0f;  // the weight scale of the block in stage 0 / 1
+  auto issue = [&](int m0_, int n0_, int kb, int stage) {
+    uint8_t* buf = smem + stage * Cfg::kStage;
+    const int64_t k_off = (int64_t)kb * 128;
+    const int w_row0 = SWIGLU ? (n0_ >> 1) : n0_;
+    load_slabs128<Cfg::kASlabs>(A, lda, m0_, M - 1, k_off, buf, wave * Cfg::kASlabs, lane);
+    load_slabs128<Cfg::kWSlabs>(W, K, w_row0, N - 1, k_off, buf + Cfg::kABytes,
+                                wave * Cfg::kWSlabs, lane, SWIGLU ? (N >> 1) - 128 : 0);
+    const int t = min(m0_ + wave * Cfg::kSaPerWave + lane % Cfg::kSaPerWave, M - 1);
+    __builtin_amdgcn_global_load_lds((const void*)(sA + (int64_t)kb * sa_ld + t),
+                                     (lds_void*)(buf + Cfg::kABytes + Cfg::kWBytes + wave * 256),
+                                     4, 0, 0);
+    const float* sw_row =
+        sW + (int64_t)((SWIGLU ? w_row0 + wn * (N >> 1) : n0_ + wn * TN * 32) >> 7) * KT;
+    const float sw = __builtin_nontemporal_load(sw_row + kb);
+    if (stage) {
+      sw1 = sw;
+    } else {
+      sw0 = sw;
+    }
+  };
+
+  v16f acc[TN][TM];
+  float s_prev[TM];
+  int m0 = 0, n0 = 0;
+  if (my_tiles > 0) {
+    origin(0, m0, n0);
+    issue(m0, n0, 0, 0);
+  }
+  // block kb of a tile sits in stage kb & 1 (K / 128 is even), so the next
+  // tile's first block goes into stage 0 while the last one (stage 1) runs
+  for (int it = 0; it < my_tiles; ++it) {
+    int nm0 = m0, nn0 = n0;
+    const bool has_next = it + 1 < my_tiles;
+    if (has_next) origin(it + 1, nm0, nn0);
+#pragma unroll
+    for (int a = 0; a < TN; ++a)
+#pragma unroll
+      for (int b = 0; b < TM; ++b)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[a][b][e] = 0.0f;
+#pragma unroll
+    for (int b = 0; b < TM; ++b) s_prev[b] = 0.0f;
+    for (int kb0 = 0; kb0 < KT; kb0 += 2) {
+#pragma unroll
+      for (int stage = 0; stage < 2; ++stage) {
+        const int kb = kb0 + stage;
+        wait_vmcnt<0>();  // this block's operands (and earlier stores) are done
+        lds_barrier();
+        // the next block: this tile's, or after its last, the next tile's
+        // first (one call site: one set of load addresses live in the loop)
+        if (kb + 1 < KT || has_next) {
+          const bool same = kb + 1 < KT;
+          issue(same ? m0 : nm0, same ? n0 : nn0, same ? kb + 1 : 0, stage ^ 1);
+        }
+        const float sw =
+            __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(stage ? sw1 : sw0)));
+        if (sw != 0.0f) {  // wave-uniform; a zero weight-scale block adds nothing
+          const uint8_t* a_lds = smem + stage * Cfg::kStage;
+          const uint8_t* w_lds = a_lds + Cfg::kABytes;
+          const float* sa_lds = reinterpret_cast<const float*>(w_lds + Cfg::kWBytes);
+#pragma unroll
+          for (int b = 0; b < TM; ++b) {
+            const int row = wm * TM * 32 + b * 32 + (lane & 31);
+            const float s_cur =
+                sa_lds[(row / Cfg::kSaPerWave) * 64 + row % Cfg::kSaPerWave] * sw;
+            const float r = s_prev[b] / s_cur;
+#pragma unroll
+            for (int a = 0; a < TN; ++a)
+#pragma unroll
+              for (int e = 0; e < 16; ++e) acc[a][b][e] *= r;
+            s_prev[b] = s_cur;
+          }
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            v8i wf[TN], af[TM];
+#pragma unroll
+            for (int a = 0; a < TN; ++a)
+              wf[a] = read_frag128(w_lds, wn * TN * 32 + a * 32 + (lane & 31), h, lane);
+#pragma unroll
+            for (int b = 0; b < TM; ++b)
+              af[b] = read_frag128(a_lds, wm * TM * 32 + b * 32 + (lane & 31), h, lane);
+#pragma unroll
+            for (int a = 0; a < TN; ++a)
+#pragma unroll
+              for (int b = 0; b < TM; ++b)
+                acc[a][b] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+                    wf[a], af[b], acc[a][b], 0, 0, 0, 0, 0, 0);
+          }
+        }
+      }
+    }
+
+    // epilogue through stage 1 (the tile's last block), pass b holding rows
+    // wm * TM * 32 + b * 32 + (0..31) of every wave
+    uint8_t* buf = smem + Cfg::kStage;
+    const bool wide = ((ldc & 7) == 0) && ((reinterpret_cast<uintptr_t>(C) & 15) == 0);
+#pragma unroll
+    for (int b = 0; b < TM; ++b) {
+      // b == 0: every wave is done with the last block's operands; b > 0:
+      // with the previous pass's rows
+      lgkm_barrier();
+      {
+        const float s = s_prev[b];
+        uint8_t* lrow = buf + (wm * 32 + (lane & 31)) * kRowBytes;
+#pragma unroll
+        for (int a = 0; a < TN; ++a)
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            const int off = (wn * TN * 32 + a * 32 + (lane >> 5) * 4 + g * 8) * 2;
+            uint2 v;
+            v.x = pack2_bf16(acc[a][b][g * 4 + 0] * s, acc[a][b][g * 4 + 1] * s);
+            v.y = pack2_bf16(acc[a][b][g * 4 + 2] * s, acc[a][b][g * 4 + 3] * s);
+            *reinterpret_cast<uint2*>(lrow + off) = v;
+          }
+      }
+      lgkm_barrier();
+      if constexpr (SWIGLU) {
+        // 16 lanes per row: 8 gate and 8 up values each, one quant group
+        const int j0 = n0 >> 1;
+        const int seg = lane & 15;
+#pragma unroll
+        for (int i = 0; i < kRowsPerWave / 4; ++i) {
+          const int prow = wave * kRowsPerWave + i * 4 + (lane >> 4);
+          const int m = m0 + (prow >> 5) * TM * 32 + b * 32 + (prow & 31);
+          const uint8_t* lrow = buf + prow * kRowBytes;
+          const uint4 g = *reinterpret_cast<const uint4*>(lrow + seg * 16);
+          const uint4 u = *reinterpret_cast<const uint4*>(lrow + 256 + seg * 16);
+          const uint32_t gw[4] = {g.x, g.y, g.z, g.w}, uw[4] = {u.x, u.y, u.z, u.w};
+          float y[8];
+          float amax = 0.0f;
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            y[2 * k] = silu_mul(lo_bf16(gw[k]), lo_bf16(uw[k]));
+            y[2 * k + 1] = silu_mul(hi_bf16(gw[k]), hi_bf16(uw[k]));
+          }
+#pragma unroll
+          for (int k = 0; k < 8; ++k) amax = fmaxf(amax, fabsf(y[k]));
+          amax = group_max<16>(amax);
+          const float scale = fp8_scale(amax);
+          const float rs = recip(scale);
+          if (m < M) {
+            const v2i o = {(int)pack4_fp8(div_by(y[0], scale, rs), div_by(y[1], scale, rs),
+                                          div_by(y[2], scale, rs), div_by(y[3], scale, rs)),
+                           (int)pack4_fp8(div_by(y[4], scale, rs), div_by(y[5], scale, rs),
+                                          div_by(y[6], scale, rs), div_by(y[7], scale, rs))};
+            __builtin_nontemporal_store(o, reinterpret_cast<v2i*>(Q + (int64_t)m * q_ld + j0 +
+                                                                 seg * 8));
+            if (seg == 0) Qs[(int64_t)(j0 >> 7) * qs_ld + m] = scale;
+          }
+        }
+      } else {
+        constexpr int kChunks = BN / 8;
+        constexpr int kRowsPerOp = 64 / kChunks;
+        const int c = lane % kChunks;
+#pragma unroll
+        for (int i = 0; i < kRowsPerWave / kRowsPerOp; ++i) {
+          const int prow = wave * kRowsPerWave + i * kRowsPerOp + lane / kChunks;
+          const int m = m0 + (prow >> 5) * TM * 32 + b * 32 + (prow & 31);
+          const uint4 v = *reinterpret_cast<const uint4*>(buf + prow * kRowBytes + c * 16);
+          if (m < M) {
+            uint16_t* dst = C + (int64_t)m * ldc + n0 + c * 8;
+            if (wide) {
+              const v4i w = {(int)v.x, (int)v.y, (int)v.z, (int)v.w};
+              __builtin_nontemporal_store(w, reinterpret_cast<v4i*>(dst));
+            } else {
+              reinterpret_cast<uint2*>(dst)[0] = make_uint2(v.x, v.y);
+              reinterpret_cast<uint2*>(dst)[1] = make_uint2(v.z, v.w);
+            }
+          }
+        }
+      }
+    }
+    m0 = nm0;
+    n0 = nn0;
+  }
+}
+
+
 // ---- ping-pong variant ------------------------------------------------------
 // The 8 waves form two groups, waves 0-3 and 4-7 (one of each per SIMD), that
 // run the same code a phase apart: group 1 passes one extra barrier at the
@@ -1708,6 +1948,27 @@ inline int persistent_grid(int total) {
   return (total < cus[dev] ? total : cus[dev]) & ~7;
 }
 
+// the persistent kernel with the cross-tile pipeline (config 22; the SwiGLU
+// epilogue with Q != nullptr); too few tiles to share out, or an odd number
+// of 128-K blocks, fall back to one workgroup per tile
+template <bool SWIGLU>
+int launch128q(const void* A, const float* sA, const void* W, const float* sW, void* C, int M,
+               int N, int K, int64_t lda, int64_t ldc, int64_t sa_ld, void* Q, int64_t q_ld,
+               float* Qs, int64_t qs_ld, hipStream_t stream) {
+  const int tiles_m = (M + 255) / 256;
+  const int tiles_n = N / 256;
+  const int grid = persistent_grid(tiles_m * tiles_n);
+  if (grid < 8 || (K / 128) % 2) {  // the stage of a block is its parity within the tile
+    if (SWIGLU)
+      return launch128_swiglu(A, sA, W, sW, Q, q_ld, Qs, qs_ld, M, N, K, lda, sa_ld, stream);
+    return launch128<256, 256, 2, 4, 2>(A, sA, W, sW, C, M, N, K, lda, ldc, sa_ld, 4, stream);
+  }
+  hipLaunchKernelGGL((gemm_fp8_k128q_kernel<SWIGLU>), dim3(grid), dim3(512), 0, stream,
+                     (const uint8_t*)A, sA, (const uint8_t*)W, sW, (uint16_t*)C, M, N, K, lda,
+                     ldc, sa_ld, tiles_m, tiles_n, 4, (uint8_t*)Q, q_ld, Qs, qs_ld);
+  QX_LAUNCH_STATUS();
+}
+
 template <int BM, int BN, int WN, int WM>
 int launch128p(const void* A, const float* sA, const void* W, const float* sW, void* C, int M,
                int N, int K, int64_t lda, int64_t ldc, int64_t sa_ld, int group_m,
@@ -1758,7 +2019,7 @@ extern "C" {
 // I = intermediate width.
 int qx_gemm_fp8_swiglu_quant(const void* A, const float* sA, const void* W, const float* sW,
                              void* Q, int64_t q_ld, float* Qs, int64_t qs_ld, int64_t M,
-                             int64_t I, int64_t K, int64_t lda, int64_t sa_ld,
+                             int64_t I, int64_t K, int64_t lda, int64_t sa_ld, int config,
                              hipStream_t stream) {
   QX_CHECK(A && sA && W && sW && Q && Qs, "gemm_swiglu: null pointer");
   QX_CHECK(M >= 0 && I > 0 && K > 0, "gemm_swiglu: bad shape M=%lld I=%lld K=%lld",
@@ -1771,7 +2032,11 @@ int qx_gemm_fp8_swiglu_quant(const void* A, const float* sA, const void* W, cons
   QX_CHECK(qs_ld >= M && sa_ld >= M, "gemm_swiglu: scale strides");
   QX_CHECK(M < (1LL << 31) && 2 * I < (1LL << 31) && K < (1LL << 31), "gemm_swiglu: dims");
   QX_CHECK(((uintptr_t)A & 15) == 0 && ((uintptr_t)W & 15) == 0, "gemm_swiglu: alignment");
+  QX_CHECK(config == 10 || config == 22, "gemm_swiglu: config %d (10 or 22)", config);
   if (M == 0) return QX_OK;
+  if (config == 22)
+    return qx::launch128q<true>(A, sA, W, sW, nullptr, (int)M, (int)(2 * I), (int)K, lda, 0,
+                                sa_ld, Q, q_ld, Qs, qs_ld, stream);
   return qx::launch128_swiglu(A, sA, W, sW, Q, q_ld, Qs, qs_ld, (int)M, (int)(2 * I), (int)K, lda,
                               sa_ld, stream);
 }
@@ -1861,6 +2126,10 @@ int qx_gemm_fp8_blockscaled(const void* A, const float* sA, const void* W, const
     case 20:
       QX_CHECK(n % 256 == 0, "gemm config 20 needs N %% 256 == 0 (N=%d)", n);
       return qx::launch_pp64<256, 256>(A, sA, W, sW, C, m, n, k, lda, ldc, sa_ld, 4, stream);
+    case 22:
+      QX_CHECK(n % 256 == 0, "gemm config 22 needs N %% 256 == 0 (N=%d)", n);
+      return qx::launch128q<false>(A, sA, W, sW, C, m, n, k, lda, ldc, sa_ld, nullptr, 0,
+                                   nullptr, 0, stream);
     default:
       QX_CHECK(false, "gemm: unknown config %d", config);
   }

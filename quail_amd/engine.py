@@ -35,6 +35,7 @@ GROUP = 128
 # QUAIL_GEMM_CONFIG forces one.
 GEMM_CONFIG_ENV = "QUAIL_GEMM_CONFIG"
 GEMM_DEFAULT_CONFIG = 10
+SWIGLU_DEFAULT_CONFIG = 10
 GEMM_ODD_WIDTH_CONFIG = 5
 
 
@@ -53,6 +54,16 @@ def gemm_config(n: int, k: int, m: int) -> int:
     if n % 256:
         return GEMM_ODD_WIDTH_CONFIG
     return GEMM_DEFAULT_CONFIG
+
+
+def swiglu_config() -> int:
+    """Tile schedule of the gate_up GEMM with the SiLU-quant epilogue: 10
+    (one workgroup per tile) or 22 (persistent, the K pipeline running
+    across tiles), as for qx_gemm_fp8_blockscaled."""
+    forced = os.environ.get(GEMM_CONFIG_ENV)
+    if forced is not None and int(forced) in (10, 22):
+        return int(forced)
+    return SWIGLU_DEFAULT_CONFIG
 
 
 class Engine:
@@ -161,7 +172,8 @@ class Engine:
             start.record()
         _lib.call("qx_gemm_fp8_swiglu_quant", _ptr(q_input), _ptr(input_scale), _ptr(w),
                   _ptr(sw), _ptr(q), q.stride(0), _ptr(scales), self._scale_ld(scales), m, half,
-                  k, q_input.stride(0), self._scale_ld(input_scale), _stream())
+                  k, q_input.stride(0), self._scale_ld(input_scale), swiglu_config(),
+                  _stream())
         if timer is not None:
             end.record()
             timer.append((m, n, k, start, end, True))

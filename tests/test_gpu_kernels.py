@@ -98,7 +98,7 @@ def test_gemm_small_shapes_match_dequantized_matmul(m, n, k):
     _bf16_close(out, want)
 
 
-@pytest.mark.parametrize("config", list(range(22)))
+@pytest.mark.parametrize("config", list(range(23)))
 def test_gemm_tile_configs_agree(config, monkeypatch):
     q, s, wq, ws = _gemm_case(300, 512, 512, seed=9)
     monkeypatch.setenv("QUAIL_GEMM_CONFIG", str(config))
@@ -113,7 +113,7 @@ def test_gemm_configs_are_bit_identical(monkeypatch):
     row's result must not depend on it)."""
     q, s, wq, ws = _gemm_case(700, 1024, 1024, seed=11)
     outs = []
-    for config in range(22):
+    for config in range(23):
         monkeypatch.setenv("QUAIL_GEMM_CONFIG", str(config))
         outs.append(_run_gemm(q, s, wq, ws).cpu())
     for config, out in enumerate(outs):
@@ -127,10 +127,10 @@ def test_gemm_persistent_configs_with_several_tiles_per_workgroup(monkeypatch):
     configuration bit for bit, and the oracle to the bf16 tolerance."""
     q, s, wq, ws = _gemm_case(2125, 4096, 384, seed=13)
     outs = {}
-    for config in (10, 5, 16, 17, 18, 19, 20, 21):
+    for config in (10, 5, 16, 17, 18, 19, 20, 21, 22):
         monkeypatch.setenv("QUAIL_GEMM_CONFIG", str(config))
         outs[config] = _run_gemm(q, s, wq, ws).cpu()
-    for config in (5, 16, 17, 18, 19, 20, 21):
+    for config in (5, 16, 17, 18, 19, 20, 21, 22):
         assert torch.equal(outs[config], outs[10]), config
     _bf16_close(outs[16], ref.gemm(q, s, ref.RefLinear(wq, ws)))
 
@@ -147,8 +147,8 @@ def test_gemm_configs_agree_with_zero_weight_blocks(monkeypatch):
     ws[2, 3] = ws[2, 4] = 0.0
     ws[5, :] = 0.0
     outs = {}
-    for config in range(22):
-        if config in (0, 1, 3, 7, 10, 13, 14, 15, 16, 18, 19, 20, 21) and 768 % 256:
+    for config in range(23):
+        if config in (0, 1, 3, 7, 10, 13, 14, 15, 16, 18, 19, 20, 21, 22) and 768 % 256:
             continue
         monkeypatch.setenv("QUAIL_GEMM_CONFIG", str(config))
         outs[config] = _run_gemm(q, s, wq, ws).cpu()
@@ -160,7 +160,9 @@ def test_gemm_configs_agree_with_zero_weight_blocks(monkeypatch):
 
 @pytest.mark.parametrize("m,i,k,zero_blocks", [(700, 768, 512, False), (333, 1536, 256, True),
                                                (2000, 9728, 2560, False)])
-def test_gate_up_swiglu_quant_equals_gemm_then_activation_quant(m, i, k, zero_blocks):
+@pytest.mark.parametrize("config", ["10", "22"])
+def test_gate_up_swiglu_quant_equals_gemm_then_activation_quant(m, i, k, zero_blocks, config,
+                                                                 monkeypatch):
     """qx_gemm_fp8_swiglu_quant (gate_up GEMM with the SiLU-quant epilogue)
     against the two launches it replaces, bit for bit: a partial token tile,
     the Qwen3-4B gate_up shape (I = 9728, K = 2560) and weight blocks whose
@@ -181,11 +183,27 @@ def test_gate_up_swiglu_quant_equals_gemm_then_activation_quant(m, i, k, zero_bl
     scales.copy_(s.T)
     q_in = q.to(DEV)
     sv = scales.permute(1, 0)
+    monkeypatch.setenv("QUAIL_GEMM_CONFIG", "10")
     want_q, want_s = eng.activation_quant(eng.gemm(q_in, sv, lin))
+    monkeypatch.setenv("QUAIL_GEMM_CONFIG", config)
     got_q, got_s = eng.gate_up_activation_quant(q_in, sv, lin)
     assert got_q.shape == (m, i) and got_s.shape == (m, i // 128)
     assert torch.equal(got_q.view(torch.uint8), want_q.view(torch.uint8))
     assert torch.equal(got_s, want_s)
+
+
+@pytest.mark.parametrize("m,n,k", [(16294, 6144, 2560), (16294, 2560, 9728), (4000, 19456, 640)])
+def test_gemm_persistent_cross_tile_pipeline_at_pack_shapes(m, n, k, monkeypatch):
+    """Config 22 (persistent, the next tile's first block loaded during the
+    current tile's last) at a pack's qkv and down shapes, several tiles per
+    workgroup, and an odd number of 128-K blocks per tile (the stage parity
+    alternates from tile to tile): bit-identical to config 10."""
+    q, s, wq, ws = _gemm_case(m, n, k, seed=m + n + k)
+    outs = {}
+    for config in (10, 22):
+        monkeypatch.setenv("QUAIL_GEMM_CONFIG", str(config))
+        outs[config] = _run_gemm(q, s, wq, ws)
+    assert torch.equal(outs[10], outs[22])
 
 
 @pytest.mark.parametrize("k,n", [(2560, 6144), (4096, 2560), (2560, 19456), (9728, 2560)])
