@@ -479,6 +479,32 @@ __device__ __forceinline__ void load_slabs128(const uint8_t* __restrict__ g, int
   }
 }
 
+// load_slabs128 for a tile whose rows are all in bounds, split in two: the
+// per-lane byte offsets within a tile (the same for every tile), computed
+// once, and the loads of one K block from a wave-uniform base
+template <int SLABS>
+__device__ __forceinline__ void slab_offsets128(int64_t ld, int first, int lane, int hi_shift,
+                                                int64_t (&off)[SLABS]) {
+  const int r_in = lane >> 3;
+  const int p = lane & 7;
+#pragma unroll
+  for (int j = 0; j < SLABS; ++j) {
+    const int slab = first + j;
+    const int row = slab * 8 + r_in;
+    off[j] = (int64_t)(row + (slab >= 16 ? hi_shift : 0)) * ld + (p ^ swz128(row)) * 16;
+  }
+}
+
+template <int SLABS>
+__device__ __forceinline__ void load_slab_offsets128(const uint8_t* base, const int64_t (&off)[SLABS],
+                                                     uint8_t* lds, int first) {
+#pragma unroll
+  for (int j = 0; j < SLABS; ++j)
+    __builtin_amdgcn_global_load_lds((const void*)(base + off[j]),
+                                     (lds_void*)(lds + (first + j) * 1024), 16, 0,
+                                     kOperandLoadPolicy);
+}
+
 __device__ __forceinline__ v8i read_frag128(const uint8_t* lds, int row, int h, int lane) {
   const int c0 = h * 4 + (lane >> 5) * 2;
   const int sw = swz128(row);
@@ -1084,13 +1110,24 @@ __global__ __launch_bounds__(512) void gemm_fp8_k128q_kernel(
   const int wm = wave / WAVES_N;
 
   float sw0 = 0.0f, sw1 = 0.0f;  // the weight scale of the block in stage 0 / 1
+  // per-lane offsets of the operand rows within a tile, the same for every
+  // tile: a block's loads add a wave-uniform base (the one-tile kernel's
+  // hoisted addresses); only a token tile past the last row clamps per lane
+  int64_t a_off[Cfg::kASlabs], w_off[Cfg::kWSlabs];
+  slab_offsets128<Cfg::kASlabs>(lda, wave * Cfg::kASlabs, lane, 0, a_off);
+  slab_offsets128<Cfg::kWSlabs>(K, wave * Cfg::kWSlabs, lane, SWIGLU ? (N >> 1) - 128 : 0, w_off);
   auto issue = [&](int m0_, int n0_, int kb, int stage) {
     uint8_t* buf = smem + stage * Cfg::kStage;
     const int64_t k_off = (int64_t)kb * 128;
     const int w_row0 = SWIGLU ? (n0_ >> 1) : n0_;
-    load_slabs128<Cfg::kASlabs>(A, lda, m0_, M - 1, k_off, buf, wave * Cfg::kASlabs, lane);
-    load_slabs128<Cfg::kWSlabs>(W, K, w_row0, N - 1, k_off, buf + Cfg::kABytes,
-                                wave * Cfg::kWSlabs, lane, SWIGLU ? (N >> 1) - 128 : 0);
+    if (m0_ + BM <= M) {  // wave-uniform
+      load_slab_offsets128<Cfg::kASlabs>(A + (int64_t)m0_ * lda + k_off, a_off, buf,
+                                         wave * Cfg::kASlabs);
+    } else {
+      load_slabs128<Cfg::kASlabs>(A, lda, m0_, M - 1, k_off, buf, wave * Cfg::kASlabs, lane);
+    }
+    load_slab_offsets128<Cfg::kWSlabs>(W + (int64_t)w_row0 * K + k_off, w_off,
+                                       buf + Cfg::kABytes, wave * Cfg::kWSlabs);
     const int t = min(m0_ + wave * Cfg::kSaPerWave + lane % Cfg::kSaPerWave, M - 1);
     __builtin_amdgcn_global_load_lds((const void*)(sA + (int64_t)kb * sa_ld + t),
                                      (lds_void*)(buf + Cfg::kABytes + Cfg::kWBytes + wave * 256),
@@ -1133,7 +1170,8 @@ __global__ __launch_bounds__(512) void gemm_fp8_k128q_kernel(
         wait_vmcnt<0>();  // this block's operands (and earlier stores) are done
         lds_barrier();
         // the next block: this tile's, or after its last, the next tile's
-        // first (one call site: one set of load addresses live in the loop)
+        // first (its addresses replace this tile's, all of whose blocks are
+        // issued by then)
         if (kb + 1 < KT || has_next) {
           const bool same = kb + 1 < KT;
           issue(same ? m0 : nm0, same ? n0 : nn0, same ? kb + 1 : 0, stage ^ 1);
