@@ -176,7 +176,10 @@ def pack_chunk(arena, groups, *, attention_mode="unified", mask="causal", timing
         used=used, table=table, cu_q=cu_q, cu_q_host=cu_q.tolist(),
         used_host=used.tolist(),
         page_rows=[table[i, :c].tolist() for i, c in enumerate(seq_pages.tolist())],
-        max_q=max_q, max_used=max_used, causal=True)
+        max_q=max_q, max_used=max_used, causal=True,
+        # the scatter source is the pack's rows in order: row i's KV goes to
+        # dst[i], which lets qk_norm_rope write it in place
+        rows_in_order=bool(src.size == n_tok and np.array_equal(src, np.arange(n_tok))))
     meta = dict(layer=0, unified=unified, cu_a=cu_a,
                 max_a=int(np.diff(cu_a).max()) if len(cu_a) > 1 else 0,
                 final_query=_final_query(cu_q, used, table, final))
@@ -439,6 +442,7 @@ def upload(chunk: Chunk, staging: InputStaging) -> Chunk:
     dev = dict(u)
     dev["src"] = staging.copy("unified_src", u["src"], torch.int64)
     dev["dst"] = staging.copy("unified_dst", u["dst"], torch.int64)
+    dev["row_dst"] = dev["dst"] if u.get("rows_in_order") else None
     if u["tail_src"] is not None:
         dev["tail_src"] = staging.copy("tail_src", u["tail_src"], torch.int64)
         dev["tail_dst"] = staging.copy("tail_dst", u["tail_dst"], torch.int64)

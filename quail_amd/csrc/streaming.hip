@@ -228,12 +228,16 @@ __global__ __launch_bounds__(kRowThreads) void add_rmsnorm_kernel(
 // from cos_sin[pos] = [cos D/2 | sin D/2] (attention.py:833-879), fp32
 // throughout, bf16 output. A head is handled by D/8 lanes; each lane holds 4
 // columns of the first half (a) and the matching 4 of the second half (b).
-template <int D, bool CS_F32>
+// POOL: the row's K goes to pool row dst[row] of kp (ko unused) and its V
+// (the qkv columns after the K heads) to the same row of vp, converted to
+// fp16 as qx_kv_scatter converts it; dst[row] < 0 writes neither.
+template <int D, bool CS_F32, bool POOL>
 __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
     const uint16_t* __restrict__ qkv, int64_t qkv_ld, uint16_t* __restrict__ qo, int64_t qo_ld,
     uint16_t* __restrict__ ko, int64_t ko_ld, const void* __restrict__ cs,
     const int64_t* __restrict__ pos, const uint16_t* __restrict__ qw,
-    const uint16_t* __restrict__ kw, int n, int HQ, int HK, float eps) {
+    const uint16_t* __restrict__ kw, int n, int HQ, int HK, float eps,
+    uint16_t* __restrict__ kp, uint16_t* __restrict__ vp, const int64_t* __restrict__ dst) {
   constexpr int LPH = D / 8;       // lanes per head
   constexpr int HALF = D / 2;
   constexpr int HPB = 256 / LPH;   // heads per pass of the workgroup
@@ -241,6 +245,25 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
   const int slot = threadIdx.x / LPH;
   const int j = threadIdx.x % LPH;
   const int64_t p = pos[row];
+  const uint16_t* xrow = qkv + (int64_t)row * qkv_ld;
+  const int total = HQ + HK;
+  const int64_t kv_row = (int64_t)HK * D;
+  int64_t drow = 0;
+  if (POOL) {
+    drow = dst[row];
+    if (drow >= 0) {
+      const uint4* vs = reinterpret_cast<const uint4*>(xrow + total * D);
+      uint4* vd = reinterpret_cast<uint4*>(vp + drow * kv_row);
+      for (int c = threadIdx.x; c < (int)(kv_row >> 3); c += 256) {
+        uint4 w = vs[c];
+        w.x = pack2_f16(lo_bf16(w.x), hi_bf16(w.x));
+        w.y = pack2_f16(lo_bf16(w.y), hi_bf16(w.y));
+        w.z = pack2_f16(lo_bf16(w.z), hi_bf16(w.z));
+        w.w = pack2_f16(lo_bf16(w.w), hi_bf16(w.w));
+        vd[c] = w;
+      }
+    }
+  }
   float cosv[4], sinv[4];
   if (CS_F32) {
     const float* c = reinterpret_cast<const float*>(cs) + p * D;
@@ -255,8 +278,6 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
     cosv[0] = lo_bf16(c2.x); cosv[1] = hi_bf16(c2.x); cosv[2] = lo_bf16(c2.y); cosv[3] = hi_bf16(c2.y);
     sinv[0] = lo_bf16(s2.x); sinv[1] = hi_bf16(s2.x); sinv[2] = lo_bf16(s2.y); sinv[3] = hi_bf16(s2.y);
   }
-  const uint16_t* xrow = qkv + (int64_t)row * qkv_ld;
-  const int total = HQ + HK;
   for (int h0 = 0; h0 < total; h0 += HPB) {
     const int h = h0 + slot;
     const bool live = h < total;  // uniform across the LPH lanes of a head
@@ -284,8 +305,10 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
       oa[k] = xa * cosv[k] - xb * sinv[k];
       ob[k] = xb * cosv[k] + xa * sinv[k];
     }
-    if (live) {
-      uint16_t* out = is_q ? qo + (int64_t)row * qo_ld + h * D : ko + (int64_t)row * ko_ld + (h - HQ) * D;
+    if (live && (is_q || !POOL || drow >= 0)) {
+      uint16_t* out = is_q    ? qo + (int64_t)row * qo_ld + h * D
+                      : POOL ? kp + drow * kv_row + (h - HQ) * D
+                             : ko + (int64_t)row * ko_ld + (h - HQ) * D;
       *reinterpret_cast<uint2*>(out + j * 4) = make_uint2(pack2_bf16(oa[0], oa[1]), pack2_bf16(oa[2], oa[3]));
       *reinterpret_cast<uint2*>(out + HALF + j * 4) =
           make_uint2(pack2_bf16(ob[0], ob[1]), pack2_bf16(ob[2], ob[3]));
@@ -484,29 +507,56 @@ int qx_add_rmsnorm(const void* h, int64_t h_ld, const void* r, int64_t r_ld, con
   QX_LAUNCH_STATUS();
 }
 
+namespace {
+int qk_norm_rope_launch(const void* qkv, int64_t qkv_ld, void* q_out, int64_t q_ld, void* k_out,
+                        int64_t k_ld, const void* cos_sin, int cs_is_f32,
+                        const int64_t* positions, const void* q_w, const void* k_w, int64_t n,
+                        int64_t HQ, int64_t HK, int64_t D, float eps, void* k_pool, void* v_pool,
+                        const int64_t* dst, hipStream_t stream) {
+  QX_CHECK(D == 64 || D == 128, "qk_norm_rope: head_dim %lld (64 or 128)", (long long)D);
+  QX_CHECK(HQ > 0 && HK > 0, "qk_norm_rope: heads");
+  QX_CHECK(qkv_ld % 4 == 0 && q_ld % 4 == 0 && k_ld % 4 == 0, "qk_norm_rope: strides");
+  if (n == 0) return QX_OK;
+  dim3 grid((unsigned)n), block(256);
+#define QX_QK(DD, F32, P)                                                                      \
+  hipLaunchKernelGGL((qk_norm_rope_kernel<DD, F32, P>), grid, block, 0, stream,                \
+                     (const uint16_t*)qkv, qkv_ld, (uint16_t*)q_out, q_ld, (uint16_t*)k_out,  \
+                     k_ld, cos_sin, positions, (const uint16_t*)q_w, (const uint16_t*)k_w,    \
+                     (int)n, (int)HQ, (int)HK, eps, (uint16_t*)k_pool, (uint16_t*)v_pool, dst)
+#define QX_QK_D(DD, P) \
+  if (cs_is_f32) QX_QK(DD, true, P); else QX_QK(DD, false, P);
+  if (dst) {
+    if (D == 128) { QX_QK_D(128, true) } else { QX_QK_D(64, true) }
+  } else {
+    if (D == 128) { QX_QK_D(128, false) } else { QX_QK_D(64, false) }
+  }
+#undef QX_QK_D
+#undef QX_QK
+  QX_LAUNCH_STATUS();
+}
+}  // namespace
+
 int qx_qk_norm_rope(const void* qkv, int64_t qkv_ld, void* q_out, int64_t q_ld, void* k_out,
                     int64_t k_ld, const void* cos_sin, int cs_is_f32, const int64_t* positions,
                     const void* q_w, const void* k_w, int64_t n, int64_t HQ, int64_t HK, int64_t D,
                     float eps, hipStream_t stream) {
   QX_CHECK(qkv && q_out && k_out && cos_sin && positions && q_w && k_w,
            "qk_norm_rope: null pointer");
-  QX_CHECK(D == 64 || D == 128, "qk_norm_rope: head_dim %lld (64 or 128)", (long long)D);
-  QX_CHECK(HQ > 0 && HK > 0, "qk_norm_rope: heads");
-  QX_CHECK(qkv_ld % 4 == 0 && q_ld % 4 == 0 && k_ld % 4 == 0, "qk_norm_rope: strides");
-  if (n == 0) return QX_OK;
-  dim3 grid((unsigned)n), block(256);
-#define QX_QK(DD, F32)                                                                         \
-  hipLaunchKernelGGL((qk_norm_rope_kernel<DD, F32>), grid, block, 0, stream,                   \
-                     (const uint16_t*)qkv, qkv_ld, (uint16_t*)q_out, q_ld, (uint16_t*)k_out,  \
-                     k_ld, cos_sin, positions, (const uint16_t*)q_w, (const uint16_t*)k_w,    \
-                     (int)n, (int)HQ, (int)HK, eps)
-  if (D == 128) {
-    if (cs_is_f32) QX_QK(128, true); else QX_QK(128, false);
-  } else {
-    if (cs_is_f32) QX_QK(64, true); else QX_QK(64, false);
-  }
-#undef QX_QK
-  QX_LAUNCH_STATUS();
+  return qk_norm_rope_launch(qkv, qkv_ld, q_out, q_ld, k_out, k_ld, cos_sin, cs_is_f32,
+                             positions, q_w, k_w, n, HQ, HK, D, eps, nullptr, nullptr, nullptr,
+                             stream);
+}
+
+int qx_qk_norm_rope_kv(const void* qkv, int64_t qkv_ld, void* q_out, int64_t q_ld, void* k_pool,
+                       void* v_pool, const int64_t* dst, const void* cos_sin, int cs_is_f32,
+                       const int64_t* positions, const void* q_w, const void* k_w, int64_t n,
+                       int64_t HQ, int64_t HK, int64_t D, float eps, hipStream_t stream) {
+  QX_CHECK(qkv && q_out && k_pool && v_pool && dst && cos_sin && positions && q_w && k_w,
+           "qk_norm_rope_kv: null pointer");
+  QX_CHECK(qkv_ld % 8 == 0 && aligned16(qkv) && aligned16(k_pool) && aligned16(v_pool),
+           "qk_norm_rope_kv: alignment");
+  return qk_norm_rope_launch(qkv, qkv_ld, q_out, q_ld, nullptr, 0, cos_sin, cs_is_f32, positions,
+                             q_w, k_w, n, HQ, HK, D, eps, k_pool, v_pool, dst, stream);
 }
 
 int qx_silu_mul_quant(const void* gate_up, int64_t gu_ld, void* q, int64_t q_ld, float* scales,

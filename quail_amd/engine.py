@@ -271,22 +271,53 @@ class Engine:
                   _ptr(scales), self._scale_ld(scales), n, half, _stream())
         return q, scales
 
+    def _rope_cache(self):
+        cache = self.rotary.cos_sin_cache
+        if cache.dtype not in (torch.bfloat16, torch.float32):
+            raise ValueError(f"cos_sin_cache dtype {cache.dtype}")
+        if cache.shape[1] != self.head_dim:
+            raise ValueError(f"cos_sin_cache width {cache.shape[1]} != head_dim {self.head_dim}")
+        return cache
+
     def qk_norm_rope(self, qkv, positions, attn):
         """Per-head normed and rotated q and k from the fused qkv output."""
         n = qkv.shape[0]
         hq, hk, d = self.num_q_heads, self.num_kv_heads, self.head_dim
         q = torch.empty((n, hq * d), dtype=torch.bfloat16, device=qkv.device)
         k = torch.empty((n, hk * d), dtype=torch.bfloat16, device=qkv.device)
-        cache = self.rotary.cos_sin_cache
-        if cache.dtype not in (torch.bfloat16, torch.float32):
-            raise ValueError(f"cos_sin_cache dtype {cache.dtype}")
-        if cache.shape[1] != d:
-            raise ValueError(f"cos_sin_cache width {cache.shape[1]} != head_dim {d}")
+        cache = self._rope_cache()
         _lib.call("qx_qk_norm_rope", _ptr(qkv), qkv.stride(0), _ptr(q), q.stride(0), _ptr(k),
                   k.stride(0), _ptr(cache), int(cache.dtype == torch.float32), _ptr(positions),
                   _ptr(attn.q_norm.weight), _ptr(attn.k_norm.weight), n, hq, hk, d,
                   float(attn.q_norm.variance_epsilon), _stream())
         return q, k
+
+    def qk_norm_rope_kv(self, qkv, positions, attn, meta):
+        """qk_norm_rope that also writes every row's K and V into the arena
+        pages of meta's layer (pool row meta["unified"]["row_dst"][i]; the
+        fresh-row write of write_kv, attention.py:1178-1191, in the same pass
+        over qkv). Returns q; this layer's write_kv then copies only the
+        retained tails."""
+        n = qkv.shape[0]
+        hq, hk, d = self.num_q_heads, self.num_kv_heads, self.head_dim
+        if qkv.shape[1] < (hq + 2 * hk) * d:
+            raise ValueError(f"qkv width {qkv.shape[1]} < {(hq + 2 * hk) * d}")
+        dst = meta["unified"]["row_dst"]
+        if dst.shape[0] != n:
+            raise ValueError(f"row_dst has {dst.shape[0]} rows, qkv {n}")
+        layer = meta["layer"]
+        k_pool, v_pool = self.arena.layer_kv(layer)
+        if v_pool.dtype != torch.float16:
+            raise ValueError(f"V pool dtype {v_pool.dtype}: this engine keeps V pages in fp16")
+        q = torch.empty((n, hq * d), dtype=torch.bfloat16, device=qkv.device)
+        cache = self._rope_cache()
+        _lib.call("qx_qk_norm_rope_kv", _ptr(qkv), qkv.stride(0), _ptr(q), q.stride(0),
+                  _ptr(k_pool), _ptr(v_pool), _ptr(dst), _ptr(cache),
+                  int(cache.dtype == torch.float32), _ptr(positions), _ptr(attn.q_norm.weight),
+                  _ptr(attn.k_norm.weight), n, hq, hk, d, float(attn.q_norm.variance_epsilon),
+                  _stream())
+        meta["kv_fresh_layer"] = layer
+        return q
 
     def kv_row_scatter(self, k3, v3, src, dst, layer):
         """Scatter KV rows into the layer's arena pages; dst < 0 is padding.
@@ -312,7 +343,12 @@ class Engine:
         pool = meta["unified"]
         if pool is None:
             return
-        if pool["src"].numel():
+        # qk_norm_rope_kv already wrote this layer's fresh rows
+        fresh = meta.pop("kv_fresh_layer", None) != layer
+        if fresh and pool["src"].numel():
+            if k3 is None:
+                raise ValueError(f"layer {layer}: no K/V rows and none written by "
+                                 "qk_norm_rope_kv")
             self.kv_row_scatter(k3, v3, pool["src"], pool["dst"], layer)
         if copy_tail and pool.get("tail_src") is not None:
             k_pool, v_pool = self.arena.layer_kv(layer)
@@ -332,11 +368,20 @@ class Engine:
             if chunk.meta.get(key) is not None:
                 raise ValueError(f"this engine has no {key}-row attention path")
         q3 = q.view(n, hq, d)
-        k3 = k.view(n, hk, d)
-        v3 = v.view(n, hk, d) if v.is_contiguous() else v
+        k3, v3 = self._kv_views(n, k, v)
         if chunk.attention_mode == "tree":
+            if k3 is None:
+                raise ValueError("the tree path reads the pack's own K and V rows")
             return self.attention_tree(q3, k3, v3, chunk.meta, output=output)
         return self.attention_unified(q3, k3, v3, chunk.meta, output=output)
+
+    def _kv_views(self, n, k, v):
+        """(n, HK, D) views of flat K and V rows; None when qk_norm_rope_kv
+        wrote them to the pages already."""
+        if k is None:
+            return None, None
+        hk, d = self.num_kv_heads, self.head_dim
+        return k.view(n, hk, d), v.view(n, hk, d) if v.is_contiguous() else v
 
     def attention_tree(self, q3, k3, v3, meta, *, output=None, quantize=True):
         """The tree attention path (attention.py:1395-1441): the pack's KV
@@ -434,8 +479,7 @@ class Engine:
         fq = meta.get("final_query")
         if fq is None or meta["unified"] is None:
             raise ValueError("the pack carries no final-row attention metadata")
-        k3 = k.view(n, hk, d)
-        v3 = v.view(n, hk, d) if v.is_contiguous() else v
+        k3, v3 = self._kv_views(n, k, v)
         self.write_kv(k3, v3, meta)
         qf = q.view(n, hq, d).index_select(0, rows)
         out = self._paged(qf, fq, meta["layer"], None, None)

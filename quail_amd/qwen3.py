@@ -48,6 +48,9 @@ class Qwen3Pipeline:
         self.fuse_swiglu = (hasattr(self.engine, "gate_up_activation_quant") and
                             all(layer.mlp.gate_up_proj.weight.shape[0] % 256 == 0
                                 for layer in self.layers))
+        # qk-norm-rope writes the pack's K and V straight into the arena pages
+        # when the engine has it and the pack's scatter source is its own rows
+        self.fuse_kv_write = hasattr(self.engine, "qk_norm_rope_kv")
 
     def _check_bounds(self, chunk):
         """Token ids index the embedding and positions the rotary cache; the
@@ -68,8 +71,10 @@ class Qwen3Pipeline:
         return (layer.self_attn.qkv_proj, layer.self_attn.o_proj,
                 layer.mlp.gate_up_proj, layer.mlp.down_proj)
 
-    def before_attention(self, hidden, residual, positions, layer):
-        """Normalize and project rows into rotary Q, K, V and the residual."""
+    def before_attention(self, hidden, residual, positions, layer, chunk=None):
+        """Normalize and project rows into rotary Q, K, V and the residual.
+        With `chunk`, K and V may go straight to its arena pages (then k and
+        v are None)."""
         engine = self.engine
         attn = layer.self_attn
         if residual is None:
@@ -77,11 +82,15 @@ class Qwen3Pipeline:
             q_in, q_scale = engine.norm_quant(hidden, layer.input_layernorm)
         else:
             q_in, q_scale = engine.norm_quant(hidden, layer.input_layernorm, residual)
-        return self._project_qkv(q_in, q_scale, positions, attn) + (residual,)
+        return self._project_qkv(q_in, q_scale, positions, attn, chunk) + (residual,)
 
-    def _project_qkv(self, q_in, q_scale, positions, attn):
+    def _project_qkv(self, q_in, q_scale, positions, attn, chunk=None):
         engine = self.engine
         qkv = engine.gemm(q_in, q_scale, attn.qkv_proj)
+        if (chunk is not None and self.fuse_kv_write and chunk.attention_mode == "unified"
+                and not chunk.meta.get("kv_written", False)
+                and (chunk.meta.get("unified") or {}).get("row_dst") is not None):
+            return engine.qk_norm_rope_kv(qkv, positions, attn, chunk.meta), None, None
         q, k = engine.qk_norm_rope(qkv, positions, attn)
         v = qkv[:, (engine.num_q_heads + engine.num_kv_heads) * engine.head_dim:]
         return q, k, v
@@ -111,10 +120,11 @@ class Qwen3Pipeline:
         final = chunk.final_indices
         for index, layer in enumerate(self.layers):
             if index == 0:
-                q, k, v = self._project_qkv(q_in, q_scale, chunk.positions, layer.self_attn)
+                q, k, v = self._project_qkv(q_in, q_scale, chunk.positions, layer.self_attn,
+                                            chunk)
             else:
                 q, k, v, residual = self.before_attention(hidden, residual, chunk.positions,
-                                                          layer)
+                                                          layer, chunk)
             if index == last and chunk.meta.get("final_query") is not None:
                 # past the last layer's KV only the final rows matter: their
                 # attention, o_proj and MLP run alone, bit-identical to what

@@ -28,7 +28,7 @@ def ref_model(model) -> ref.RefModel:
 
 
 def run_stage(model, workload, readout_kind="margins", num_pages=None, use_tree=True,
-              attention_mode="unified"):
+              attention_mode="unified", fuse_kv_write=None):
     """Run one stage of the workload through the GPU engine; returns
     (results per document, StageRun)."""
     from quail_amd.arena import KVArena
@@ -44,6 +44,8 @@ def run_stage(model, workload, readout_kind="margins", num_pages=None, use_tree=
                     len(model.model.layers), num_pages, workload.page_tokens,
                     cfg.kv_heads, cfg.head_dim)
     pipe = Qwen3Pipeline(model, arena)
+    if fuse_kv_write is not None:
+        pipe.fuse_kv_write = fuse_kv_write
     labels = workload.label_ids
     if readout_kind == "classify":
         readout = ro.AsyncLabelLogprobs(model.lm_head.weight, labels, normalize=False)

@@ -333,6 +333,43 @@ def test_qk_norm_rope(hq, hk, d, cache_dtype):
     _bf16_close(k, k_ref, min_ulp1=0.998)
 
 
+@pytest.mark.parametrize("hq,hk,d", [(4, 2, 64), (32, 8, 128)])
+@pytest.mark.parametrize("cache_dtype", [torch.bfloat16, torch.float32])
+def test_qk_norm_rope_kv_equals_norm_rope_then_scatter(hq, hk, d, cache_dtype):
+    """The fused pass writes q, and K / fp16 V into pool rows dst[i], bit
+    for bit as qk_norm_rope followed by kv_row_scatter(src = 0..n-1);
+    dst < 0 rows write nothing."""
+    n, pool_rows = 93, 320
+    g = _gen(7 * hq + d)
+    qkv = (torch.randn(n, (hq + 2 * hk) * d, generator=g) * 3).to(torch.bfloat16).to(DEV)
+    pos = torch.randint(0, 4000, (n,), generator=g).to(DEV)
+    cache = ref.rope_cache(d, 4096, 1e6).to(cache_dtype).to(DEV)
+    attn = type("A", (), {})()
+    attn.q_norm = type("N", (), {"weight": (1 + 0.1 * torch.randn(d, generator=g)).to(
+        torch.bfloat16).to(DEV), "variance_epsilon": 1e-6})()
+    attn.k_norm = type("N", (), {"weight": (1 + 0.1 * torch.randn(d, generator=g)).to(
+        torch.bfloat16).to(DEV), "variance_epsilon": 1e-6})()
+    dst = torch.randperm(pool_rows, generator=g)[:n].to(DEV)
+    dst[[0, 17, n - 1]] = -1
+    pools = []
+    for _ in range(2):
+        kp = torch.full((pool_rows, hk, d), 7.0, dtype=torch.bfloat16, device=DEV)
+        vp = torch.full((pool_rows, hk, d), 7.0, dtype=torch.float16, device=DEV)
+        pools.append((kp, vp))
+    sep = _engine(hq, hk, d, arena=_Arena(*pools[0], 16), cache=cache)
+    q_ref, k = sep.qk_norm_rope(qkv, pos, attn)
+    sep.kv_row_scatter(k, qkv[:, (hq + hk) * d:], torch.arange(n, device=DEV), dst, 0)
+    fused = _engine(hq, hk, d, arena=_Arena(*pools[1], 16), cache=cache)
+    meta = {"layer": 0, "unified": {"row_dst": dst}}
+    q = fused.qk_norm_rope_kv(qkv, pos, attn, meta)
+    torch.cuda.synchronize()
+    assert meta["kv_fresh_layer"] == 0
+    assert torch.equal(q, q_ref)
+    assert torch.equal(pools[1][0], pools[0][0])
+    assert torch.equal(pools[1][1], pools[0][1])
+    assert int((pools[1][0].view(pool_rows, -1) != 7.0).all(1).sum()) == n - 3
+
+
 # ---- KV scatter and paged attention ---------------------------------------------------
 
 class _Arena:
