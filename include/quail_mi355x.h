@@ -276,6 +276,20 @@ int qx_merge_attn_quant(const void* a, int64_t a_ld, const void* b, int64_t b_ld
                         int64_t q_ld, float* scales, int64_t s_ld, hipStream_t stream);
 
 /*
+ * Call C's merge into call B's output (merge_partial, attention.py:407-429,
+ * called at :1424-1434 for label-path rows): for i < count and each head h,
+ * with r = index[i], lb = lse[h*lse_ld + r], lc = lse_c[h*lse_c_ld + i],
+ * top = max(lb, lc), wb = exp(lb - top), wc = exp(lc - top):
+ * out[r, h] = bf16(out[r, h] * (wb / (wb + wc)) + out_c[i, h] * (wc / (wb + wc)))
+ * and lse[h*lse_ld + r] = top + ln(wb + wc), in fp32. Rows hold H * D bf16
+ * (o_ld, c_ld elements apart); index must not repeat. A (row, head) with no
+ * keys on either side (top = -inf) is left unchanged.
+ */
+int qx_merge_partial(void* out, int64_t o_ld, float* lse, int64_t lse_ld, const int64_t* index,
+                     const void* out_c, int64_t c_ld, const float* lse_c, int64_t lse_c_ld,
+                     int64_t count, int64_t H, int64_t D, hipStream_t stream);
+
+/*
  * Last-token answer head over the retained head rows (t <= 16):
  * logits = normed . rows^T; mode 0 rounds logits to bf16 (AnswerRows.logits,
  * AsyncLabelLogprobs normalize=False: readout.py:44-48, 188-191), mode 1

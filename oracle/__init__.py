@@ -11,4 +11,5 @@ Modules:
   packing_ref.py brute-force checks of pack layouts (prefix tree, pages, KV reads)
   pages_ref.py  the page accounting of the KV arena, in plain Python
   pack_ref.py   the unified pack layout, in plain Python
+  labels_ref.py the label trie, its paths and each path row's context
 """

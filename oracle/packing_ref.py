@@ -82,14 +82,17 @@ def check_pack(chunk, page, pool: PoolModel, prompt_of_key):
     return checked
 
 
-def check_pack_tree(chunk, page, pool: PoolModel, prompt_of_key):
+def check_pack_tree(chunk, page, pool: PoolModel, prompt_of_key, context_of_row=None):
     """The tree layout's reads (attention.py:1395-1441): the pack's KV writes
     land in the pool first (kv_src -> kv_dst); a row then reads, in call B,
     its reader sequence's `used` keys through that sequence's table (not
-    causal) when source[row] >= 0, and in call A the rows of its own cu_a
-    segment up to itself. Together, in that order, they must be exactly its
-    document's tokens at positions 0..its own position. Returns the number
-    of rows checked; raises AssertionError naming the first bad row."""
+    causal) when source[row] >= 0, in call C (label-path rows,
+    reads["nodes"], :1424-1434) the gathered rows of its node sequence, and
+    in call A the rows of its own cu_a segment up to itself. Together, in
+    that order, they must be exactly its document's tokens at positions
+    0..its own position, or context_of_row(key, row) when that gives a
+    list. Returns the number of rows checked; raises AssertionError naming
+    the first bad row."""
     meta = chunk.meta
     host = chunk.host or {}
     ids = np.asarray(chunk.host_ids)
@@ -100,7 +103,20 @@ def check_pack_tree(chunk, page, pool: PoolModel, prompt_of_key):
         pool.apply(ids, positions, dict(src=kv_src, dst=kv_dst))
     reads = host.get("reads", meta.get("reads"))
     cu_a = np.asarray(host.get("segments", meta.get("segments"))["cu_q"], dtype=np.int64)
-    b_keys = {}
+    b_keys, c_keys = {}, {}
+    nodes = reads.get("nodes") if reads is not None else None
+    if nodes is not None:
+        q_rows = np.asarray(nodes["rows"], dtype=np.int64)
+        k_rows = np.asarray(nodes["key_rows"], dtype=np.int64)
+        ncu_q = np.asarray(nodes["cu_q"], dtype=np.int64)
+        ncu_k = np.asarray(nodes["cu_k"], dtype=np.int64)
+        b_index = np.asarray(nodes["b_index"], dtype=np.int64)
+        for s in range(len(ncu_q) - 1):
+            keys = [(int(ids[j]), int(positions[j])) for j in k_rows[ncu_k[s]:ncu_k[s + 1]]]
+            for i in range(int(ncu_q[s]), int(ncu_q[s + 1])):
+                c_keys[int(q_rows[i])] = keys
+        for i, r in enumerate(q_rows.tolist()):
+            assert int(np.asarray(reads["rows"])[b_index[i]]) == r, f"node row {r}: b_index"
     if reads is not None:
         rows = np.asarray(reads["rows"], dtype=np.int64)
         cu = np.asarray(reads["cu_q"], dtype=np.int64)
@@ -122,11 +138,13 @@ def check_pack_tree(chunk, page, pool: PoolModel, prompt_of_key):
         prompt = list(prompt_of_key(key))
         for r in range(row0, row1):
             pos = int(positions[r])
-            assert ids[r] == prompt[pos], f"row {r}: token {ids[r]} != prompt[{pos}]"
+            want = context_of_row(key, r) if context_of_row is not None else None
+            if want is None:
+                assert ids[r] == prompt[pos], f"row {r}: token {ids[r]} != prompt[{pos}]"
+                want = [(int(t), p) for p, t in enumerate(prompt[:pos + 1])]
             a0 = int(cu_a[seg_of[r]])
-            got = list(b_keys.get(r, [])) + [(int(ids[j]), int(positions[j]))
-                                             for j in range(a0, r + 1)]
-            want = [(int(t), p) for p, t in enumerate(prompt[:pos + 1])]
+            got = (list(b_keys.get(r, [])) + list(c_keys.get(r, []))
+                   + [(int(ids[j]), int(positions[j])) for j in range(a0, r + 1)])
             assert got == want, (f"row {r} of {key!r} at position {pos} reads "
                                  f"{got[:4]}...{got[-2:]} (len {len(got)}), want len {len(want)}")
             checked += 1

@@ -51,6 +51,7 @@ SIGNATURES = {
                          _i64, _i64, _f32, _i32, _p, _i64, _p, _i64, _p, _i64, _p],
     "qx_merge_attn_quant": [_p, _i64, _p, _i64, _p, _i64, _p, _i64, _p, _i64, _i64, _i64, _p,
                             _i64, _p, _i64, _p],
+    "qx_merge_partial": [_p, _i64, _p, _i64, _p, _p, _i64, _p, _i64, _i64, _i64, _i64, _p],
     "qx_prefix_tree": [_p, _p, _i64, _i64, _p, _p, _p],
     "qx_pages_create": [_i64, _i64, _p],
     "qx_pages_destroy": [_p],

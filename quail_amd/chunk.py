@@ -200,7 +200,7 @@ def pack_chunk(arena, groups, *, attention_mode="unified", mask="causal", timing
                  host_ids=ids, host_positions=positions)
 
 
-_TREE_UNSUPPORTED = ("canvas", "paths", "read_mask", "read_rows", "questions")
+_TREE_UNSUPPORTED = ("canvas", "read_rows", "questions")
 
 
 def _pack_tree(arena, groups, *, timing=None, attention_heads=None):
@@ -217,12 +217,21 @@ def _pack_tree(arena, groups, *, timing=None, attention_heads=None):
     in one sequence. Fresh rows of paged keys (and kept suffix rows) are
     written to the key's pages first (kv_src -> kv_dst), so a later suffix
     or a child can read them.
+
+    Label paths (`paths`, one suffix holding the trie paths back to back,
+    chunk.py:765-786): each path is its own call A segment at positions
+    f + its first node's depth onward, every path row reads the document's
+    pages in call B, and a path's rows read the rows above its first node
+    (leading rows of earlier paths, its `gathers`) in call C,
+    `reads["nodes"]` (chunk.py:894-907). `read_mask` marks the one
+    suffix's rows that feed the answer (chunk.py:726-741).
     """
     t0 = time.perf_counter()
     id_parts, pos_parts, finals, cu_a = [], [], [], [0]
     rows_per_answer, multi = [], False
     layout, row_spans, fresh_keys = [], [], []
     kv_writes, reader_rows, read_keys, read_used, cu_q = [], [], [], [], [0]
+    node_q, node_k, node_cu_q, node_cu_k = [], [], [0], [0]
     # the pages each read sequence goes through: its read key's table; a
     # stacked run whose read key has left the arena (its last borrower was
     # admitted) reads its first document's table, whose leading pages are
@@ -276,18 +285,56 @@ def _pack_tree(arena, groups, *, timing=None, attention_heads=None):
         total = int(slen.sum())
         ends = np.cumsum(slen)
         begins = ends - slen
+        paths = g.get("paths")
         if n:
             id_parts.append(sids)
-            within = np.arange(total, dtype=np.int64) - np.repeat(begins, slen)
-            pos_parts.append(f + within)
-            if g.get("read_all_rows"):
+            if g.get("read_mask") is not None:
+                marked = np.asarray(g["read_mask"], dtype=bool)
+                if n != 1 or len(marked) != total:
+                    raise ValueError(f"group {key!r}: read_mask marks one suffix's rows")
+                read = s_row0 + np.flatnonzero(marked)
+                finals.append(read)
+                rows_per_answer.append(np.array([len(read)], dtype=np.int64))
+                multi = True
+            elif g.get("read_all_rows"):
                 finals.append(np.arange(s_row0, s_row0 + total, dtype=np.int64))
                 rows_per_answer.append(slen)
                 multi = True
             else:
                 finals.append(s_row0 + ends - 1)
                 rows_per_answer.append(np.ones(n, dtype=np.int64))
-            cu_a.extend((s_row0 + ends).tolist())
+            if paths is not None:
+                if n != 1 or not g.get("read_all_rows") or fresh:
+                    raise ValueError(f"group {key!r}: paths pack one suffix of a resident "
+                                     f"document, every row read")
+                lengths = np.asarray([len(nodes) for nodes, _, _ in paths], dtype=np.int64)
+                if int(lengths.sum()) != total:
+                    raise ValueError(f"group {key!r}: paths hold {int(lengths.sum())} rows, "
+                                     f"the suffix {total}")
+                starts = np.asarray([first for _, first, _ in paths], dtype=np.int64)
+                path_ends = s_row0 + np.cumsum(lengths)
+                path_row0 = path_ends - lengths
+                pos_parts.append(f + np.repeat(starts, lengths)
+                                 + np.arange(total, dtype=np.int64)
+                                 - np.repeat(path_row0 - s_row0, lengths))
+                cu_a.extend(path_ends.tolist())
+                for index, (_, _, gathers) in enumerate(paths):
+                    if not gathers:
+                        continue
+                    if any(c >= index or count > lengths[c] for c, count in gathers):
+                        raise ValueError(f"group {key!r}: path {index} gathers rows outside "
+                                         f"the earlier paths")
+                    node_q.append(np.arange(path_row0[index], path_ends[index],
+                                            dtype=np.int64))
+                    node_k.append(np.concatenate([
+                        np.arange(path_row0[c], path_row0[c] + count, dtype=np.int64)
+                        for c, count in gathers]))
+                    node_cu_q.append(node_cu_q[-1] + int(lengths[index]))
+                    node_cu_k.append(node_cu_k[-1] + len(node_k[-1]))
+            else:
+                within = np.arange(total, dtype=np.int64) - np.repeat(begins, slen)
+                pos_parts.append(f + within)
+                cu_a.extend((s_row0 + ends).tolist())
             n_tok += total
             keep = int(g.get("write_suffix_tokens") or 0)
             if keep and paged:
@@ -326,6 +373,20 @@ def _pack_tree(arena, groups, *, timing=None, attention_heads=None):
         used = np.asarray(read_used, dtype=np.int32)
         reads = dict(rows=rows, cu_q=np.asarray(cu_q, dtype=np.int32), max_q=max_q, used=used,
                      max_used=int(used.max()), table=table, source=source, causal=False)
+    if node_q:
+        q_rows = _cat(node_q)
+        if reads is None or (reads["source"][q_rows] < 0).any():
+            raise ValueError("path rows read their document in call B; the document needs "
+                             "arena pages")
+        ncu_q = np.asarray(node_cu_q, dtype=np.int32)
+        ncu_k = np.asarray(node_cu_k, dtype=np.int32)
+        reads["nodes"] = dict(
+            rows=q_rows, key_rows=_cat(node_k), cu_q=ncu_q, cu_k=ncu_k,
+            used=np.diff(ncu_k).astype(np.int32), max_q=int(np.diff(ncu_q).max()),
+            max_used=int(np.diff(ncu_k).max()), causal=False,
+            # each node row's index among call B's rows
+            b_index=reads["source"][q_rows].astype(np.int64))
+        reads["nodes"]["max_k"] = reads["nodes"]["max_used"]
     kv_src = kv_dst = None
     if kv_writes:
         src, dst = [], []
@@ -342,8 +403,8 @@ def _pack_tree(arena, groups, *, timing=None, attention_heads=None):
                     max_q=int(np.diff(cu_a_arr).max()) if len(cu_a) > 1 else 0, causal=True)
     segments["max_used"] = segments["max_q"]
     if attention_heads is not None:
-        for tables in (segments, reads):
-            if tables is not None:
+        for tables in (segments, reads, reads and reads.get("nodes")):
+            if tables:
                 tables["work"], tables["n_work"] = _work_list(tables, attention_heads)
     ids = _cat(id_parts)
     positions = _cat(pos_parts)
@@ -491,5 +552,16 @@ def _upload_tree(chunk: Chunk, staging: InputStaging) -> Chunk:
                    source=staging.copy("read_source", reads["source"], torch.int32))
         if reads.get("work") is not None and reads["n_work"]:
             dev["work"] = staging.copy("read_work", reads["work"], torch.int32)
+        nodes = reads.get("nodes")
+        if nodes is not None:
+            dev["nodes"] = dict(
+                nodes, rows=staging.copy("node_rows", nodes["rows"], torch.int64),
+                key_rows=staging.copy("node_key_rows", nodes["key_rows"], torch.int64),
+                cu_q=staging.copy("node_cu_q", nodes["cu_q"], torch.int32),
+                cu_k=staging.copy("node_cu_k", nodes["cu_k"], torch.int32),
+                used=staging.copy("node_used", nodes["used"], torch.int32),
+                b_index=staging.copy("node_b_index", nodes["b_index"], torch.int64))
+            if nodes.get("work") is not None and nodes["n_work"]:
+                dev["nodes"]["work"] = staging.copy("node_work", nodes["work"], torch.int32)
         meta["reads"] = dev
     return chunk

@@ -482,6 +482,37 @@ int launch_attn(const void* q, int64_t q_ld, const int64_t* q_index, const void*
 // y = bf16(a + (b - a) * w), and y is quantized per head to e4m3 with
 // scale max(amax, 1e-10) / 448, as the o_proj input (QUANT, D = 128), or
 // stored as bf16 (QUANT off). One wave per (row, 512 columns): each lane
+// Call C's merge into call B's rows (merge_partial, attention.py:407-429):
+// one wave per (i, head); row index[i] of out / lse takes
+// out*wb/(wb+wc) + out_c*wc/(wb+wc) with wb = exp(lb - top), wc = exp(lc - top),
+// top = max(lb, lc), and lse top + ln(wb + wc); a pair with no keys on
+// either side (top = -inf) is left as it is.
+__global__ __launch_bounds__(256) void merge_partial_kernel(
+    uint16_t* __restrict__ out, int64_t o_ld, float* __restrict__ lse, int64_t l_ld,
+    const int64_t* __restrict__ index, const uint16_t* __restrict__ oc, int64_t c_ld,
+    const float* __restrict__ lc, int64_t lc_ld, int count, int H, int D) {
+  const int lane = threadIdx.x & 63;
+  const int wid = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (wid >= count * H) return;
+  const int i = wid / H;
+  const int h = wid % H;
+  const int64_t r = index[i];
+  const float b = lse[h * l_ld + r];
+  const float c = lc[h * lc_ld + i];
+  const float top = fmaxf(b, c);
+  if (top == -INFINITY) return;
+  const float wb = expf(b - top), wc = expf(c - top);
+  const float total = wb + wc;
+  const float fb = wb / total, fc = wc / total;
+  uint16_t* orow = out + r * o_ld + h * D;
+  const uint16_t* crow = oc + (int64_t)i * c_ld + h * D;
+  for (int e = lane; e < D; e += 64) {
+    const float y = bf16_to_f32(orow[e]) * fb + bf16_to_f32(crow[e]) * fc;
+    orow[e] = f32_to_bf16(y);
+  }
+  if (lane == 0) lse[h * l_ld + r] = top + logf(total);
+}
+
 // holds 8 consecutive values of one head.
 template <bool QUANT>
 __global__ __launch_bounds__(256) void merge_attn_quant_kernel(
@@ -667,6 +698,21 @@ int qx_merge_attn_quant(const void* a, int64_t a_ld, const void* b, int64_t b_ld
                        (const uint16_t*)a, a_ld, (const uint16_t*)b, b_ld, la, la_ld, lb, lb_ld,
                        source, (uint8_t*)q, q_ld, nullptr, 0, (int)n, width, blocks, (int)D);
   }
+  QX_LAUNCH_STATUS();
+}
+
+int qx_merge_partial(void* out, int64_t o_ld, float* lse, int64_t lse_ld, const int64_t* index,
+                     const void* out_c, int64_t c_ld, const float* lse_c, int64_t lse_c_ld,
+                     int64_t count, int64_t H, int64_t D, hipStream_t stream) {
+  QX_CHECK(out && lse && index && out_c && lse_c, "merge_partial: null pointer");
+  QX_CHECK((D == 64 || D == 128) && H > 0, "merge_partial: heads %lld x %lld", (long long)H,
+           (long long)D);
+  QX_CHECK(o_ld >= H * D && c_ld >= H * D && lse_c_ld >= count, "merge_partial: strides");
+  if (count == 0) return QX_OK;
+  const int64_t waves = count * H;
+  hipLaunchKernelGGL(qx::merge_partial_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0,
+                     stream, (uint16_t*)out, o_ld, lse, lse_ld, index, (const uint16_t*)out_c,
+                     c_ld, lse_c, lse_c_ld, (int)count, (int)H, (int)D);
   QX_LAUNCH_STATUS();
 }
 

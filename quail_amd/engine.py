@@ -387,7 +387,8 @@ class Engine:
         """The tree attention path (attention.py:1395-1441): the pack's KV
         writes into arena pages, then call A (causal over the pack's own rows
         in `cu_a` segments), call B (the reader rows over resident pages, not
-        causal), each with its log-sum-exp, and one fused merge + o_proj
+        causal; label-path rows also over their ancestor rows, call C, merged
+        into B), each with its log-sum-exp, and one fused merge + o_proj
         input quantization (attention.py:902-948). Returns (e4m3, scales),
         or with quantize=False the merged bf16 rows (for tests)."""
         n = q3.shape[0]
@@ -423,6 +424,8 @@ class Engine:
         lse_b = torch.empty((hq, max(nb, 1)), dtype=torch.float32, device=dev)
         self._lse_call(q3, reads["rows"], k_pool, v_pool, reads, reads["table"], None, scale,
                        out_b, lse_b)
+        if reads.get("nodes") is not None:
+            self._call_c(q3, k_rows, v_rows, reads["nodes"], scale, out_b, lse_b)
         args = (_ptr(out_a), out_a.stride(0), _ptr(out_b), out_b.stride(0), _ptr(lse_a),
                 lse_a.stride(0), _ptr(lse_b), lse_b.stride(0), _ptr(reads["source"]), n, hq, d)
         if d == GROUP and quantize:
@@ -439,6 +442,29 @@ class Engine:
             self.quant(merged, output=(o_q, o_s))
         meta["layer"] += 1
         return o_q, o_s
+
+    def _call_c(self, q3, k_rows, v_rows, nodes, scale, out_b, lse_b):
+        """Call C (attention.py:1424-1434): label-path rows over the rows
+        above their first node (gathered from the pack's own K and V rows),
+        not causal, merged into their call B rows (merge_partial)."""
+        hq, hk, d = self.num_q_heads, self.num_kv_heads, self.head_dim
+        dev = q3.device
+        nq = nodes["rows"].shape[0]
+        nk = nodes["key_rows"].shape[0]
+        row = hk * d
+        k_c = torch.empty((nk, row), dtype=torch.bfloat16, device=dev)
+        v_c = torch.empty((nk, row), dtype=torch.float16, device=dev)
+        into = torch.arange(nk, dtype=torch.int64, device=dev)
+        _lib.call("qx_kv_scatter", _ptr(k_rows), k_rows.stride(0), _ptr(v_rows), v_rows.stride(0),
+                  _ptr(k_c), _ptr(v_c), _ptr(nodes["key_rows"]), _ptr(into), nk, row, 0,
+                  _stream())
+        out_c = torch.empty((nq, hq * d), dtype=torch.bfloat16, device=dev)
+        lse_c = torch.empty((hq, max(nq, 1)), dtype=torch.float32, device=dev)
+        self._lse_call(q3, nodes["rows"], k_c, v_c, nodes, None, nodes["cu_k"], scale, out_c,
+                       lse_c)
+        _lib.call("qx_merge_partial", _ptr(out_b), out_b.stride(0), _ptr(lse_b), lse_b.stride(0),
+                  _ptr(nodes["b_index"]), _ptr(out_c), out_c.stride(0), _ptr(lse_c),
+                  lse_c.stride(0), nq, hq, d, _stream())
 
     def _lse_call(self, q3, q_index, k, v, tables, table, cu_k, scale, out, lse):
         """One qx_attention_lse call over `tables` (cu_q, used, max_q,

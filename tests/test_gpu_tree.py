@@ -284,3 +284,96 @@ def test_qwen3_4b_tree_attention_equals_the_unified_attention():
         print("tree vs unified attention, |diff| / head amax: quantiles 50/90/99/99.9% "
               + " ".join(f"{v:.2e}" for v in qs.tolist()) + f" max {rel.max().item():.2e}")
         assert qs[3].item() <= 2 ** -7 and rel.max().item() <= 2 ** -5
+
+
+@pytest.mark.parametrize("hq,hk,d,doc_len", [(32, 8, 128, 37), (4, 2, 64, 300)])
+@pytest.mark.parametrize("every_node", [False, True])
+def test_label_path_rows_attend_to_document_ancestors_and_path(hq, hk, d, doc_len, every_node):
+    """Trie-scored AI.CLASSIFY rows (attention.py:1395-1441 with call C,
+    :1424-1434, and merge_partial, :407-429): each path row's attention
+    output equals float32 attention over the document's keys (from its
+    pages), its trie ancestors' rows and itself, taken from the trie alone,
+    not from the pack's maps. Same tolerances as the other tree calls."""
+    from oracle.labels_ref import path_reads, path_tokens, read_nodes, trie_paths
+    from quail_amd.arena import KVArena
+    from quail_amd.chunk import InputStaging, pack_chunk, upload
+    from quail_amd.engine import Engine
+
+    labels = ((10,), (20, 21, 22), (20, 25, 26, 27, 28), (30, 31, 32), (30, 31, 33))
+    g = torch.Generator().manual_seed(doc_len + d)
+    arena = KVArena(1, 64, 16, hk, d)
+    engine = Engine(arena, num_q_heads=hq, num_kv_heads=hk, head_dim=d,
+                    rotary=type("R", (), {"cos_sin_cache": None})())
+    heads = (hq, hk, d)
+    doc = list(range(100, 100 + doc_len))
+    arena.activate("doc", doc_len)
+
+    def rows(n):
+        return [(torch.randn(n, h, d, generator=g) * s).to(torch.bfloat16).to(DEV)
+                for h, s in ((hq, 1.0), (hk, 1.0), (hk, 2.0))]
+
+    first = pack_chunk(arena, [dict(key="doc", prefix=doc, f=doc_len, suffixes=[])],
+                       attention_mode="tree", attention_heads=heads)
+    upload(first, InputStaging())
+    q1, k1, v1 = rows(doc_len)
+    engine.attention_tree(q1, k1, v1, first.meta, quantize=False)
+    read = None if every_node else read_nodes(labels)
+    paths = trie_paths(labels, read)
+    tokens = path_tokens(paths, 7)
+    chunk = pack_chunk(arena, [dict(key="doc", prefix=None, f=doc_len, suffixes=[tokens],
+                                    read_all_rows=True, paths=paths,
+                                    read_mask=None if every_node else path_reads(paths, read))],
+                       attention_mode="tree", attention_heads=heads)
+    assert chunk.meta["reads"].get("nodes") is not None
+    upload(chunk, InputStaging())
+    n = len(tokens)
+    q2, k2, v2 = rows(n)
+    out = engine.attention_tree(q2, k2, v2, chunk.meta, quantize=False)
+    torch.cuda.synchronize()
+    row_of = {node: i for i, node in enumerate(nd for nodes, _, _ in paths for nd in nodes)}
+    scale = d ** -0.5
+    for r, node in enumerate(nd for nodes, _, _ in paths for nd in nodes):
+        mine = [row_of[node[:depth]] for depth in range(len(node) + 1)]
+        k = torch.cat([k1, k2[mine]])
+        v = torch.cat([v1, v2[mine]])
+        want, _ = _ref_attention(q2[r:r + 1], k, v, scale, causal=False)
+        got = out[r].float().view(1, hq, d)
+        assert (got - want).abs().max().item() <= 2e-2, f"row {r} node {node}"
+
+
+def test_merge_partial_matches_the_reference_merge():
+    """qx_merge_partial against the reference's merge_partial
+    (attention.py:407-429) in float32: merged rows within one bf16 ulp (the
+    kernel may fuse the multiply-add), log-sum-exps to 1e-5; a row with no
+    call C keys (-inf) keeps its call B result."""
+    g = torch.Generator().manual_seed(5)
+    nb, nc, hq, d = 50, 20, 4, 128
+    out = torch.randn(nb, hq * d, generator=g).to(torch.bfloat16)
+    lse = torch.randn(hq, nb, generator=g) * 3
+    index = torch.randperm(nb, generator=g)[:nc]
+    oc = torch.randn(nc, hq * d, generator=g).to(torch.bfloat16)
+    lc = torch.randn(hq, nc, generator=g) * 3
+    lc[1, 3] = float("-inf")
+    lb = lse[:, index]
+    top = torch.maximum(lb, lc)
+    wb, wc = (lb - top).exp(), (lc - top).exp()
+    total = wb + wc
+    merged = (out[index].float().view(nc, hq, d) * (wb / total).T[..., None]
+              + oc.float().view(nc, hq, d) * (wc / total).T[..., None])
+    want_out = out.clone()
+    want_out[index] = merged.to(torch.bfloat16).view(nc, hq * d)
+    want_lse = lse.clone()
+    want_lse[:, index] = top + total.log()
+    o, l_, i_ = out.to(DEV), lse.to(DEV), index.to(DEV)
+    c, lcd = oc.to(DEV), lc.to(DEV)
+    _lib.call("qx_merge_partial", _p(o), o.stride(0), _p(l_), l_.stride(0), _p(i_), _p(c),
+              c.stride(0), _p(lcd), lcd.stride(0), nc, hq, d, _stream())
+    torch.cuda.synchronize()
+    got = o.float().cpu()
+    want = want_out.float()
+    diff = (got - want).abs()
+    assert bool((diff <= want.abs() * 2 ** -7 + 1e-30).all())
+    assert (diff == 0).float().mean() >= 0.99
+    torch.testing.assert_close(l_.cpu(), want_lse, rtol=1e-5, atol=1e-5)
+    r = int(index[3])
+    assert torch.equal(o[r, 1 * d:2 * d].cpu(), out[r, d:2 * d])

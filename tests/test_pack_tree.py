@@ -148,3 +148,78 @@ def test_siblings_share_one_stacked_read_of_their_parent():
     assert reads["rows"].tolist() == list(range(n_root, len(chunk.host_ids)))
     assert chunk.meta["cu_a"].tolist()[:2] == [0, n_root]
     check_pack_tree(chunk, 16, PoolModel(), {adm.keys[i]: d for i, d in enumerate(docs)}.__getitem__)
+
+
+# ---- label paths (trie-scored AI.CLASSIFY): call C --------------------------------------
+
+from oracle.labels_ref import (fed_nodes, label_trie, path_contexts, path_reads,  # noqa: E402
+                               path_tokens, read_nodes, trie_paths)
+
+LABELS = ((10,), (20, 21, 22), (20, 25, 26, 27, 28), (30, 31, 32), (30, 31, 33))
+SPLIT = ((10,), (20, 21), (20, 22), (30, 31, 32), (40,), (40, 41))
+
+
+def test_label_trie_known_answers():
+    # tests/planner/test_classify_cost.py:16, 106-108: LABELS feeds a 4-token
+    # suffix and reads 3 of its rows; :138-141: where SPLIT's labels split
+    read = read_nodes(LABELS)
+    paths = trie_paths(LABELS, read)
+    assert len(path_tokens(paths, 7)) == 4 and sum(path_reads(paths, read)) == 3
+    assert read == {(), (20,), (30, 31)}
+    assert read_nodes(SPLIT) == {(), (20,), (40,)}
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_trie_paths_hold_every_fed_node_once_and_gather_its_ancestors(seed):
+    rng = np.random.default_rng(seed)
+    labels = {tuple(rng.integers(1, 5, rng.integers(1, 6)).tolist())
+              for _ in range(rng.integers(2, 9))}
+    labels = sorted(labels)
+    for read in (None, read_nodes(labels)):
+        paths = trie_paths(labels, read)
+        fed = fed_nodes(set(label_trie(labels)) if read is None else read)
+        held = [node for nodes, _, _ in paths for node in nodes]
+        assert sorted(held) == sorted(fed) and len(held) == len(set(held))
+        where = {}
+        for p, (nodes, first, _) in enumerate(paths):
+            assert first == len(nodes[0])
+            assert all(b[:-1] == a for a, b in zip(nodes, nodes[1:]))
+            where.update({node: (p, r) for r, node in enumerate(nodes)})
+        for nodes, _, gathers in paths:
+            rows = {(c, r) for c, count in gathers for r in range(count)}
+            assert rows == {where[nodes[0][:d]] for d in range(len(nodes[0]))}
+
+
+@pytest.mark.parametrize("labels", [LABELS, SPLIT])
+@pytest.mark.parametrize("every_node", [False, True])
+def test_label_paths_read_their_document_ancestors_and_path(labels, every_node):
+    """Each path row reads the document (call B), the rows above its path's
+    first node (call C) and its path up to itself (call A): exactly the
+    document, the answer cue and its trie node's tokens."""
+    arena = plain_arena()
+    doc = list(range(100, 137))          # 37 tokens: the last page is partial
+    arena.activate("doc", len(doc))
+    pool = PoolModel()
+    first = pack_chunk(arena, [dict(key="doc", prefix=doc, f=len(doc), suffixes=[])],
+                       attention_mode="tree")
+    assert check_pack_tree(first, 16, pool, lambda k: doc) == len(doc)
+    read = None if every_node else read_nodes(labels)
+    paths = trie_paths(labels, read)
+    cue = 7
+    tokens = path_tokens(paths, cue)
+    mask = path_reads(paths, read)
+    group = dict(key="doc", prefix=None, f=len(doc), suffixes=[tokens], read_all_rows=True,
+                 paths=paths, read_mask=None if every_node else mask)
+    chunk = pack_chunk(arena, [group], attention_mode="tree")
+    contexts = path_contexts(paths, cue, doc)
+    assert check_pack_tree(chunk, 16, pool, lambda k: doc,
+                           lambda k, r: contexts[r]) == len(tokens)
+    assert chunk.final_indices.tolist() == [i for i, m in enumerate(mask) if m]
+    assert chunk.rows_per_answer.tolist() == ([len(tokens)] if every_node else [sum(mask)])
+    nodes = chunk.meta["reads"]["nodes"]
+    assert nodes["rows"].tolist() == list(range(len(paths[0][0]), len(tokens)))
+    with pytest.raises(ValueError, match="paths pack one suffix"):
+        pack_chunk(arena, [dict(group, read_all_rows=False)], attention_mode="tree")
+    with pytest.raises(ValueError, match="paths hold"):
+        pack_chunk(arena, [dict(group, suffixes=[tokens + [1]], read_mask=None)],
+                   attention_mode="tree")
