@@ -377,3 +377,51 @@ def test_merge_partial_matches_the_reference_merge():
     torch.testing.assert_close(l_.cpu(), want_lse, rtol=1e-5, atol=1e-5)
     r = int(index[3])
     assert torch.equal(o[r, 1 * d:2 * d].cpu(), out[r, d:2 * d])
+
+
+@pytest.mark.parametrize("every_node", [False, True])
+def test_tiny_label_path_pass_matches_each_label_prefix_run_whole(every_node):
+    """The whole pipeline in tree mode over a label-path pack (trie-scored
+    AI.CLASSIFY): a document is computed in one pack, then its trie paths in
+    the next, reading it from its pages (call B), their ancestors (call C)
+    and their own path (call A). Every read row's final-normed hidden state
+    equals the oracle's for its document + cue + node tokens run whole as
+    one prompt, within the tiny model's FP8 noise floor (relative 0.06, as
+    the unified pack's oracle test)."""
+    from oracle import qwen3_ref as ref
+    from oracle.labels_ref import path_reads, path_tokens, read_nodes, trie_paths
+    from quail_amd.arena import KVArena
+    from quail_amd.chunk import InputStaging, pack_chunk, upload
+    from quail_amd.qwen3 import Qwen3Pipeline
+    from tests.helpers import ref_model
+
+    cfg = CONFIGS["tiny"]
+    model = build_synthetic(cfg, seed=4, device="cuda", gen_device="cpu", norm_init="random")
+    wl = make_workload("tiny", seed=4)
+    doc = list(wl.prompts[0][:-1])
+    cue = int(wl.prompts[0][-1])
+    labels = ((10,), (20, 21, 22), (20, 25, 26, 27, 28), (30, 31, 32), (30, 31, 33))
+    arena = KVArena(cfg.layers, 256, 16, cfg.kv_heads, cfg.head_dim)
+    pipe = Qwen3Pipeline(model, arena)
+    heads = (cfg.heads, cfg.kv_heads, cfg.head_dim)
+    arena.activate("doc", len(doc))
+    first = pack_chunk(arena, [dict(key="doc", prefix=doc, f=len(doc), suffixes=[[cue]])],
+                       attention_mode="tree", attention_heads=heads)
+    upload(first, InputStaging())
+    pipe.forward_chunk(first)
+    read = None if every_node else read_nodes(labels)
+    paths = trie_paths(labels, read)
+    mask = path_reads(paths, read)
+    chunk = pack_chunk(arena, [dict(key="doc", prefix=None, f=len(doc),
+                                    suffixes=[path_tokens(paths, cue)], read_all_rows=True,
+                                    paths=paths, read_mask=None if every_node else mask)],
+                       attention_mode="tree", attention_heads=heads)
+    upload(chunk, InputStaging())
+    got = pipe.forward_chunk(chunk).float().cpu()
+    nodes = [nd for ns, _, _ in paths for nd in ns]
+    prompts = [doc + [cue] + list(nd) for nd, m in zip(nodes, mask) if m]
+    want = ref.forward_documents(ref_model(model), prompts).float()
+    assert got.shape == want.shape
+    rel = ((got - want).norm() / want.norm()).item()
+    print(f"label-path rows vs each prefix run whole: relative {rel:.4f}")
+    assert rel <= 0.06, rel
