@@ -100,6 +100,35 @@ def _pack_arrays(handle):
     return out
 
 
+def _suffix_reads(g, s_row0, slen):
+    """The answer rows of a group's suffixes (chunk.py:726-764): the marked
+    rows of its one suffix (`read_mask`), the last `read_rows[j]` rows of
+    suffix j, every row (`read_all_rows`), or each suffix's last row.
+    Returns (rows, rows per answer, several rows per answer?)."""
+    key = g["key"]
+    n = len(slen)
+    ends = s_row0 + np.cumsum(slen)
+    total = int(slen.sum())
+    if g.get("read_mask") is not None:
+        marked = np.asarray(g["read_mask"], dtype=bool)
+        if n != 1 or len(marked) != total:
+            raise ValueError(f"group {key!r}: read_mask marks one suffix's rows")
+        rows = s_row0 + np.flatnonzero(marked)
+        return rows, np.array([len(rows)], dtype=np.int64), True
+    if g.get("read_rows") is not None:
+        counts = np.asarray(g["read_rows"], dtype=np.int64)
+        if len(counts) != n or (counts > slen).any() or (counts < 0).any():
+            raise ValueError(f"group {key!r}: read_rows must give each suffix at most its "
+                             f"length")
+        rows = (np.repeat(ends - counts, counts)
+                + np.arange(int(counts.sum()), dtype=np.int64)
+                - np.repeat(np.cumsum(counts) - counts, counts))
+        return rows, counts, True
+    if g.get("read_all_rows"):
+        return np.arange(s_row0, s_row0 + total, dtype=np.int64), slen.astype(np.int64), True
+    return ends - 1, np.ones(n, dtype=np.int64), False
+
+
 def pack_chunk(arena, groups, *, attention_mode="unified", mask="causal", timing=None,
                attention_heads=None):
     """Pack groups for one unified causal forward pass (host arrays only).
@@ -130,10 +159,18 @@ def pack_chunk(arena, groups, *, attention_mode="unified", mask="causal", timing
         key = g["key"]
         if not acct.is_resident(key):
             raise ValueError(f"group {key!r}: the paged unified path needs arena pages")
+        if g.get("paths") is not None:
+            raise ValueError(f"group {key!r}: paths pack one suffix, every row read, under "
+                             f"tree attention")
+        for name in ("canvas", "questions"):
+            if g.get(name) is not None:
+                raise ValueError(f"group {key!r}: this engine has no {name} rows")
         keys.append(key)
         fresh = g.get("prefix") is not None
         prefix = np.asarray(g["prefix"], dtype=np.int64) if fresh else None
         sids, slen = _as_suffixes(g["suffixes"])
+        if g.get("read_mask") is not None or g.get("read_rows") is not None:
+            _suffix_reads(g, 0, slen)   # refuse bad answer rows before pages move
         if fresh:
             prefixes.append(prefix)
         suffix_lens.append(slen)
@@ -169,6 +206,13 @@ def pack_chunk(arena, groups, *, attention_mode="unified", mask="causal", timing
     table = table.reshape(-1, width)
     key_of = {acct.key_id(k): k for k in keys}
     spans = row_spans.reshape(-1, 3).tolist()
+    if any(g.get("read_mask") is not None or g.get("read_rows") is not None for g in groups):
+        # answer rows other than the last / every suffix row
+        parts = [_suffix_reads(g, span[1], slen)
+                 for g, span, slen in zip(groups, spans, suffix_lens) if len(slen)]
+        final = _cat([p[0] for p in parts])
+        rows_per_answer = _cat([p[1] for p in parts])
+        multi = any(p[2] for p in parts)
     unified = dict(
         src=src, dst=dst,
         tail_src=tail_src if has_tail else None,
@@ -200,7 +244,7 @@ def pack_chunk(arena, groups, *, attention_mode="unified", mask="causal", timing
                  host_ids=ids, host_positions=positions)
 
 
-_TREE_UNSUPPORTED = ("canvas", "read_rows", "questions")
+_TREE_UNSUPPORTED = ("canvas", "questions")
 
 
 def _pack_tree(arena, groups, *, timing=None, attention_heads=None):
@@ -288,21 +332,10 @@ def _pack_tree(arena, groups, *, timing=None, attention_heads=None):
         paths = g.get("paths")
         if n:
             id_parts.append(sids)
-            if g.get("read_mask") is not None:
-                marked = np.asarray(g["read_mask"], dtype=bool)
-                if n != 1 or len(marked) != total:
-                    raise ValueError(f"group {key!r}: read_mask marks one suffix's rows")
-                read = s_row0 + np.flatnonzero(marked)
-                finals.append(read)
-                rows_per_answer.append(np.array([len(read)], dtype=np.int64))
-                multi = True
-            elif g.get("read_all_rows"):
-                finals.append(np.arange(s_row0, s_row0 + total, dtype=np.int64))
-                rows_per_answer.append(slen)
-                multi = True
-            else:
-                finals.append(s_row0 + ends - 1)
-                rows_per_answer.append(np.ones(n, dtype=np.int64))
+            read, per_answer, several = _suffix_reads(g, s_row0, slen)
+            finals.append(read)
+            rows_per_answer.append(per_answer)
+            multi = multi or several
             if paths is not None:
                 if n != 1 or not g.get("read_all_rows") or fresh:
                     raise ValueError(f"group {key!r}: paths pack one suffix of a resident "

@@ -171,3 +171,38 @@ def test_tiny_paged_oracle_agrees_on_the_same_pack():
     torch.testing.assert_close(paged.float(), dense.float(), rtol=0.02, atol=0.02)
     rel = ((normed - dense.float()).norm() / dense.float().norm()).item()
     assert rel <= 0.06, rel     # the FP8 noise floor of the tiny model (see module doc)
+
+
+@pytest.mark.parametrize("mode", ["unified", "tree"])
+def test_read_rows_answers_equal_those_rows_of_read_all(mode):
+    """Several trailing answer rows per suffix (read_rows, chunk.py:742-756):
+    the same pack read with read_all_rows gives the same final-normed rows,
+    bit for bit (every kernel is row-local; in the unified pack the last
+    layer attends for the answer rows only)."""
+    from quail_amd.arena import KVArena
+    from quail_amd.chunk import InputStaging, pack_chunk, upload
+    from quail_amd.qwen3 import Qwen3Pipeline
+
+    cfg = CONFIGS["tiny"]
+    model = build_synthetic(cfg, seed=6, device="cuda", gen_device="cpu", norm_init="random")
+    docs = make_workload("tiny", seed=6).prompts[:3]
+    outs = {}
+    for name in ("all", "rows"):
+        arena = KVArena(cfg.layers, 256, 16, cfg.kv_heads, cfg.head_dim)
+        pipe = Qwen3Pipeline(model, arena)
+        groups = []
+        for i, d in enumerate(docs):
+            d = [int(t) for t in d]
+            arena.activate(i, len(d) - 8)
+            g = dict(key=i, prefix=d[:-8], f=len(d) - 8, suffixes=[d[-8:-5], d[-5:]])
+            g.update(read_all_rows=True) if name == "all" else g.update(read_rows=[2, 3])
+            groups.append(g)
+        chunk = pack_chunk(arena, groups, attention_mode=mode,
+                           attention_heads=(cfg.heads, cfg.kv_heads, cfg.head_dim))
+        final = chunk.final_indices.copy()
+        upload(chunk, InputStaging())
+        outs[name] = (pipe.forward_chunk(chunk).float().cpu(), final.tolist())
+    (all_rows, all_final), (got, final) = outs["all"], outs["rows"]
+    assert len(final) == 3 * 5 and got.shape[0] == len(final)
+    pick = [all_final.index(r) for r in final]
+    assert torch.equal(got, all_rows[pick])

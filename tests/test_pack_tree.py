@@ -223,3 +223,41 @@ def test_label_paths_read_their_document_ancestors_and_path(labels, every_node):
     with pytest.raises(ValueError, match="paths hold"):
         pack_chunk(arena, [dict(group, suffixes=[tokens + [1]], read_mask=None)],
                    attention_mode="tree")
+
+
+@pytest.mark.parametrize("mode", ["unified", "tree"])
+def test_read_rows_and_read_mask_pick_the_answer_rows(mode):
+    """read_rows: the last read_rows[j] rows of suffix j answer
+    (chunk.py:742-756); read_mask: the marked rows of a group's one suffix
+    (:726-741). Rows 0-3 and 12-13 are the two prefixes."""
+    arena = plain_arena()
+    arena.activate("a", 4)
+    arena.activate("b", 2)
+    groups = [dict(key="a", prefix=[1, 2, 3, 4], f=4,
+                   suffixes=[[10, 11, 12], [13], [14, 15, 16, 17]], read_rows=[2, 1, 3]),
+              dict(key="b", prefix=[5, 6], f=2, suffixes=[[20, 21, 22]], read_mask=[1, 0, 1])]
+    chunk = pack_chunk(arena, groups, attention_mode=mode)
+    assert chunk.final_indices.tolist() == [5, 6, 7, 9, 10, 11, 14, 16]
+    assert chunk.rows_per_answer.tolist() == [2, 1, 3, 2]
+    if mode == "unified":
+        # the last layer's final-row attention follows the answer rows
+        fq = chunk.meta["final_query"]
+        assert int(fq["cu_q"][-1]) == 8
+        for t in chunk.temporary_keys:
+            arena.free_key(t)
+    with pytest.raises(ValueError, match="read_rows"):
+        pack_chunk(arena, [dict(groups[0], read_rows=[4, 1, 1])], attention_mode=mode)
+    with pytest.raises(ValueError, match="read_mask"):
+        pack_chunk(arena, [dict(groups[1], read_mask=[1, 0])], attention_mode=mode)
+    assert arena.free_pages == arena.num_pages - 2   # nothing left behind
+
+
+def test_unified_refuses_paths_and_canvas():
+    arena = plain_arena()
+    arena.activate("a", 4)
+    with pytest.raises(ValueError, match="tree attention"):
+        pack_chunk(arena, [dict(key="a", prefix=[1, 2, 3, 4], f=4, suffixes=[[5]],
+                                read_all_rows=True, paths=[([()], 0, [])])])
+    with pytest.raises(ValueError, match="canvas"):
+        pack_chunk(arena, [dict(key="a", prefix=[1, 2, 3, 4], f=4, suffixes=[[5]],
+                                canvas=[1, 2])])
