@@ -37,6 +37,12 @@ GEMM_CONFIG_ENV = "QUAIL_GEMM_CONFIG"
 GEMM_DEFAULT_CONFIG = 10
 SWIGLU_DEFAULT_CONFIG = 10
 GEMM_ODD_WIDTH_CONFIG = 5
+# 22 = config 10's tiles on a persistent grid with the K pipeline running
+# across tiles: faster when the 256 x 256 tiles fill whole waves of the 256
+# CUs (the fill and epilogue of one tile overlap the next), slower on a
+# partial last wave, which one workgroup per tile spreads better
+GEMM_WHOLE_WAVES_CONFIG = 22
+CUS = 256
 
 
 def _ptr(t):
@@ -53,6 +59,10 @@ def gemm_config(n: int, k: int, m: int) -> int:
         return int(forced)
     if n % 256:
         return GEMM_ODD_WIDTH_CONFIG
+    tiles = -(-m // 256) * (n // 256)
+    if tiles >= CUS and tiles % CUS in (0,) + tuple(range(CUS - CUS // 8, CUS)) and \
+            (k // 128) % 2 == 0:
+        return GEMM_WHOLE_WAVES_CONFIG
     return GEMM_DEFAULT_CONFIG
 
 

@@ -52,3 +52,21 @@ def test_attention_work_list_is_heaviest_first_and_covers_every_tile():
     with pytest.raises(_lib.QxError, match="capacity"):
         _lib.count("qx_paged_attention_work", cu_q.ctypes.data, used.ctypes.data, 3, 32, 8,
                    128, 1, work.ctypes.data, 3)
+
+
+def test_gemm_config_choice_by_shape(monkeypatch):
+    """Persistent config 22 where 256 x 256 tiles fill whole waves of the 256
+    CUs (and K has an even number of 128-blocks), config 10 on a partial
+    last wave, config 5 for widths not a multiple of 256; the environment
+    variable forces one."""
+    from quail_amd.engine import GEMM_CONFIG_ENV, gemm_config
+    monkeypatch.delenv(GEMM_CONFIG_ENV, raising=False)
+    assert gemm_config(6144, 2560, 16294) == 22     # 64 x 24 tiles: 6 waves
+    assert gemm_config(6144, 2560, 16000) == 22     # 1512 tiles: last wave 91% full
+    assert gemm_config(2560, 4096, 16294) == 10     # 640 tiles: 2.5 waves
+    assert gemm_config(6144, 2560, 12000) == 10     # 1128 tiles
+    assert gemm_config(6144, 2688, 16294) == 10     # 21 K-blocks
+    assert gemm_config(6144, 2560, 256) == 10       # fewer tiles than CUs
+    assert gemm_config(2688, 2560, 16294) == 5
+    monkeypatch.setenv(GEMM_CONFIG_ENV, "14")
+    assert gemm_config(6144, 2560, 16294) == 14
