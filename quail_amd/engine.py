@@ -302,6 +302,26 @@ class Engine:
                   float(attn.q_norm.variance_epsilon), _stream())
         return q, k
 
+    def qk_norm_rope_rows(self, qkv, positions, attn):
+        """q, k and fp16 v rows in one pass over qkv (qx_qk_norm_rope_kv
+        with the identity row map): the tree path's call A reads K and V
+        of the pack's own rows contiguous, V in fp16 as the pages hold it."""
+        n = qkv.shape[0]
+        hq, hk, d = self.num_q_heads, self.num_kv_heads, self.head_dim
+        if qkv.shape[1] < (hq + 2 * hk) * d:
+            raise ValueError(f"qkv width {qkv.shape[1]} < {(hq + 2 * hk) * d}")
+        dev = qkv.device
+        q = torch.empty((n, hq * d), dtype=torch.bfloat16, device=dev)
+        k = torch.empty((n, hk * d), dtype=torch.bfloat16, device=dev)
+        v = torch.empty((n, hk * d), dtype=torch.float16, device=dev)
+        rows = torch.arange(n, dtype=torch.int64, device=dev)
+        cache = self._rope_cache()
+        _lib.call("qx_qk_norm_rope_kv", _ptr(qkv), qkv.stride(0), _ptr(q), q.stride(0), _ptr(k),
+                  _ptr(v), _ptr(rows), _ptr(cache), int(cache.dtype == torch.float32),
+                  _ptr(positions), _ptr(attn.q_norm.weight), _ptr(attn.k_norm.weight), n, hq,
+                  hk, d, float(attn.q_norm.variance_epsilon), _stream())
+        return q, k, v
+
     def qk_norm_rope_kv(self, qkv, positions, attn, meta):
         """qk_norm_rope that also writes every row's K and V into the arena
         pages of meta's layer (pool row meta["unified"]["row_dst"][i]; the
@@ -408,12 +428,16 @@ class Engine:
         if meta.get("kv_src") is not None and meta["kv_src"].numel():
             self.kv_row_scatter(k3, v3, meta["kv_src"], meta["kv_dst"], layer)
         # call A reads the pack's own K and V rows: contiguous, V in fp16 as
-        # the pages hold it (one identity scatter)
+        # the pages hold it (as qk_norm_rope_rows gives them, else one
+        # identity scatter)
         row = hk * d
-        k_rows = torch.empty((n, row), dtype=torch.bfloat16, device=dev)
-        v_rows = torch.empty((n, row), dtype=torch.float16, device=dev)
-        _lib.call("qx_kv_scatter", _ptr(k3), k3.stride(0), _ptr(v3), v3.stride(0), _ptr(k_rows),
-                  _ptr(v_rows), None, None, n, row, 1, _stream())
+        if (v3.dtype == torch.float16 and k3.is_contiguous() and v3.is_contiguous()):
+            k_rows, v_rows = k3.reshape(n, row), v3.reshape(n, row)
+        else:
+            k_rows = torch.empty((n, row), dtype=torch.bfloat16, device=dev)
+            v_rows = torch.empty((n, row), dtype=torch.float16, device=dev)
+            _lib.call("qx_kv_scatter", _ptr(k3), k3.stride(0), _ptr(v3), v3.stride(0),
+                      _ptr(k_rows), _ptr(v_rows), None, None, n, row, 1, _stream())
         scale = float(d ** -0.5)
         seg = meta["segments"]
         out_a = torch.empty((n, hq * d), dtype=torch.bfloat16, device=dev)

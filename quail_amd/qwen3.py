@@ -91,6 +91,9 @@ class Qwen3Pipeline:
                 and not chunk.meta.get("kv_written", False)
                 and (chunk.meta.get("unified") or {}).get("row_dst") is not None):
             return engine.qk_norm_rope_kv(qkv, positions, attn, chunk.meta), None, None
+        if (chunk is not None and self.fuse_kv_write and chunk.attention_mode == "tree"
+                and hasattr(engine, "qk_norm_rope_rows")):
+            return engine.qk_norm_rope_rows(qkv, positions, attn)
         q, k = engine.qk_norm_rope(qkv, positions, attn)
         v = qkv[:, (engine.num_q_heads + engine.num_kv_heads) * engine.head_dim:]
         return q, k, v

@@ -111,26 +111,30 @@ def test_tiny_if_score_and_classify_readouts():
     np.testing.assert_allclose(np.stack(logits), want_logits.numpy(), atol=0.05)
 
 
-def test_kv_write_in_qk_norm_rope_is_bit_identical(monkeypatch):
-    """The pipeline with K and V written by qk_norm_rope_kv gives the same
-    margins, bit for bit, as with the separate qk_norm_rope + kv_scatter,
-    and takes the fused path on every layer of every pack."""
+@pytest.mark.parametrize("mode", ["unified", "tree"])
+def test_kv_write_in_qk_norm_rope_is_bit_identical(monkeypatch, mode):
+    """The pipeline with K and V written by the qk-norm-rope pass (into the
+    pages, qk_norm_rope_kv; as contiguous rows with fp16 V for the tree
+    path, qk_norm_rope_rows) gives the same margins, bit for bit, as with
+    the separate qk_norm_rope + kv_scatter, and takes the fused path on
+    every layer of every pack."""
     from quail_amd.engine import Engine
 
     cfg = CONFIGS["tiny"]
     wl = make_workload("tiny", seed=5)
     model = build_synthetic(cfg, seed=5, device="cuda", gen_device="cpu", norm_init="random")
     calls = []
-    fused = Engine.qk_norm_rope_kv
+    name = "qk_norm_rope_kv" if mode == "unified" else "qk_norm_rope_rows"
+    fused = getattr(Engine, name)
 
     def counted(self, *args, **kwargs):
         calls.append(1)
         return fused(self, *args, **kwargs)
 
-    monkeypatch.setattr(Engine, "qk_norm_rope_kv", counted)
-    base, _ = run_stage(model, wl, "margins", fuse_kv_write=False)
+    monkeypatch.setattr(Engine, name, counted)
+    base, _ = run_stage(model, wl, "margins", fuse_kv_write=False, attention_mode=mode)
     assert not calls
-    got, run = run_stage(model, wl, "margins", fuse_kv_write=True)
+    got, run = run_stage(model, wl, "margins", fuse_kv_write=True, attention_mode=mode)
     assert len(calls) == cfg.layers * run.stats["chunks"]
     assert len(got) == len(base)
     assert all(np.array_equal(np.asarray(a), np.asarray(b)) for a, b in zip(got, base))
