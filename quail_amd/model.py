@@ -58,7 +58,7 @@ class Qwen3Config:
 
 
 CONFIGS = {
-    # 1 tiny, 3 Qwen3-4B, 4 Qwen3-8B, 5 Qwen3-32B-shaped
+    # the benchmark models: a 2-layer tiny model for tests, Qwen3-4B, -8B and -32B shapes
     "tiny": Qwen3Config("tiny", 2, 256, 4, 2, 64, 768, 4096, max_positions=4096),
     "qwen3-4b": Qwen3Config("qwen3-4b", 36, 2560, 32, 8, 128, 9728, 151936),
     "qwen3-8b": Qwen3Config("qwen3-8b", 36, 4096, 32, 8, 128, 12288, 151936),
