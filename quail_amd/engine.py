@@ -302,10 +302,12 @@ class Engine:
                   float(attn.q_norm.variance_epsilon), _stream())
         return q, k
 
-    def qk_norm_rope_rows(self, qkv, positions, attn):
+    def qk_norm_rope_rows(self, qkv, positions, attn, identity=None):
         """q, k and fp16 v rows in one pass over qkv (qx_qk_norm_rope_kv
-        with the identity row map): the tree path's call A reads K and V
-        of the pack's own rows contiguous, V in fp16 as the pages hold it."""
+        with the identity row map; `identity` = arange(n) int64 on the
+        device, made here when not given): the tree path's call A reads K
+        and V of the pack's own rows contiguous, V in fp16 as the pages
+        hold it."""
         n = qkv.shape[0]
         hq, hk, d = self.num_q_heads, self.num_kv_heads, self.head_dim
         if qkv.shape[1] < (hq + 2 * hk) * d:
@@ -314,7 +316,10 @@ class Engine:
         q = torch.empty((n, hq * d), dtype=torch.bfloat16, device=dev)
         k = torch.empty((n, hk * d), dtype=torch.bfloat16, device=dev)
         v = torch.empty((n, hk * d), dtype=torch.float16, device=dev)
-        rows = torch.arange(n, dtype=torch.int64, device=dev)
+        rows = identity if identity is not None else torch.arange(n, dtype=torch.int64,
+                                                                   device=dev)
+        if rows.shape[0] != n or rows.dtype != torch.int64:
+            raise ValueError("identity must be arange(n) int64")
         cache = self._rope_cache()
         _lib.call("qx_qk_norm_rope_kv", _ptr(qkv), qkv.stride(0), _ptr(q), q.stride(0), _ptr(k),
                   _ptr(v), _ptr(rows), _ptr(cache), int(cache.dtype == torch.float32),

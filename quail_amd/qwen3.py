@@ -10,8 +10,12 @@ projection; the final norm runs on `chunk.final_indices` only.
 Launches are fused relative to the reference's sequence, with identical
 results: the embedding gather with layer 0's norm_quant; the gate_up
 projection with the SiLU-gated product and its quant (the bf16 gate_up rows
-are never written); the final-row gather with the final fused_add_rms_norm.
+are never written); the final-row gather with the final fused_add_rms_norm;
+the pack's K and V writes with the qk-norm-rope pass (into the arena pages
+for a unified pack, as the contiguous rows call A reads for a tree pack).
 """
+
+import torch
 
 from quail_amd.engine import Engine
 
@@ -93,7 +97,11 @@ class Qwen3Pipeline:
             return engine.qk_norm_rope_kv(qkv, positions, attn, chunk.meta), None, None
         if (chunk is not None and self.fuse_kv_write and chunk.attention_mode == "tree"
                 and hasattr(engine, "qk_norm_rope_rows")):
-            return engine.qk_norm_rope_rows(qkv, positions, attn)
+            identity = chunk.meta.get("identity_rows")
+            if identity is None or identity.shape[0] != qkv.shape[0]:
+                identity = torch.arange(qkv.shape[0], dtype=torch.int64, device=qkv.device)
+                chunk.meta["identity_rows"] = identity
+            return engine.qk_norm_rope_rows(qkv, positions, attn, identity)
         q, k = engine.qk_norm_rope(qkv, positions, attn)
         v = qkv[:, (engine.num_q_heads + engine.num_kv_heads) * engine.head_dim:]
         return q, k, v
