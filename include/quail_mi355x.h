@@ -122,14 +122,18 @@ int qx_qk_norm_rope(const void* qkv, int64_t qkv_ld, void* q_out, int64_t q_ld, 
  * above; the normed, rotated K of row i goes to pool row dst[i] of k_pool and
  * its V (qkv columns (HQ+HK)*D .. (HQ+2*HK)*D, bf16) to the same row of
  * v_pool converted to fp16; dst[i] < 0 writes neither. Pool rows are HK*D
- * elements. The same values as qx_qk_norm_rope followed by qx_kv_scatter
- * (src = 0..n-1, v_to_f16 = 1), in one pass over qkv: it fuses
- * Engine.qk_norm_rope (attention.py:1251-1255) with the fresh-row write of
- * Engine.write_kv (attention.py:1178-1191) when the pack's scatter source is
- * its own rows in order; the retained-tail copy stays a qx_kv_scatter.
+ * elements. dst2 (may be NULL): the same K and V rows also go to row
+ * dst2[i] (when >= 0) of k_pool2 / v_pool2 (the tree path: contiguous rows
+ * for call A, dst = 0..n-1, and the arena pages). The same values as
+ * qx_qk_norm_rope followed by qx_kv_scatter (src = 0..n-1, v_to_f16 = 1), in
+ * one pass over qkv: it fuses Engine.qk_norm_rope (attention.py:1251-1255)
+ * with the fresh-row write of Engine.write_kv (attention.py:1178-1191) when
+ * the pack's scatter source is its own rows in order; the retained-tail copy
+ * stays a qx_kv_scatter.
  */
 int qx_qk_norm_rope_kv(const void* qkv, int64_t qkv_ld, void* q_out, int64_t q_ld, void* k_pool,
-                       void* v_pool, const int64_t* dst, const void* cos_sin, int cs_is_f32,
+                       void* v_pool, const int64_t* dst, void* k_pool2, void* v_pool2,
+                       const int64_t* dst2, const void* cos_sin, int cs_is_f32,
                        const int64_t* positions, const void* q_w, const void* k_w, int64_t n,
                        int64_t HQ, int64_t HK, int64_t D, float eps, hipStream_t stream);
 

@@ -33,8 +33,8 @@ SIGNATURES = {
     "qx_add_rmsnorm": [_p, _i64, _p, _i64, _p, _p, _p, _i64, _p, _i64, _i64, _i64, _f32, _p],
     "qx_qk_norm_rope": [_p, _i64, _p, _i64, _p, _i64, _p, _i32, _p, _p, _p, _i64, _i64, _i64,
                         _i64, _f32, _p],
-    "qx_qk_norm_rope_kv": [_p, _i64, _p, _i64, _p, _p, _p, _p, _i32, _p, _p, _p, _i64, _i64,
-                           _i64, _i64, _f32, _p],
+    "qx_qk_norm_rope_kv": [_p, _i64, _p, _i64, _p, _p, _p, _p, _p, _p, _p, _i32, _p, _p, _p,
+                           _i64, _i64, _i64, _i64, _f32, _p],
     "qx_silu_mul_quant": [_p, _i64, _p, _i64, _p, _i64, _i64, _i64, _p],
     "qx_gemm_fp8_swiglu_quant": [_p, _p, _p, _p, _p, _i64, _p, _i64, _i64, _i64, _i64, _i64,
                                  _i64, _i32, _p],

@@ -431,6 +431,12 @@ def _pack_tree(arena, groups, *, timing=None, attention_heads=None):
             src.append(np.arange(r0, r1, dtype=np.int64))
             dst.append(rows)
         kv_src, kv_dst = _cat(src), _cat(dst)
+    # pool row per pack row (-1: none), for the qk-norm-rope pass to write
+    # the KV of the pack's rows into the pages itself
+    row_pool_dst = None
+    if kv_src is not None and len(np.unique(kv_src)) == len(kv_src):
+        row_pool_dst = np.full(n_tok, -1, dtype=np.int64)
+        row_pool_dst[kv_src] = kv_dst
     cu_a_arr = np.asarray(cu_a, dtype=np.int32)
     segments = dict(cu_q=cu_a_arr, used=np.diff(cu_a_arr).astype(np.int32),
                     max_q=int(np.diff(cu_a_arr).max()) if len(cu_a) > 1 else 0, causal=True)
@@ -442,7 +448,8 @@ def _pack_tree(arena, groups, *, timing=None, attention_heads=None):
     ids = _cat(id_parts)
     positions = _cat(pos_parts)
     final = _cat(finals)
-    meta = dict(layer=0, unified=None, kv_src=kv_src, kv_dst=kv_dst, reads=reads,
+    meta = dict(layer=0, unified=None, kv_src=kv_src, kv_dst=kv_dst, row_pool_dst=row_pool_dst,
+                reads=reads,
                 segments=segments, cu_a=cu_a_arr, max_a=segments["max_q"])
     if timing is not None:
         timing["pack_py"] = timing.get("pack_py", 0.0) + (t1 - t0)
@@ -569,6 +576,9 @@ def _upload_tree(chunk: Chunk, staging: InputStaging) -> Chunk:
     if meta["kv_src"] is not None:
         meta["kv_src"] = staging.copy("kv_src", meta["kv_src"], torch.int64)
         meta["kv_dst"] = staging.copy("kv_dst", meta["kv_dst"], torch.int64)
+    if meta.get("row_pool_dst") is not None:
+        chunk.host["row_pool_dst"] = meta["row_pool_dst"]
+        meta["row_pool_dst"] = staging.copy("row_pool_dst", meta["row_pool_dst"], torch.int64)
     seg = meta["segments"]
     dev = dict(seg, cu_q=staging.copy("cu_a", seg["cu_q"], torch.int32),
                used=staging.copy("segment_lengths", seg["used"], torch.int32))

@@ -230,14 +230,16 @@ __global__ __launch_bounds__(kRowThreads) void add_rmsnorm_kernel(
 // columns of the first half (a) and the matching 4 of the second half (b).
 // POOL: the row's K goes to pool row dst[row] of kp (ko unused) and its V
 // (the qkv columns after the K heads) to the same row of vp, converted to
-// fp16 as qx_kv_scatter converts it; dst[row] < 0 writes neither.
+// fp16 as qx_kv_scatter converts it; dst[row] < 0 writes neither. With dst2,
+// the same K and V rows also go to row dst2[row] (when >= 0) of kp2 / vp2.
 template <int D, bool CS_F32, bool POOL>
 __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
     const uint16_t* __restrict__ qkv, int64_t qkv_ld, uint16_t* __restrict__ qo, int64_t qo_ld,
     uint16_t* __restrict__ ko, int64_t ko_ld, const void* __restrict__ cs,
     const int64_t* __restrict__ pos, const uint16_t* __restrict__ qw,
     const uint16_t* __restrict__ kw, int n, int HQ, int HK, float eps,
-    uint16_t* __restrict__ kp, uint16_t* __restrict__ vp, const int64_t* __restrict__ dst) {
+    uint16_t* __restrict__ kp, uint16_t* __restrict__ vp, const int64_t* __restrict__ dst,
+    uint16_t* __restrict__ kp2, uint16_t* __restrict__ vp2, const int64_t* __restrict__ dst2) {
   constexpr int LPH = D / 8;       // lanes per head
   constexpr int HALF = D / 2;
   constexpr int HPB = 256 / LPH;   // heads per pass of the workgroup
@@ -248,19 +250,22 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
   const uint16_t* xrow = qkv + (int64_t)row * qkv_ld;
   const int total = HQ + HK;
   const int64_t kv_row = (int64_t)HK * D;
-  int64_t drow = 0;
+  int64_t drow = 0, drow2 = -1;
   if (POOL) {
     drow = dst[row];
-    if (drow >= 0) {
+    drow2 = dst2 ? dst2[row] : -1;
+    if (drow >= 0 || drow2 >= 0) {
       const uint4* vs = reinterpret_cast<const uint4*>(xrow + total * D);
-      uint4* vd = reinterpret_cast<uint4*>(vp + drow * kv_row);
+      uint4* vd = drow >= 0 ? reinterpret_cast<uint4*>(vp + drow * kv_row) : nullptr;
+      uint4* vd2 = drow2 >= 0 ? reinterpret_cast<uint4*>(vp2 + drow2 * kv_row) : nullptr;
       for (int c = threadIdx.x; c < (int)(kv_row >> 3); c += 256) {
         uint4 w = vs[c];
         w.x = pack2_f16(lo_bf16(w.x), hi_bf16(w.x));
         w.y = pack2_f16(lo_bf16(w.y), hi_bf16(w.y));
         w.z = pack2_f16(lo_bf16(w.z), hi_bf16(w.z));
         w.w = pack2_f16(lo_bf16(w.w), hi_bf16(w.w));
-        vd[c] = w;
+        if (drow >= 0) vd[c] = w;
+        if (drow2 >= 0) vd2[c] = w;
       }
     }
   }
@@ -309,6 +314,12 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
       uint16_t* out = is_q    ? qo + (int64_t)row * qo_ld + h * D
                       : POOL ? kp + drow * kv_row + (h - HQ) * D
                              : ko + (int64_t)row * ko_ld + (h - HQ) * D;
+      *reinterpret_cast<uint2*>(out + j * 4) = make_uint2(pack2_bf16(oa[0], oa[1]), pack2_bf16(oa[2], oa[3]));
+      *reinterpret_cast<uint2*>(out + HALF + j * 4) =
+          make_uint2(pack2_bf16(ob[0], ob[1]), pack2_bf16(ob[2], ob[3]));
+    }
+    if (POOL && live && !is_q && drow2 >= 0) {
+      uint16_t* out = kp2 + drow2 * kv_row + (h - HQ) * D;
       *reinterpret_cast<uint2*>(out + j * 4) = make_uint2(pack2_bf16(oa[0], oa[1]), pack2_bf16(oa[2], oa[3]));
       *reinterpret_cast<uint2*>(out + HALF + j * 4) =
           make_uint2(pack2_bf16(ob[0], ob[1]), pack2_bf16(ob[2], ob[3]));
@@ -512,7 +523,8 @@ int qk_norm_rope_launch(const void* qkv, int64_t qkv_ld, void* q_out, int64_t q_
                         int64_t k_ld, const void* cos_sin, int cs_is_f32,
                         const int64_t* positions, const void* q_w, const void* k_w, int64_t n,
                         int64_t HQ, int64_t HK, int64_t D, float eps, void* k_pool, void* v_pool,
-                        const int64_t* dst, hipStream_t stream) {
+                        const int64_t* dst, void* k_pool2, void* v_pool2, const int64_t* dst2,
+                        hipStream_t stream) {
   QX_CHECK(D == 64 || D == 128, "qk_norm_rope: head_dim %lld (64 or 128)", (long long)D);
   QX_CHECK(HQ > 0 && HK > 0, "qk_norm_rope: heads");
   QX_CHECK(qkv_ld % 4 == 0 && q_ld % 4 == 0 && k_ld % 4 == 0, "qk_norm_rope: strides");
@@ -522,7 +534,8 @@ int qk_norm_rope_launch(const void* qkv, int64_t qkv_ld, void* q_out, int64_t q_
   hipLaunchKernelGGL((qk_norm_rope_kernel<DD, F32, P>), grid, block, 0, stream,                \
                      (const uint16_t*)qkv, qkv_ld, (uint16_t*)q_out, q_ld, (uint16_t*)k_out,  \
                      k_ld, cos_sin, positions, (const uint16_t*)q_w, (const uint16_t*)k_w,    \
-                     (int)n, (int)HQ, (int)HK, eps, (uint16_t*)k_pool, (uint16_t*)v_pool, dst)
+                     (int)n, (int)HQ, (int)HK, eps, (uint16_t*)k_pool, (uint16_t*)v_pool, dst, \
+                     (uint16_t*)k_pool2, (uint16_t*)v_pool2, dst2)
 #define QX_QK_D(DD, P) \
   if (cs_is_f32) QX_QK(DD, true, P); else QX_QK(DD, false, P);
   if (dst) {
@@ -544,19 +557,23 @@ int qx_qk_norm_rope(const void* qkv, int64_t qkv_ld, void* q_out, int64_t q_ld, 
            "qk_norm_rope: null pointer");
   return qk_norm_rope_launch(qkv, qkv_ld, q_out, q_ld, k_out, k_ld, cos_sin, cs_is_f32,
                              positions, q_w, k_w, n, HQ, HK, D, eps, nullptr, nullptr, nullptr,
-                             stream);
+                             nullptr, nullptr, nullptr, stream);
 }
 
 int qx_qk_norm_rope_kv(const void* qkv, int64_t qkv_ld, void* q_out, int64_t q_ld, void* k_pool,
-                       void* v_pool, const int64_t* dst, const void* cos_sin, int cs_is_f32,
+                       void* v_pool, const int64_t* dst, void* k_pool2, void* v_pool2,
+                       const int64_t* dst2, const void* cos_sin, int cs_is_f32,
                        const int64_t* positions, const void* q_w, const void* k_w, int64_t n,
                        int64_t HQ, int64_t HK, int64_t D, float eps, hipStream_t stream) {
   QX_CHECK(qkv && q_out && k_pool && v_pool && dst && cos_sin && positions && q_w && k_w,
            "qk_norm_rope_kv: null pointer");
-  QX_CHECK(qkv_ld % 8 == 0 && aligned16(qkv) && aligned16(k_pool) && aligned16(v_pool),
+  QX_CHECK(!dst2 || (k_pool2 && v_pool2), "qk_norm_rope_kv: second destination pools");
+  QX_CHECK(qkv_ld % 8 == 0 && aligned16(qkv) && aligned16(k_pool) && aligned16(v_pool) &&
+               (!dst2 || (aligned16(k_pool2) && aligned16(v_pool2))),
            "qk_norm_rope_kv: alignment");
   return qk_norm_rope_launch(qkv, qkv_ld, q_out, q_ld, nullptr, 0, cos_sin, cs_is_f32, positions,
-                             q_w, k_w, n, HQ, HK, D, eps, k_pool, v_pool, dst, stream);
+                             q_w, k_w, n, HQ, HK, D, eps, k_pool, v_pool, dst, k_pool2, v_pool2,
+                             dst2, stream);
 }
 
 int qx_silu_mul_quant(const void* gate_up, int64_t gu_ld, void* q, int64_t q_ld, float* scales,

@@ -302,12 +302,15 @@ class Engine:
                   float(attn.q_norm.variance_epsilon), _stream())
         return q, k
 
-    def qk_norm_rope_rows(self, qkv, positions, attn, identity=None):
+    def qk_norm_rope_rows(self, qkv, positions, attn, identity=None, meta=None):
         """q, k and fp16 v rows in one pass over qkv (qx_qk_norm_rope_kv
         with the identity row map; `identity` = arange(n) int64 on the
         device, made here when not given): the tree path's call A reads K
         and V of the pack's own rows contiguous, V in fp16 as the pages
-        hold it."""
+        hold it. With a tree pack's meta carrying `row_pool_dst` (pool row
+        per pack row, -1 for none), the same pass also writes the pack's KV
+        into the arena pages of meta's layer (the kv_src -> kv_dst writes,
+        attention.py:1405)."""
         n = qkv.shape[0]
         hq, hk, d = self.num_q_heads, self.num_kv_heads, self.head_dim
         if qkv.shape[1] < (hq + 2 * hk) * d:
@@ -321,10 +324,22 @@ class Engine:
         if rows.shape[0] != n or rows.dtype != torch.int64:
             raise ValueError("identity must be arange(n) int64")
         cache = self._rope_cache()
+        pools, dst2 = (None, None), None
+        if meta is not None and meta.get("row_pool_dst") is not None:
+            dst2 = meta["row_pool_dst"]
+            if dst2.shape[0] != n:
+                raise ValueError(f"row_pool_dst has {dst2.shape[0]} rows, qkv {n}")
+            pools = self.arena.layer_kv(meta["layer"])
+            if pools[1].dtype != torch.float16:
+                raise ValueError(f"V pool dtype {pools[1].dtype}: this engine keeps V pages "
+                                 f"in fp16")
         _lib.call("qx_qk_norm_rope_kv", _ptr(qkv), qkv.stride(0), _ptr(q), q.stride(0), _ptr(k),
-                  _ptr(v), _ptr(rows), _ptr(cache), int(cache.dtype == torch.float32),
+                  _ptr(v), _ptr(rows), _ptr(pools[0]), _ptr(pools[1]), _ptr(dst2), _ptr(cache),
+                  int(cache.dtype == torch.float32),
                   _ptr(positions), _ptr(attn.q_norm.weight), _ptr(attn.k_norm.weight), n, hq,
                   hk, d, float(attn.q_norm.variance_epsilon), _stream())
+        if dst2 is not None:
+            meta["kv_fresh_layer"] = meta["layer"]
         return q, k, v
 
     def qk_norm_rope_kv(self, qkv, positions, attn, meta):
@@ -347,7 +362,7 @@ class Engine:
         q = torch.empty((n, hq * d), dtype=torch.bfloat16, device=qkv.device)
         cache = self._rope_cache()
         _lib.call("qx_qk_norm_rope_kv", _ptr(qkv), qkv.stride(0), _ptr(q), q.stride(0),
-                  _ptr(k_pool), _ptr(v_pool), _ptr(dst), _ptr(cache),
+                  _ptr(k_pool), _ptr(v_pool), _ptr(dst), None, None, None, _ptr(cache),
                   int(cache.dtype == torch.float32), _ptr(positions), _ptr(attn.q_norm.weight),
                   _ptr(attn.k_norm.weight), n, hq, hk, d, float(attn.q_norm.variance_epsilon),
                   _stream())
@@ -430,7 +445,8 @@ class Engine:
         hq, hk, d = self.num_q_heads, self.num_kv_heads, self.head_dim
         layer = meta["layer"]
         dev = q3.device
-        if meta.get("kv_src") is not None and meta["kv_src"].numel():
+        written = meta.pop("kv_fresh_layer", None) == layer   # by qk_norm_rope_rows
+        if meta.get("kv_src") is not None and meta["kv_src"].numel() and not written:
             self.kv_row_scatter(k3, v3, meta["kv_src"], meta["kv_dst"], layer)
         # call A reads the pack's own K and V rows: contiguous, V in fp16 as
         # the pages hold it (as qk_norm_rope_rows gives them, else one

@@ -101,7 +101,7 @@ class Qwen3Pipeline:
             if identity is None or identity.shape[0] != qkv.shape[0]:
                 identity = torch.arange(qkv.shape[0], dtype=torch.int64, device=qkv.device)
                 chunk.meta["identity_rows"] = identity
-            return engine.qk_norm_rope_rows(qkv, positions, attn, identity)
+            return engine.qk_norm_rope_rows(qkv, positions, attn, identity, chunk.meta)
         q, k = engine.qk_norm_rope(qkv, positions, attn)
         v = qkv[:, (engine.num_q_heads + engine.num_kv_heads) * engine.head_dim:]
         return q, k, v
