@@ -370,6 +370,39 @@ def test_qk_norm_rope_kv_equals_norm_rope_then_scatter(hq, hk, d, cache_dtype):
     assert int((pools[1][0].view(pool_rows, -1) != 7.0).all(1).sum()) == n - 3
 
 
+def test_qk_norm_rope_rows_with_pages_equals_norm_rope_then_scatters():
+    """The tree path's pass: q, contiguous K and fp16 V rows, and the same
+    K/V into pool rows row_pool_dst[i] (none when negative), bit for bit as
+    qk_norm_rope, then the identity and the page scatters."""
+    hq, hk, d, n, pool_rows = 32, 8, 128, 70, 256
+    g = _gen(31)
+    qkv = (torch.randn(n, (hq + 2 * hk) * d, generator=g) * 3).to(torch.bfloat16).to(DEV)
+    pos = torch.randint(0, 4000, (n,), generator=g).to(DEV)
+    cache = ref.rope_cache(d, 4096, 1e6).to(torch.bfloat16).to(DEV)
+    attn = type("A", (), {})()
+    attn.q_norm = type("N", (), {"weight": (1 + 0.1 * torch.randn(d, generator=g)).to(
+        torch.bfloat16).to(DEV), "variance_epsilon": 1e-6})()
+    attn.k_norm = type("N", (), {"weight": (1 + 0.1 * torch.randn(d, generator=g)).to(
+        torch.bfloat16).to(DEV), "variance_epsilon": 1e-6})()
+    dst = torch.randperm(pool_rows, generator=g)[:n].to(DEV)
+    dst[::3] = -1
+    pools = [(torch.zeros(pool_rows, hk, d, dtype=torch.bfloat16, device=DEV),
+              torch.zeros(pool_rows, hk, d, dtype=torch.float16, device=DEV)) for _ in range(2)]
+    sep = _engine(hq, hk, d, arena=_Arena(*pools[0], 16), cache=cache)
+    q_ref, k_ref = sep.qk_norm_rope(qkv, pos, attn)
+    v_ref = qkv[:, (hq + hk) * d:].float().half()
+    keep = dst >= 0
+    sep.kv_row_scatter(k_ref, qkv[:, (hq + hk) * d:], torch.arange(n, device=DEV)[keep],
+                       dst[keep], 0)
+    fused = _engine(hq, hk, d, arena=_Arena(*pools[1], 16), cache=cache)
+    meta = {"layer": 0, "row_pool_dst": dst}
+    q, k, v = fused.qk_norm_rope_rows(qkv, pos, attn, meta=meta)
+    torch.cuda.synchronize()
+    assert meta["kv_fresh_layer"] == 0
+    assert torch.equal(q, q_ref) and torch.equal(k, k_ref) and torch.equal(v, v_ref)
+    assert torch.equal(pools[1][0], pools[0][0]) and torch.equal(pools[1][1], pools[0][1])
+
+
 # ---- KV scatter and paged attention ---------------------------------------------------
 
 class _Arena:
