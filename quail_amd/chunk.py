@@ -419,6 +419,9 @@ def _pack_tree(arena, groups, *, timing=None, attention_heads=None):
             max_used=int(np.diff(ncu_k).max()), causal=False,
             # each node row's index among call B's rows
             b_index=reads["source"][q_rows].astype(np.int64))
+        # where call C's gathered K/V rows land: 0..len(key_rows)-1
+        reads["nodes"]["gather_rows"] = np.arange(len(reads["nodes"]["key_rows"]),
+                                                  dtype=np.int64)
         reads["nodes"]["max_k"] = reads["nodes"]["max_used"]
     kv_src = kv_dst = None
     if kv_writes:
@@ -603,7 +606,8 @@ def _upload_tree(chunk: Chunk, staging: InputStaging) -> Chunk:
                 cu_q=staging.copy("node_cu_q", nodes["cu_q"], torch.int32),
                 cu_k=staging.copy("node_cu_k", nodes["cu_k"], torch.int32),
                 used=staging.copy("node_used", nodes["used"], torch.int32),
-                b_index=staging.copy("node_b_index", nodes["b_index"], torch.int64))
+                b_index=staging.copy("node_b_index", nodes["b_index"], torch.int64),
+                gather_rows=staging.copy("node_gather_rows", nodes["gather_rows"], torch.int64))
             if nodes.get("work") is not None and nodes["n_work"]:
                 dev["nodes"]["work"] = staging.copy("node_work", nodes["work"], torch.int32)
         meta["reads"] = dev

@@ -509,7 +509,9 @@ class Engine:
         row = hk * d
         k_c = torch.empty((nk, row), dtype=torch.bfloat16, device=dev)
         v_c = torch.empty((nk, row), dtype=torch.float16, device=dev)
-        into = torch.arange(nk, dtype=torch.int64, device=dev)
+        into = nodes.get("gather_rows")
+        if not torch.is_tensor(into):
+            into = torch.arange(nk, dtype=torch.int64, device=dev)
         _lib.call("qx_kv_scatter", _ptr(k_rows), k_rows.stride(0), _ptr(v_rows), v_rows.stride(0),
                   _ptr(k_c), _ptr(v_c), _ptr(nodes["key_rows"]), _ptr(into), nk, row, 0,
                   _stream())
