@@ -59,20 +59,35 @@ def gemm_config(n: int, k: int, m: int) -> int:
         return int(forced)
     if n % 256:
         return GEMM_ODD_WIDTH_CONFIG
-    tiles = -(-m // 256) * (n // 256)
-    if tiles >= CUS and tiles % CUS in (0,) + tuple(range(CUS - CUS // 8, CUS)) and \
-            (k // 128) % 2 == 0:
+    if _whole_waves(n, k, m):
         return GEMM_WHOLE_WAVES_CONFIG
     return GEMM_DEFAULT_CONFIG
 
 
-def swiglu_config() -> int:
-    """Tile schedule of the gate_up GEMM with the SiLU-quant epilogue: 10
-    (one workgroup per tile) or 22 (persistent, the K pipeline running
-    across tiles), as for qx_gemm_fp8_blockscaled."""
-    forced = os.environ.get(GEMM_CONFIG_ENV)
-    if forced is not None and int(forced) in (10, 22):
-        return int(forced)
+def _whole_waves(n: int, k: int, m: int) -> bool:
+    """256 x 256 tiles fill whole waves of the CUs (the last at least 7/8
+    full) and K has an even number of 128-blocks (config 22's pipeline)."""
+    tiles = -(-m // 256) * (n // 256)
+    return (tiles >= CUS and tiles % CUS in (0,) + tuple(range(CUS - CUS // 8, CUS))
+            and (k // 128) % 2 == 0)
+
+
+SWIGLU_CONFIG_ENV = "QUAIL_SWIGLU_CONFIG"
+
+
+def swiglu_config(n: int = 0, k: int = 0, m: int = 0) -> int:
+    """Tile schedule of the gate_up GEMM with the SiLU-quant epilogue (n =
+    gate_up rows, 256 per tile): 10 (one workgroup per tile) or 22
+    (persistent, the K pipeline running across tiles), chosen as for
+    qx_gemm_fp8_blockscaled (22 where the tiles fill whole waves: the
+    gate_up of a full pack, +1% against 10 in the pass). QUAIL_SWIGLU_CONFIG
+    forces it alone, QUAIL_GEMM_CONFIG with every GEMM."""
+    for env in (SWIGLU_CONFIG_ENV, GEMM_CONFIG_ENV):
+        forced = os.environ.get(env)
+        if forced is not None and int(forced) in (10, 22):
+            return int(forced)
+    if n % 256 == 0 and _whole_waves(n, k, m):
+        return GEMM_WHOLE_WAVES_CONFIG
     return SWIGLU_DEFAULT_CONFIG
 
 
@@ -182,7 +197,7 @@ class Engine:
             start.record()
         _lib.call("qx_gemm_fp8_swiglu_quant", _ptr(q_input), _ptr(input_scale), _ptr(w),
                   _ptr(sw), _ptr(q), q.stride(0), _ptr(scales), self._scale_ld(scales), m, half,
-                  k, q_input.stride(0), self._scale_ld(input_scale), swiglu_config(),
+                  k, q_input.stride(0), self._scale_ld(input_scale), swiglu_config(n, k, m),
                   _stream())
         if timer is not None:
             end.record()

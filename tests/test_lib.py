@@ -70,3 +70,14 @@ def test_gemm_config_choice_by_shape(monkeypatch):
     assert gemm_config(2688, 2560, 16294) == 5
     monkeypatch.setenv(GEMM_CONFIG_ENV, "14")
     assert gemm_config(6144, 2560, 16294) == 14
+
+
+def test_swiglu_config_choice_by_shape(monkeypatch):
+    from quail_amd.engine import GEMM_CONFIG_ENV, SWIGLU_CONFIG_ENV, swiglu_config
+    monkeypatch.delenv(GEMM_CONFIG_ENV, raising=False)
+    monkeypatch.delenv(SWIGLU_CONFIG_ENV, raising=False)
+    assert swiglu_config(19456, 2560, 16294) == 22   # 64 x 76 tiles: 19 waves
+    assert swiglu_config(19456, 2560, 9000) == 10    # 36 x 76 = 2736 tiles
+    assert swiglu_config(19456, 2688, 16294) == 10   # 21 K-blocks
+    monkeypatch.setenv(SWIGLU_CONFIG_ENV, "10")
+    assert swiglu_config(19456, 2560, 16294) == 10
