@@ -65,6 +65,8 @@ def parse():
                    help="size of the counter-calibration copy (0: none)")
     p.add_argument("--summarize", default=None,
                    help="summarize a rocprofv3 CSV directory and exit")
+    p.add_argument("--gemm-alone-reps", type=int, default=20,
+                   help="launches per shape of the GEMM-alone record (0 skips it)")
     return p.parse_args()
 
 
@@ -156,6 +158,57 @@ def cpu_baseline(model, workload, target_s):
                         f"documents per prompt token of the corpus"))
 
 
+GEMM_ALONE_M = 8192
+# (K, N) of the four Qwen3-4B projections: qkv, o_proj, gate_up, down
+GEMM_ALONE_SHAPES = ((2560, 6144), (4096, 2560), (2560, 19456), (9728, 2560))
+
+
+def gemm_alone(reps: int = 20, seed: int = 0):
+    """The FP8 block-scaled GEMM alone at the Qwen3-4B projection shapes,
+    M = 8192 tokens: activations bf16 N(0, 1) quantized per token per 128
+    columns (qx_group_quant), weights N(0, 0.02) quantized per 128 x 128
+    block, bf16 output; each shape timed over `reps` launches with HIP events
+    on the launch stream after 3 untimed ones. Returns the sub-record."""
+    import torch
+
+    from quail_amd.engine import Engine, gemm_config
+    from quail_amd.model import quantize_blocks
+
+    eng = Engine(None, num_q_heads=1, num_kv_heads=1, head_dim=128, rotary=None)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    shapes = {}
+    m = GEMM_ALONE_M
+    for k, n in GEMM_ALONE_SHAPES:
+        x = torch.randn(m, k, generator=g, device="cuda").to(torch.bfloat16)
+        q, s = eng.quant(x)
+        w, sw = quantize_blocks(torch.randn(n, k, generator=g, device="cuda") * 0.02)
+        lin = type("Linear", (), {})()
+        lin.weight, lin.weight_scale_inv = w, sw
+        out = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
+        for _ in range(3):
+            eng.gemm(q, s, lin, out=out)
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(reps):
+            eng.gemm(q, s, lin, out=out)
+        end.record()
+        torch.cuda.synchronize()
+        us = start.elapsed_time(end) * 1e3 / reps
+        tflops = 2.0 * m * n * k / (us * 1e-6) / 1e12
+        shapes[f"{k}x{n}"] = dict(us=round(us, 2), tflops=round(tflops, 1),
+                                  frac=round(tflops * 1e12 / PEAK_FP8, 4),
+                                  config=gemm_config(n, k, m))
+        del x, q, s, w, sw, out
+    total_flops = sum(2.0 * m * n * k for k, n in GEMM_ALONE_SHAPES)
+    total_us = sum(v["us"] for v in shapes.values())
+    return dict(workload=f"FP8 block-scaled GEMM alone, Qwen3-4B projection shapes (K x N), "
+                         f"M = {m} tokens, bf16 output",
+                m=m, reps=reps, shapes=shapes,
+                tflops_all=round(total_flops / (total_us * 1e-6) / 1e12, 1),
+                frac_all=round(total_flops / (total_us * 1e-6) / PEAK_FP8, 4))
+
+
 def _short(name: str) -> str:
     """A kernel name without its parameter list, at most 110 characters."""
     name = name.strip('"').replace("(anonymous namespace)::", "")
@@ -202,8 +255,16 @@ def summarize(directory: str, copy_mib: int) -> None:
                   f"avg {gemm_ns / gemm_calls / 1e3:.2f} us")
     for path in counters:
         per = defaultdict(lambda: defaultdict(list))
+        dispatch = defaultdict(dict)     # (kernel, dispatch id) -> counter values
         for r in csv.DictReader(open(path)):
-            per[r["Counter_Name"]][_short(r["Kernel_Name"])].append(float(r["Counter_Value"]))
+            kernel = _short(r["Kernel_Name"])
+            per[r["Counter_Name"]][kernel].append(float(r["Counter_Value"]))
+            d = dispatch[(kernel, r["Dispatch_Id"])]
+            d[r["Counter_Name"]] = float(r["Counter_Value"])
+            d["_ns"] = float(r["End_Timestamp"]) - float(r["Start_Timestamp"])
+        if "MfmaUtil" in per or "SQ_INSTS_MFMA" in per:
+            summarize_mfma(dispatch)
+            continue
         for counter, kernels in per.items():
             print(f"\n{counter} (KiB per dispatch)")
             print(f"{'calls':>7} {'mean KiB':>14}  kernel")
@@ -218,6 +279,37 @@ def summarize(directory: str, copy_mib: int) -> None:
                 print(f"copy calibration: {copy_mib} MiB moved, counter reads "
                       f"{copy[0][-1] * 1024 / 2**20:.1f} MiB, factor {factor:.4f}")
                 print(f"{counter}_bytes_per_gemm_launch = {mean:.0f}")
+
+
+def summarize_mfma(dispatch) -> None:
+    """Per-kernel means of an MFMA/VALU/LDS counter pass: MfmaUtil and
+    VALUBusy are rocprofv3's own derived metrics (counter_defs.yaml:
+    SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE * SIMDs) and
+    SQ_ACTIVE_INST_VALU / (CUs * GRBM_GUI_ACTIVE), in %); FP8 TFLOP/s is
+    SQ_INSTS_VALU_MFMA_MOPS_F8 * 512 FLOP over the dispatch's duration under
+    the profiler; VALU/MFMA is SQ_INSTS_VALU (which counts the MFMAs too)
+    per SQ_INSTS_MFMA."""
+    from collections import defaultdict
+
+    groups = defaultdict(list)
+    for (kernel, _), d in dispatch.items():
+        groups[kernel].append(d)
+    cols = ("MfmaUtil", "VALUBusy", "SQ_INSTS_MFMA", "SQ_INSTS_VALU", "SQ_INSTS_LDS",
+            "SQ_LDS_BANK_CONFLICT", "SQ_INSTS_VALU_MFMA_MOPS_F8",
+            "SQ_INSTS_VALU_MFMA_MOPS_BF16", "SQ_INSTS_VALU_MFMA_MOPS_F16")
+    print(f"{'calls':>6} {'avg us':>9} {'MFMA%':>6} {'VALU%':>6} {'VALU/MFMA':>9} "
+          f"{'LDS inst':>10} {'LDS confl':>10} {'TFLOP/s':>8}  kernel")
+    for kernel, ds in sorted(groups.items(), key=lambda kv: -sum(d["_ns"] for d in kv[1])):
+        mean = {c: sum(d.get(c, 0.0) for d in ds) / len(ds) for c in cols + ("_ns",)}
+        ns = mean["_ns"]
+        mops = (mean["SQ_INSTS_VALU_MFMA_MOPS_F8"] + mean["SQ_INSTS_VALU_MFMA_MOPS_BF16"] +
+                mean["SQ_INSTS_VALU_MFMA_MOPS_F16"])
+        tflops = mops * 512 / (ns * 1e-9) / 1e12 if ns else 0.0
+        ratio = (mean["SQ_INSTS_VALU"] / mean["SQ_INSTS_MFMA"]
+                 if mean["SQ_INSTS_MFMA"] else float("nan"))
+        print(f"{len(ds):6d} {ns / 1e3:9.2f} {mean['MfmaUtil']:6.1f} {mean['VALUBusy']:6.1f} "
+              f"{ratio:9.2f} {mean['SQ_INSTS_LDS']:10.3g} {mean['SQ_LDS_BANK_CONFLICT']:10.3g} "
+              f"{tflops:8.1f}  {kernel}")
 
 
 def load_traffic():
@@ -393,6 +485,10 @@ def main():
     e2e_frac = t_roof / (elapsed / args.steps)
 
     log(f"timed {args.steps} steps: {elapsed:.3f} s")
+    alone = None
+    if args.gemm_alone_reps > 0:
+        alone = gemm_alone(args.gemm_alone_reps, args.seed)
+        log(f"gemm alone: {alone['shapes']}")
     cpu = None
     if args.cpu_seconds > 0:
         cpu = cpu_baseline(model, wl, args.cpu_seconds)
@@ -439,6 +535,7 @@ def main():
             "per_shape_tflops": {s: round(v[0] / (v[1] * 1e-3) / 1e12, 1)
                                  for s, v in per_shape.items()},
         },
+        "gemm_alone": alone,
         "cpu_baseline": cpu,
         "setup_s": round(t_build, 1),
     }
