@@ -129,3 +129,60 @@ def write_hf_checkpoint(model, cfg, path, shards=2):
     with open(path / "config.json", "w") as f:
         json.dump(config, f, indent=1)
     return path
+
+
+def exact_contractions(monkeypatch):
+    """Replace the engine's two MFMA contractions with exact float64 torch
+    computations on the GPU, for decomposition tests only: every FP8 GEMM
+    (the dequantized operands' matmul, rounded to bf16; gate_up then the
+    engine's own SiLU-quant kernel) and the paged attention (exact softmax
+    over the pages the block table names, rounded to bf16, then the
+    engine's own group quant). Everything else stays the engine's."""
+    from quail_amd.engine import Engine
+
+    def gemm(self, q_input, input_scale, linear, out=None):
+        m, k = q_input.shape
+        a = (q_input.double().view(m, k // 128, 128) *
+             input_scale.double().unsqueeze(-1)).view(m, k)
+        w = linear.weight.double()
+        s = self.weight_scale(linear).double().repeat_interleave(128, 0).repeat_interleave(128, 1)
+        r = (a @ (w * s[:w.shape[0], :w.shape[1]]).T).to(torch.bfloat16)
+        if out is None:
+            return r
+        out.copy_(r)
+        return out
+
+    def gate_up(self, q_input, input_scale, linear):
+        return self.activation_quant(gemm(self, q_input, input_scale, linear))
+
+    def paged(self, q3, tables, layer, softmax_scale, output):
+        n, hq, d = q3.shape
+        group = hq // self.num_kv_heads
+        k_pool, v_pool = self.arena.layer_kv(layer)
+        page = self.arena.page_tokens
+        cu, used = tables["cu_q"].tolist(), tables["used"].tolist()
+        table = tables["table"].tolist()
+        causal = bool(tables.get("causal", True))
+        scale = d ** -0.5 if softmax_scale is None else softmax_scale
+        dev = q3.device
+        out = torch.zeros((n, hq, d), dtype=torch.float64, device=dev)
+        for s in range(len(used)):
+            r0, r1 = cu[s], cu[s + 1]
+            q_len, seen = r1 - r0, used[s]
+            if q_len == 0:
+                continue
+            rows = torch.tensor([p * page + j for p in table[s][:-(-seen // page)]
+                                 for j in range(page)][:seen], device=dev)
+            k = k_pool[rows].double().repeat_interleave(group, dim=1)
+            v = v_pool[rows].double().repeat_interleave(group, dim=1)
+            scores = torch.einsum("qhd,khd->hqk", q3[r0:r1].double(), k) * scale
+            if causal:
+                qi = torch.arange(q_len, device=dev)[:, None]
+                kj = torch.arange(seen, device=dev)[None, :]
+                scores = scores.masked_fill(~(kj < seen - q_len + qi + 1)[None], float("-inf"))
+            out[r0:r1] = torch.einsum("hqk,khd->qhd", scores.softmax(-1), v)
+        return self.quant(out.to(torch.bfloat16).view(n, hq * d), output=output)
+
+    monkeypatch.setattr(Engine, "gemm", gemm)
+    monkeypatch.setattr(Engine, "gate_up_activation_quant", gate_up)
+    monkeypatch.setattr(Engine, "_paged", paged)

@@ -2,22 +2,31 @@
 
 The tiny Qwen3 configuration (2 layers, hidden 256, 4/2 heads, D 64,
 random-init, 16 documents behind a 32-token shared prefix, one 2048-row
-pack) against the oracle's dequantized path (float64 contractions). The
-oracle runs each document's prompt whole (no pages, no borrowing), so a
-wrong page table, scatter map, position or borrowed prefix shows up here.
+pack) against the oracle (oracle/qwen3_ref.py, itself pinned against torch
+and transformers in tests/test_oracle_pins.py). The oracle runs each
+document's prompt whole (no pages, no borrowing), so a wrong page table,
+scatter map, position or borrowed prefix shows up here.
 
-Tolerances. FP8 activation quantization makes this network amplify any
-arithmetic difference: one e4m3 code flip moves a value by 1/16, and flips
-seed more flips layer by layer, up to the FP8 noise floor. gfx950's FP8
-MFMA rounds inside its 64-term dot product (measured: median relative
-error 8e-6 against the exact sum, ~1% of bf16 GEMM outputs one ulp off),
-so the GPU cannot track the exact path bit for bit. Measured over 512
-documents (32 seeds): 99.0% of yes-minus-no margins within 0.05 of the
-oracle, max 0.065, rms 0.020; the oracle itself in float32 instead of
-float64 sits at 100% / 0.046 / 0.010. Decisions agree on every document
-whose oracle margin is outside +-0.05 (98.2% of all documents; the oracle's
-float32 self-agreement is 99.4%). The asserts below hold those measured
-bounds with a margin for seed variation.
+Two oracle precisions. The reference's torch dequantized path computes its
+matmuls and attention in float32 (the torch path on the CPU); the oracle
+in float64 is the exact value of the same arithmetic. The float64 oracle is
+the checker here.
+
+Why the bar is not asserted per document over many random seeds: FP8
+activation quantization makes this network amplify any rounding
+difference (one e4m3 code flip moves a value by 1/16, and flips seed more
+flips), and random-init margins crowd zero (1% of them within 0.006).
+Measured over 512 documents per norm init (32 seeds): the float32 torch
+path itself agrees with the exact float64 value on 98.8-99.0% of decisions
+(max |d| 0.05, rms 0.011-0.012). This engine against float64: 98.0-98.6%
+within 0.05, max 0.064, rms 0.021, 97.7-98.6% of decisions, every decision
+whose exact margin is outside +-0.05. The two sources are gfx950's FP8 MFMA,
+which rounds inside its dot product (mean relative error 9e-5 against the
+exact block sum; bf16 MFMA on the same operands 6e-7), and the attention's
+fp16 P; with both contractions replaced by exact ones (everything else the
+engine's own kernels) the pass reaches 100% within 0.05 and 99.8% of
+decisions, and either one left in alone already reaches rms ~0.02.
+test_exact_contractions_meet_the_bar_on_every_document asserts that strictly.
 """
 
 import numpy as np
@@ -27,40 +36,49 @@ import torch
 from oracle import qwen3_ref as ref
 from quail_amd.model import CONFIGS, build_synthetic
 from quail_amd.workload import make_workload
-from tests.helpers import ref_model, run_stage
+from tests.helpers import exact_contractions, ref_model, run_stage
 
 pytestmark = pytest.mark.gpu
 
 TOL = 0.05
 
 
-def _margins(model, wl):
-    results, run = run_stage(model, wl, "margins")
+def _margins(model, wl, **kwargs):
+    results, run = run_stage(model, wl, "margins", **kwargs)
     ym = np.array([r[0] - r[1] for r in results], dtype=np.float64)
     return ym, run
 
 
-def _oracle_margins(model, wl):
+def _oracle_margins(model, wl, precision=torch.float64):
     m = ref_model(model)
-    normed = ref.forward_documents(m, wl.prompts)
-    rows = m.head[list(wl.label_ids[:2])]
-    yes, no, bits, _ = ref.answer(normed, rows, [1, 0], mode=0)
+    ref.set_precision(precision)
+    try:
+        normed = ref.forward_documents(m, wl.prompts)
+        rows = m.head[list(wl.label_ids[:2])]
+        yes, no, bits, _ = ref.answer(normed, rows, [1, 0], mode=0)
+    finally:
+        ref.set_precision(torch.float64)
     return (yes - no).double().numpy(), normed
 
 
-def _check(got, want, within=0.98, max_abs=0.1):
+def _report(name, got, want):
     d = np.abs(got - want)
-    print(f"margins: n={len(d)} within {TOL}: {np.mean(d <= TOL):.4f} max {d.max():.4f} "
-          f"rms {np.sqrt(np.mean(d ** 2)):.4f} agree {np.mean((got > 0) == (want > 0)):.4f}")
-    assert np.mean(d <= TOL) >= within
-    assert d.max() <= max_abs
-    # decisions agree wherever the oracle's margin is outside the tolerance band
-    clear = np.abs(want) > TOL
-    assert np.all((got[clear] > 0) == (want[clear] > 0))
+    agree = np.mean((got > 0) == (want > 0))
+    print(f"{name}: n={len(d)} within {TOL}: {np.mean(d <= TOL):.4f} max {d.max():.4f} "
+          f"rms {np.sqrt(np.mean(d ** 2)):.4f} decisions agree {agree:.4f}")
+    return d, agree
 
 
 @pytest.mark.parametrize("norm_init", ["ones", "random"])
-def test_tiny_ai_if_margin_within_tolerance(norm_init):
+def test_config1_margins(norm_init):
+    """Config 1 (seed 0, one 2048-row pack, 15 documents borrowing the
+    32-token prefix) against the float64 oracle: at most 0.06 from it, at
+    most one document past 0.05 (measured: random norm weights max 0.045,
+    all 16 within; norm weights 1 max 0.051, one at 0.051), and the same
+    decision on every document whose exact margin is outside +-0.05 (the
+    one that differs has |margin| 0.007). A one-ulp change of the bf16
+    rotary cache alone moves the exact oracle's margins by up to 0.023 here,
+    so a per-document 0.05 bound sits on the noise floor (module doc)."""
     cfg = CONFIGS["tiny"]
     wl = make_workload("tiny", seed=0)
     model = build_synthetic(cfg, seed=0, device="cuda", gen_device="cpu", norm_init=norm_init)
@@ -68,25 +86,67 @@ def test_tiny_ai_if_margin_within_tolerance(norm_init):
     want, _ = _oracle_margins(model, wl)
     assert run.stats["chunks"] == 1
     assert run.stats["borrowed_tokens"] == 15 * 32      # 2 pages by 15 documents
-    _check(got, want, within=15 / 16)
+    d, agree = _report(f"config 1 ({norm_init} norms) vs float64", got, want)
+    assert d.max() <= 0.06
+    assert np.sum(d > TOL) <= 1
+    clear = np.abs(want) > TOL
+    assert np.all((got[clear] > 0) == (want[clear] > 0))
 
 
-def test_tiny_decisions_over_many_seeds():
-    """8 seeds x 16 documents."""
+@pytest.mark.parametrize("norm_init", ["ones", "random"])
+def test_tiny_margins_against_exact_math(norm_init):
+    """8 seeds x 16 documents against the float64 oracle, at the bounds the
+    FP8 noise floor allows (module docstring; measured within 0.969 / 0.984,
+    max 0.054 / 0.062, rms 0.021, decisions 0.984): no margin further than
+    0.075, rms at most 0.025, >= 96% within 0.05, every decision whose exact
+    margin is outside +-0.05 the same, >= 97.5% of all decisions."""
     cfg = CONFIGS["tiny"]
     got_all, want_all = [], []
     for seed in range(8):
         wl = make_workload("tiny", seed=seed)
         model = build_synthetic(cfg, seed=seed, device="cuda", gen_device="cpu",
-                                norm_init="random")
+                                norm_init=norm_init)
         got, _ = _margins(model, wl)
         want, _ = _oracle_margins(model, wl)
         got_all.append(got)
         want_all.append(want)
     got = np.concatenate(got_all)
     want = np.concatenate(want_all)
-    _check(got, want, within=0.97)
-    assert np.mean((got > 0) == (want > 0)) >= 0.95
+    d, agree = _report(f"8 seeds ({norm_init} norms) vs float64", got, want)
+    assert d.max() <= 0.075
+    assert np.sqrt(np.mean(d ** 2)) <= 0.025
+    assert np.mean(d <= TOL) >= 0.96
+    clear = np.abs(want) > TOL
+    assert np.all((got[clear] > 0) == (want[clear] > 0))
+    assert agree >= 0.975
+
+
+@pytest.mark.parametrize("norm_init", ["ones", "random"])
+def test_exact_contractions_meet_the_bar_on_every_document(monkeypatch, norm_init):
+    """Decomposition: the engine with its two MFMA contractions (the FP8
+    GEMMs and the paged attention) replaced by exact float64 ones on the GPU
+    and everything else its own (packing, pages, embedding, every norm and
+    quantization kernel, qk-norm-rope with the KV page writes, the final
+    norm and the answer head) meets the north-star bar against the float64
+    oracle on every one of 8 seeds x 16 documents: all margins within 0.05
+    and >= 99.5% of decisions (measured 100%, max 0.043). What separates
+    the engine from it is the MFMAs' rounding alone."""
+    exact_contractions(monkeypatch)
+    cfg = CONFIGS["tiny"]
+    got_all, want_all = [], []
+    for seed in range(8):
+        wl = make_workload("tiny", seed=seed)
+        model = build_synthetic(cfg, seed=seed, device="cuda", gen_device="cpu",
+                                norm_init=norm_init)
+        got, _ = _margins(model, wl)
+        want, _ = _oracle_margins(model, wl)
+        got_all.append(got)
+        want_all.append(want)
+    got = np.concatenate(got_all)
+    want = np.concatenate(want_all)
+    d, agree = _report(f"exact contractions ({norm_init} norms)", got, want)
+    assert np.all(d <= TOL)
+    assert agree >= 0.995
 
 
 def test_tiny_if_score_and_classify_readouts():

@@ -503,6 +503,15 @@ def test_answer_head_modes():
         else:
             torch.testing.assert_close(logits.cpu(), want, rtol=1e-4, atol=1e-4)
         yes, no, b, sc = ref.answer(normed, rows, cls.tolist(), mode)
-        agree = (bits.cpu() == b).float().mean().item()
-        assert agree >= 0.97
-        torch.testing.assert_close(score.cpu(), sc, rtol=1e-2, atol=1e-2)
+        gy, gn = yn[:, 0].cpu(), yn[:, 1].cpu()
+        # the bits are the kernel's own yes > no, and its logits are the
+        # oracle's to one bf16 ulp (mode 0) or 1e-4 (mode 1): the decisions
+        # agree wherever the oracle's yes-no gap is wider than twice that
+        assert torch.equal(bits.cpu(), (gy > gn).to(torch.uint8))
+        big = torch.maximum(yes.abs(), no.abs())
+        slack = 2 * big * 2 ** -7 if mode == 0 else torch.full_like(big, 2e-4)
+        clear = (yes - no).abs() > slack
+        assert clear.float().mean() >= 0.9
+        assert torch.equal(bits.cpu()[clear], b[clear])
+        # sigmoid' <= 1/4: one bf16 ulp of a ~1 logit moves the score < 2e-3
+        torch.testing.assert_close(score.cpu(), sc, rtol=0, atol=4e-3 if mode == 0 else 1e-4)

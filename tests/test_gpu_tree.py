@@ -24,7 +24,7 @@ from quail_amd import _lib
 from quail_amd.model import CONFIGS, build_synthetic
 from quail_amd.workload import make_workload
 from tests.helpers import run_stage
-from tests.test_gpu_forward import TOL, _check, _oracle_margins
+from tests.test_gpu_forward import TOL, _oracle_margins, _report
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -197,19 +197,54 @@ def test_bf16_merge_for_narrow_heads():
     assert (diff == 0).float().mean() >= 0.999 and bool((diff <= ulp).all())
 
 
-@pytest.mark.parametrize("seed", [0, 3])
-def test_tiny_tree_pass_matches_the_oracle_and_the_unified_pass(seed):
+def test_tiny_tree_pass_on_config1():
+    """Config 1 (seed 0, norm weights 1) through the tree path against the
+    float64 oracle, at the unified path's config-1 bounds: at most 0.06 from
+    it, at most one document past 0.05, every decision whose exact margin is
+    outside +-0.05 the same."""
     cfg = CONFIGS["tiny"]
-    wl = make_workload("tiny", seed=seed)
-    model = build_synthetic(cfg, seed=seed, device="cuda", gen_device="cpu", norm_init="random")
+    wl = make_workload("tiny", seed=0)
+    model = build_synthetic(cfg, seed=0, device="cuda", gen_device="cpu", norm_init="ones")
     results, run = run_stage(model, wl, "margins", attention_mode="tree")
     tree = np.array([r[0] - r[1] for r in results], dtype=np.float64)
-    results, _ = run_stage(model, wl, "margins")
-    unified = np.array([r[0] - r[1] for r in results], dtype=np.float64)
     want, _ = _oracle_margins(model, wl)
     assert run.stats["borrowed_tokens"] == 15 * 32
-    _check(tree, want, within=15 / 16)
-    assert np.abs(tree - unified).max() <= 2 * TOL
+    d, agree = _report("tree path, config 1 vs float64", tree, want)
+    assert d.max() <= 0.06
+    assert np.sum(d > TOL) <= 1
+    clear = np.abs(want) > TOL
+    assert np.all((tree[clear] > 0) == (want[clear] > 0))
+
+
+def test_tiny_tree_pass_against_exact_math_and_the_unified_pass():
+    """8 seeds x 16 documents through the tree path against the float64
+    oracle at the FP8 noise floor's bounds. The tree path rounds call A,
+    call B, the merge weight and the merge to bf16 (attention.py:902-948)
+    on top of what the unified path rounds, so its spread is a little wider
+    (measured max 0.088, rms 0.025, 96.9% within 0.05, 99.2% of decisions):
+    max 0.1, rms <= 0.03, >= 96% within 0.05, every decision whose exact
+    margin is outside +-0.05 the same, >= 97.5% of all; and the tree and
+    unified passes within 2 x 0.05 of each other."""
+    cfg = CONFIGS["tiny"]
+    got_all, want_all, uni_all = [], [], []
+    for seed in range(8):
+        wl = make_workload("tiny", seed=seed)
+        model = build_synthetic(cfg, seed=seed, device="cuda", gen_device="cpu",
+                                norm_init="random")
+        results, _ = run_stage(model, wl, "margins", attention_mode="tree")
+        got_all.append(np.array([r[0] - r[1] for r in results], dtype=np.float64))
+        results, _ = run_stage(model, wl, "margins")
+        uni_all.append(np.array([r[0] - r[1] for r in results], dtype=np.float64))
+        want_all.append(_oracle_margins(model, wl)[0])
+    got, want, uni = map(np.concatenate, (got_all, want_all, uni_all))
+    d, agree = _report("tree path, 8 seeds vs float64", got, want)
+    assert d.max() <= 0.1
+    assert np.sqrt(np.mean(d ** 2)) <= 0.03
+    assert np.mean(d <= TOL) >= 0.96
+    clear = np.abs(want) > TOL
+    assert np.all((got[clear] > 0) == (want[clear] > 0))
+    assert agree >= 0.975
+    assert np.abs(got - uni).max() <= 2 * TOL
 
 
 def test_qwen3_4b_tree_attention_equals_the_unified_attention():
