@@ -124,6 +124,24 @@ class KVArena:
             self.evicted_prefix_tokens += tokens
             self.evicted_pages += acct.free_key(key)
 
+    def evict_retained(self, pages_needed: int) -> tuple:
+        """Free retained keys nothing holds, oldest-priority first, until
+        pages_needed pages have come free (arena.py:468-492). Returns the
+        evicted keys."""
+        acct = self.accounting
+        start = acct.free_pages
+        keys = []
+        while acct.free_pages - start < pages_needed:
+            victim = acct.pop_retained_victim(keep=frozenset(self._holds))
+            if victim is None:
+                break
+            key, pages, tokens = victim
+            self.evicted_keys += 1
+            self.evicted_prefix_tokens += tokens
+            self.evicted_pages += acct.free_key(key)
+            keys.append(key)
+        return tuple(keys)
+
     def activate(self, key, tokens: int, capacity_tokens=None, base_tokens=None, borrow=None):
         """Make a prefix active (pinned), evicting retained KV when needed."""
         acct = self.accounting

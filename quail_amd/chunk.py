@@ -60,6 +60,15 @@ class Chunk:
     host: dict = field(default_factory=dict)
 
 
+def pages_for_questions(arena, groups) -> int:
+    """At most the temporary pages the groups' questions take in a unified
+    pack (a question that does not fit its key's pages gets the prefix's
+    partial last page and its own rows)."""
+    t = arena.page_tokens
+    return sum(arena.pages_needed(t + len(np.asarray(s).reshape(-1)))
+               for g in groups for s in g["suffixes"])
+
+
 def _as_suffixes(sufs):
     arrays = [np.asarray(s, dtype=np.int64) for s in sufs]
     lengths = np.asarray([len(a) for a in arrays], dtype=np.int64)

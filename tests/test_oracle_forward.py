@@ -42,7 +42,7 @@ def test_paged_pack_forward_equals_whole_documents():
             got[d] = normed[i]
         packs += 1
     assert packs >= 2
-    assert adm.borrowing.borrowed_tokens > 0
+    assert adm.borrowed_tokens > 0
     dense = ref.forward_documents(m, wl.prompts)
     paged = torch.stack([got[d] for d in range(len(wl.prompts))])
     torch.testing.assert_close(paged.float(), dense.float(), rtol=0.02, atol=0.02)

@@ -120,10 +120,10 @@ def test_packs_read_exactly_their_documents(seed):
         for d in docs_left:
             arena.free_key(adm.keys[d])
     total = sum(len(d) for d in docs)
-    assert checked == total - adm.borrowing.borrowed_tokens
+    assert checked == total - adm.borrowed_tokens
     assert packs >= 2
     assert arena.free_pages == arena.num_pages
-    assert adm.borrowing.borrowed_tokens > 0
+    assert adm.borrowed_tokens > 0
 
 
 def test_borrowers_read_parent_pages_written_in_the_same_pack():

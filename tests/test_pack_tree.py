@@ -124,7 +124,7 @@ def test_tree_packs_read_exactly_their_documents(seed):
     for left in live:
         for d in left:
             arena.free_key(adm.keys[d])
-    assert checked == sum(len(d) for d in docs) - adm.borrowing.borrowed_tokens
+    assert checked == sum(len(d) for d in docs) - adm.borrowed_tokens
     assert packs >= 2 and stacked > 0
     assert arena.free_pages == arena.num_pages
 
