@@ -121,11 +121,12 @@ int qx_qk_norm_rope(const void* qkv, int64_t qkv_ld, void* q_out, int64_t q_ld, 
  * qx_qk_norm_rope with the row's KV written straight into arena pages: q as
  * above; the normed, rotated K of row i goes to pool row dst[i] of k_pool and
  * its V (qkv columns (HQ+HK)*D .. (HQ+2*HK)*D, bf16) to the same row of
- * v_pool converted to fp16; dst[i] < 0 writes neither. Pool rows are HK*D
+ * v_pool, as bf16, or with v_f16 as fp16 (round to nearest even, saturated
+ * at +-65504); dst[i] < 0 writes neither. Pool rows are HK*D
  * elements. dst2 (may be NULL): the same K and V rows also go to row
  * dst2[i] (when >= 0) of k_pool2 / v_pool2 (the tree path: contiguous rows
  * for call A, dst = 0..n-1, and the arena pages). The same values as
- * qx_qk_norm_rope followed by qx_kv_scatter (src = 0..n-1, v_to_f16 = 1), in
+ * qx_qk_norm_rope followed by qx_kv_scatter (src = 0..n-1), in
  * one pass over qkv: it fuses Engine.qk_norm_rope (attention.py:1251-1255)
  * with the fresh-row write of Engine.write_kv (attention.py:1178-1191) when
  * the pack's scatter source is its own rows in order; the retained-tail copy
@@ -135,7 +136,8 @@ int qx_qk_norm_rope_kv(const void* qkv, int64_t qkv_ld, void* q_out, int64_t q_l
                        void* v_pool, const int64_t* dst, void* k_pool2, void* v_pool2,
                        const int64_t* dst2, const void* cos_sin, int cs_is_f32,
                        const int64_t* positions, const void* q_w, const void* k_w, int64_t n,
-                       int64_t HQ, int64_t HK, int64_t D, float eps, hipStream_t stream);
+                       int64_t HQ, int64_t HK, int64_t D, float eps, int v_f16,
+                       hipStream_t stream);
 
 /*
  * y = g * sigmoid(g) * u over rows [g (I) | u (I)], fp32; per-token
@@ -191,10 +193,11 @@ int qx_group_quant(const void* x, int64_t x_ld, void* q, int64_t q_ld, float* sc
 /*
  * k_pool[dst[i]] = k[src[i]], v_pool[dst[i]] = v[src[i]] for rows of
  * row_elems 16-bit values; dst[i] < 0 writes nothing. Source rows have
- * strides k_ld and v_ld (v may be the strided v slice of qkv). The V pool
- * holds fp16: with v_to_f16 the bf16 V rows are converted (round to nearest
- * even) as they are written; without it (the pool-to-pool tail copy) rows
- * are copied unchanged. Replaces the Triton kv_row_scatter
+ * strides k_ld and v_ld (v may be the strided v slice of qkv). K rows are
+ * bf16 and copied; V rows are copied as they are, or with v_to_f16 the bf16
+ * V rows go to an fp16 V pool (round to nearest even, saturated at
+ * +-65504; the pool-to-pool tail copy runs without it). Replaces the Triton
+ * kv_row_scatter
  * (attention.py:885-897) of Engine.kv_row_scatter / write_kv
  * (attention.py:1165-1195), including its pool-to-pool tail copy. With src
  * and dst both NULL, row i goes to row i (a contiguous copy, V converted:
@@ -209,8 +212,9 @@ int qx_embed(const void* table, int64_t t_ld, const int64_t* ids, void* out, int
              int64_t n, int64_t H, hipStream_t stream);
 
 /*
- * Varlen GQA attention reading K (bf16) and V (fp16, as qx_kv_scatter
- * writes it) through a block table: sequence s has
+ * Varlen GQA attention reading bf16 K and a bf16 (v_bf16 = 1, the
+ * reference arena's pools) or fp16 (v_bf16 = 0) V pool through a block
+ * table: sequence s has
  * query rows [cu_q[s], cu_q[s+1]) and keys [0, used[s]) at pool rows
  * table[s*table_ld + j/page]*page + j%page; causal masking aligned
  * bottom-right. Replaces Engine.attention_unified -> _paged ->
@@ -225,7 +229,7 @@ int qx_paged_attention(const void* q, int64_t q_ld, const void* k_pool, const vo
                        int64_t seqs, int64_t max_q, int64_t max_used, int64_t HQ, int64_t HK,
                        int64_t D, int64_t page, float scale, int causal, void* out_bf16,
                        void* out_fp8, int64_t o_ld, float* scales, int64_t s_ld,
-                       const int* work, int64_t n_work, hipStream_t stream);
+                       const int* work, int64_t n_work, int v_bf16, hipStream_t stream);
 
 /*
  * Host function: the work list for qx_paged_attention's `work` argument
@@ -249,9 +253,9 @@ int64_t qx_paged_attention_work(const int* cu_q, const int* used, int64_t seqs, 
  * lse[h*lse_ld + i] = ln(sum_j exp(scale * q_i . k_j)) (-inf for a row that
  * sees no key).
  *   table != NULL, cu_k == NULL: call B, keys [0, used[s]) read through the
- *     block table as in qx_paged_attention (K bf16, V fp16 pools);
+ *     block table as in qx_paged_attention (bf16 K pool, V as v_bf16 says);
  *   table == NULL, cu_k != NULL: call A, key j of sequence s is row
- *     cu_k[s] + j of k (bf16) and v (fp16), rows of HK * D elements, and
+ *     cu_k[s] + j of k (bf16) and v (as v_bf16 says), rows of HK * D elements, and
  *     used[s] <= cu_k[s+1] - cu_k[s].
  * q_index (may be NULL): query i reads Q row q_index[i] (the reference's
  * q3.index_select(0, reads["rows"]), without the copy). causal aligns
@@ -262,7 +266,7 @@ int qx_attention_lse(const void* q, int64_t q_ld, const int64_t* q_index, const 
                      int64_t table_ld, const int* cu_k, int64_t seqs, int64_t max_q,
                      int64_t max_used, int64_t HQ, int64_t HK, int64_t D, float scale, int causal,
                      void* out_bf16, int64_t o_ld, float* lse, int64_t lse_ld, const int* work,
-                     int64_t n_work, hipStream_t stream);
+                     int64_t n_work, int v_bf16, hipStream_t stream);
 
 /*
  * Replaces Engine.merge_attn_quant / the merge_attn_quant Triton kernel

@@ -34,7 +34,7 @@ SIGNATURES = {
     "qx_qk_norm_rope": [_p, _i64, _p, _i64, _p, _i64, _p, _i32, _p, _p, _p, _i64, _i64, _i64,
                         _i64, _f32, _p],
     "qx_qk_norm_rope_kv": [_p, _i64, _p, _i64, _p, _p, _p, _p, _p, _p, _p, _i32, _p, _p, _p,
-                           _i64, _i64, _i64, _i64, _f32, _p],
+                           _i64, _i64, _i64, _i64, _f32, _i32, _p],
     "qx_silu_mul_quant": [_p, _i64, _p, _i64, _p, _i64, _i64, _i64, _p],
     "qx_gemm_fp8_swiglu_quant": [_p, _p, _p, _p, _p, _i64, _p, _i64, _i64, _i64, _i64, _i64,
                                  _i64, _i32, _p],
@@ -45,10 +45,10 @@ SIGNATURES = {
     "qx_kv_scatter": [_p, _i64, _p, _i64, _p, _p, _p, _p, _i64, _i64, _i32, _p],
     "qx_embed": [_p, _i64, _p, _p, _i64, _i64, _i64, _p],
     "qx_paged_attention": [_p, _i64, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64,
-                           _i64, _i64, _f32, _i32, _p, _p, _i64, _p, _i64, _p, _i64, _p],
+                           _i64, _i64, _f32, _i32, _p, _p, _i64, _p, _i64, _p, _i64, _i32, _p],
     "qx_paged_attention_work": [_p, _p, _i64, _i64, _i64, _i64, _i32, _p, _i64],
     "qx_attention_lse": [_p, _i64, _p, _p, _p, _p, _p, _p, _i64, _p, _i64, _i64, _i64, _i64,
-                         _i64, _i64, _f32, _i32, _p, _i64, _p, _i64, _p, _i64, _p],
+                         _i64, _i64, _f32, _i32, _p, _i64, _p, _i64, _p, _i64, _i32, _p],
     "qx_merge_attn_quant": [_p, _i64, _p, _i64, _p, _i64, _p, _i64, _p, _i64, _i64, _i64, _p,
                             _i64, _p, _i64, _p],
     "qx_merge_partial": [_p, _i64, _p, _i64, _p, _p, _i64, _p, _i64, _i64, _i64, _i64, _p],

@@ -21,9 +21,12 @@ from quail_amd.pages import PageArena
 
 class KVArena:
     def __init__(self, num_layers: int, num_pages: int, page_tokens: int, num_kv_heads: int,
-                 d_head: int, dtype=torch.bfloat16, device="cuda"):
+                 d_head: int, dtype=torch.bfloat16, device="cuda", v_dtype=torch.float16):
+        if dtype != torch.bfloat16 or v_dtype not in (torch.bfloat16, torch.float16):
+            raise ValueError("K pages are bf16; V pages bf16 or fp16")
         self.torch = torch
         self.dtype = dtype
+        self.v_dtype = v_dtype
         self.device = device
         self.num_layers = num_layers
         self.kv_shape = (num_kv_heads, d_head)
@@ -43,9 +46,11 @@ class KVArena:
         storage = torch.empty(2 * self.num_layers * size, dtype=self.dtype, device=self.device)
         parts = storage.split([size] * (2 * self.num_layers))
         self.k = [p.view(rows, heads, dim) for p in parts[0::2]]
-        # V pages hold fp16 (same 16-bit slots): the attention's PV product
-        # runs in fp16, so V is converted once, when it is written
-        self.v = [p.view(torch.float16).view(rows, heads, dim) for p in parts[1::2]]
+        # V pages: bf16 as the reference's arena holds them, or fp16 (the
+        # default here: the same 16-bit slots; bf16 V rows are converted once,
+        # when written, and the PV product then keeps 11 bits of each
+        # probability instead of 8)
+        self.v = [p.view(self.v_dtype).view(rows, heads, dim) for p in parts[1::2]]
         self._holds = {}
         self._deferred = set()
 

@@ -31,10 +31,12 @@
 // O^T keeps one query per lane, so rescaling needs no shuffles. The V^T
 // operand of the PV MFMA comes straight from the row-major V tile through
 // gfx950's transposing LDS read (ds_read_b64_tr_b16). The PV product runs in
-// fp16: P in (0, 1] keeps 11 significant bits (bf16 would keep 8), and the V
-// pool holds fp16 (qx_kv_scatter converts bf16 V rows once, exactly for |v|
-// in [2^-14, 65504]).
+// the V pool's 16-bit type: bf16, as the reference's FlashAttention does with
+// the bf16 pools of its arena, or fp16 for an arena that stores V in fp16
+// (P then keeps 11 significant bits instead of 8); the row sums take the
+// unrounded fp32 P.
 #include <algorithm>
+#include <type_traits>
 #include <vector>
 
 #include "qx_common.h"
@@ -49,7 +51,7 @@ constexpr int kBK = 64;          // keys per KV tile
 constexpr int kPage = 16;        // tokens per arena page
 constexpr int kMaxPages = 2048;  // page-table entries staged in LDS per sequence
 // a row's reference max moves when a tile raises its max by more than this
-// many powers of two (probabilities then stay below 2^8 in fp16)
+// many powers of two (probabilities then stay below 2^8)
 constexpr float kLazyLog2 = 8.0f;
 
 typedef short v4s __attribute__((ext_vector_type(4)));
@@ -68,7 +70,11 @@ __device__ __forceinline__ int vswz(int key) { return D == 128 ? ((key & 3) << 2
 // CONTIG: keys are contiguous rows, key j of sequence s at row cu_k[s] + j
 // (no block table). q_index (optional): query row i reads Q row q_index[i].
 // lse (optional): lse[h * lse_ld + i] = ln(sum_j exp(scale * s_ij)) of row i.
-template <int D, int HPB, int QSUB, bool QUANT, bool CONTIG>
+// VBF: the V pool holds bf16 and the PV product runs in bf16 (P rounded to
+// bf16); otherwise V holds fp16 and P is rounded to fp16 (11 significant
+// bits against bf16's 8: the closer result, for an arena of this engine's
+// own that stores V in fp16).
+template <int D, int HPB, int QSUB, bool QUANT, bool CONTIG, bool VBF>
 __global__ __launch_bounds__(HPB * QSUB * 64) void paged_attention_kernel(
     const uint16_t* __restrict__ q, int64_t q_ld, const int64_t* __restrict__ q_index,
     const uint16_t* __restrict__ kp, const uint16_t* __restrict__ vp,
@@ -279,7 +285,7 @@ __global__ __launch_bounds__(HPB * QSUB * 64) void paged_attention_kernel(
     tmax = max_halves(tmax);
     // Lazy rescale: the reference max m_run, against which p and O are kept,
     // moves only when a tile raises the row max by more than kLazyLog2 (log2
-    // units, so p < 2^kLazyLog2, well inside fp16), and O is rescaled only
+    // units, so p < 2^kLazyLog2), and O is rescaled only
     // when some row of the wave moved: VALU work on the MFMA accumulators
     // stalls the matrix core, and after a row's first tiles its max rarely
     // jumps that far. A tile that adds nothing to a row (wholly masked for
@@ -298,7 +304,8 @@ __global__ __launch_bounds__(HPB * QSUB * 64) void paged_attention_kernel(
         for (int e = 0; e < 16; ++e) o[d][e] *= alpha;
     }
     float psum = 0.f;
-    v8h pf[4];
+    using PV = std::conditional_t<VBF, v8bf, v8h>;
+    PV pf[4];
 #pragma unroll
     for (int kc = 0; kc < 4; ++kc) {
 #pragma unroll
@@ -307,7 +314,11 @@ __global__ __launch_bounds__(HPB * QSUB * 64) void paged_attention_kernel(
         const float pv =
             __builtin_amdgcn_exp2f(fmaf(sacc[kc >> 1][(kc & 1) * 8 + j], scale_log2, -m_use));
         psum += pv;
-        pf[kc][j] = (_Float16)pv;
+        if constexpr (VBF) {
+          pf[kc][j] = (__bf16)pv;
+        } else {
+          pf[kc][j] = (_Float16)pv;
+        }
       }
     }
     psum = sum_halves(psum);
@@ -320,7 +331,7 @@ __global__ __launch_bounds__(HPB * QSUB * 64) void paged_attention_kernel(
 #pragma unroll
     for (int kc = 0; kc < 4; ++kc) {
       const int kbase_b = ((kc >> 1) * 32 + (kc & 1) * 16) * ROW;
-      v8h vf[NDS];
+      PV vf[NDS];
 #pragma unroll
       for (int d = 0; d < NDS; ++d) {
         const v4s lo =
@@ -328,11 +339,15 @@ __global__ __launch_bounds__(HPB * QSUB * 64) void paged_attention_kernel(
         const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
             (lds_v4s*)(vl + kbase_b + 8 * ROW + v_off[d]));
         const v8s both = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-        vf[d] = __builtin_bit_cast(v8h, both);
+        vf[d] = __builtin_bit_cast(PV, both);
       }
 #pragma unroll
       for (int d = 0; d < NDS; ++d)
-        o[d] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[d], pf[kc], o[d], 0, 0, 0);
+        if constexpr (VBF) {
+          o[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[d], pf[kc], o[d], 0, 0, 0);
+        } else {
+          o[d] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[d], pf[kc], o[d], 0, 0, 0);
+        }
     }
   };
 
@@ -439,13 +454,13 @@ __global__ __launch_bounds__(HPB * QSUB * 64) void paged_attention_kernel(
   }
 }
 
-template <int D, int HPB, int QSUB>
-int launch_attn(const void* q, int64_t q_ld, const int64_t* q_index, const void* kp,
-                const void* vp, const int* cu_q, const int* used, const int* table,
-                int64_t table_ld, const int* cu_k, int seqs, int max_q, int max_used, int HQ,
-                int HK, int page, float scale, int causal, void* out16, void* out8, int64_t o_ld,
-                float* scales, int64_t s_ld, float* lse, int64_t lse_ld, const int* work,
-                int n_work, hipStream_t stream) {
+template <int D, int HPB, int QSUB, bool VBF>
+int launch_attn_v(const void* q, int64_t q_ld, const int64_t* q_index, const void* kp,
+                  const void* vp, const int* cu_q, const int* used, const int* table,
+                  int64_t table_ld, const int* cu_k, int seqs, int max_q, int max_used, int HQ,
+                  int HK, int page, float scale, int causal, void* out16, void* out8,
+                  int64_t o_ld, float* scales, int64_t s_ld, float* lse, int64_t lse_ld,
+                  const int* work, int n_work, hipStream_t stream) {
   const int G = HQ / HK;
   constexpr int BQ = 32 * QSUB;
   const int zgroups = HK * (G / HPB);
@@ -457,22 +472,40 @@ int launch_attn(const void* q, int64_t q_ld, const int64_t* q_index, const void*
   const uint16_t* k16 = (const uint16_t*)kp;
   const uint16_t* v16 = (const uint16_t*)vp;
   if (out8) {
-    hipLaunchKernelGGL((paged_attention_kernel<D, HPB, QSUB, true, false>), grid, block, 0,
+    hipLaunchKernelGGL((paged_attention_kernel<D, HPB, QSUB, true, false, VBF>), grid, block, 0,
                        stream, q16, q_ld, q_index, k16, v16, cu_q, used, table, table_ld, cu_k,
                        max_used, HQ, HK, scale_log2, causal, nullptr, (uint8_t*)out8, o_ld,
                        scales, s_ld, lse, lse_ld, work, zgroups, seqs);
   } else if (cu_k) {
-    hipLaunchKernelGGL((paged_attention_kernel<D, HPB, QSUB, false, true>), grid, block, 0,
+    hipLaunchKernelGGL((paged_attention_kernel<D, HPB, QSUB, false, true, VBF>), grid, block, 0,
                        stream, q16, q_ld, q_index, k16, v16, cu_q, used, table, table_ld, cu_k,
                        max_used, HQ, HK, scale_log2, causal, (uint16_t*)out16, nullptr, o_ld,
                        nullptr, 0, lse, lse_ld, work, zgroups, seqs);
   } else {
-    hipLaunchKernelGGL((paged_attention_kernel<D, HPB, QSUB, false, false>), grid, block, 0,
+    hipLaunchKernelGGL((paged_attention_kernel<D, HPB, QSUB, false, false, VBF>), grid, block, 0,
                        stream, q16, q_ld, q_index, k16, v16, cu_q, used, table, table_ld, cu_k,
                        max_used, HQ, HK, scale_log2, causal, (uint16_t*)out16, nullptr, o_ld,
                        nullptr, 0, lse, lse_ld, work, zgroups, seqs);
   }
   QX_LAUNCH_STATUS();
+}
+
+template <int D, int HPB, int QSUB>
+int launch_attn(const void* q, int64_t q_ld, const int64_t* q_index, const void* kp,
+                const void* vp, const int* cu_q, const int* used, const int* table,
+                int64_t table_ld, const int* cu_k, int seqs, int max_q, int max_used, int HQ,
+                int HK, int page, float scale, int causal, void* out16, void* out8, int64_t o_ld,
+                float* scales, int64_t s_ld, float* lse, int64_t lse_ld, const int* work,
+                int n_work, int v_bf16, hipStream_t stream) {
+  if (v_bf16)
+    return launch_attn_v<D, HPB, QSUB, true>(q, q_ld, q_index, kp, vp, cu_q, used, table,
+                                             table_ld, cu_k, seqs, max_q, max_used, HQ, HK, page,
+                                             scale, causal, out16, out8, o_ld, scales, s_ld, lse,
+                                             lse_ld, work, n_work, stream);
+  return launch_attn_v<D, HPB, QSUB, false>(q, q_ld, q_index, kp, vp, cu_q, used, table,
+                                            table_ld, cu_k, seqs, max_q, max_used, HQ, HK, page,
+                                            scale, causal, out16, out8, o_ld, scales, s_ld, lse,
+                                            lse_ld, work, n_work, stream);
 }
 
 // The tree path's merge (attention.py:902-948, merge_attn_quant with QUANT):
@@ -591,7 +624,7 @@ int attention_impl(const void* q, int64_t q_ld, const int64_t* q_index, const vo
                    int64_t max_used, int64_t HQ, int64_t HK, int64_t D, int64_t page, float scale,
                    int causal, void* out_bf16, void* out_fp8, int64_t o_ld, float* scales,
                    int64_t s_ld, float* lse, int64_t lse_ld, const int* work, int64_t n_work,
-                   hipStream_t stream) {
+                   int v_bf16, hipStream_t stream) {
   QX_CHECK(q && k_pool && v_pool && cu_q && used && (table || cu_k), "attention: null pointer");
   QX_CHECK(out_bf16 || out_fp8, "attention: no output");
   QX_CHECK(!(out_fp8 && (cu_k || lse || q_index)), "attention: fused quant is for the paged call");
@@ -614,7 +647,7 @@ int attention_impl(const void* q, int64_t q_ld, const int64_t* q_index, const vo
                                     table_ld, cu_k, args_seqs, args_mq, args_mu, (int)HQ,      \
                                     (int)HK, (int)page, scale, causal, out_bf16, out_fp8,      \
                                     o_ld, scales, s_ld, lse, lse_ld, work, (int)n_work,        \
-                                    stream)
+                                    v_bf16, stream)
   if (D == 128) {
     if (hpb == 4) QX_ATTN(128, 4, 2);
     if (hpb == 2) QX_ATTN(128, 2, 4);
@@ -635,6 +668,7 @@ extern "C" {
 
 // out_fp8 != NULL: write the e4m3 o_proj input and its scales (D must be
 // 128); otherwise write bf16 to out_bf16. o_ld is in elements of the output.
+// v_bf16: the V pool holds bf16 (the reference arena's pools), else fp16.
 // max_used bounds every used[s] (FA's max_seqlen_k) and must be at most
 // 2048 * page (the page-table row each workgroup stages in LDS).
 int qx_paged_attention(const void* q, int64_t q_ld, const void* k_pool, const void* v_pool,
@@ -642,29 +676,31 @@ int qx_paged_attention(const void* q, int64_t q_ld, const void* k_pool, const vo
                        int64_t seqs, int64_t max_q, int64_t max_used, int64_t HQ, int64_t HK,
                        int64_t D, int64_t page, float scale, int causal, void* out_bf16,
                        void* out_fp8, int64_t o_ld, float* scales, int64_t s_ld,
-                       const int* work, int64_t n_work, hipStream_t stream) {
+                       const int* work, int64_t n_work, int v_bf16, hipStream_t stream) {
   QX_CHECK(table, "attention: null pointer");
   return qx::attention_impl(q, q_ld, nullptr, k_pool, v_pool, cu_q, used, table, table_ld,
                             nullptr, seqs, max_q, max_used, HQ, HK, D, page, scale, causal,
                             out_bf16, out_fp8, o_ld, scales, s_ld, nullptr, 0, work, n_work,
-                            stream);
+                            v_bf16, stream);
 }
 
 // The tree path's two calls: bf16 output plus each row's log-sum-exp.
 // table != NULL: paged keys as in qx_paged_attention; table == NULL: key j
-// of sequence s is row cu_k[s] + j of k and v (rows of HK * D elements, V
-// fp16). q_index (may be NULL): query row i reads Q row q_index[i].
+// of sequence s is row cu_k[s] + j of k (bf16) and v, rows of HK * D
+// elements. q_index (may be NULL): query row i reads Q row q_index[i].
+// v_bf16: V (pool or rows) holds bf16, else fp16.
 int qx_attention_lse(const void* q, int64_t q_ld, const int64_t* q_index, const void* k,
                      const void* v, const int* cu_q, const int* used, const int* table,
                      int64_t table_ld, const int* cu_k, int64_t seqs, int64_t max_q,
                      int64_t max_used, int64_t HQ, int64_t HK, int64_t D, float scale, int causal,
                      void* out_bf16, int64_t o_ld, float* lse, int64_t lse_ld, const int* work,
-                     int64_t n_work, hipStream_t stream) {
+                     int64_t n_work, int v_bf16, hipStream_t stream) {
   QX_CHECK(out_bf16 && lse, "attention_lse: null output");
   QX_CHECK((table == nullptr) != (cu_k == nullptr), "attention_lse: give a table or cu_k");
   return qx::attention_impl(q, q_ld, q_index, k, v, cu_q, used, table, table_ld, cu_k, seqs,
                             max_q, max_used, HQ, HK, D, qx::kPage, scale, causal, out_bf16,
-                            nullptr, o_ld, nullptr, 0, lse, lse_ld, work, n_work, stream);
+                            nullptr, o_ld, nullptr, 0, lse, lse_ld, work, n_work, v_bf16,
+                            stream);
 }
 
 // The tree path's LSE merge fused with the o_proj input quantization

@@ -69,10 +69,21 @@ __device__ __forceinline__ uint32_t pack2_bf16(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, v);
 }
 
-// Two fp32 -> packed fp16 (round to nearest even).
-__device__ __forceinline__ uint32_t pack2_f16(float lo, float hi) {
-  const f16x2 v = {(_Float16)lo, (_Float16)hi};
+// Two fp32 -> packed fp16, round to nearest even, saturated at +-65504 (a
+// value past fp16's range becomes its largest finite value, not inf).
+__device__ __forceinline__ uint32_t pack2_f16_sat(float lo, float hi) {
+  const f16x2 v = {(_Float16)fminf(fmaxf(lo, -65504.0f), 65504.0f),
+                   (_Float16)fminf(fmaxf(hi, -65504.0f), 65504.0f)};
   return __builtin_bit_cast(uint32_t, v);
+}
+
+// The 8 bf16 of a 16-byte chunk as fp16 (pack2_f16_sat).
+__device__ __forceinline__ uint4 bf16x8_to_f16(uint4 w) {
+  w.x = pack2_f16_sat(lo_bf16(w.x), hi_bf16(w.x));
+  w.y = pack2_f16_sat(lo_bf16(w.y), hi_bf16(w.y));
+  w.z = pack2_f16_sat(lo_bf16(w.z), hi_bf16(w.z));
+  w.w = pack2_f16_sat(lo_bf16(w.w), hi_bf16(w.w));
+  return w;
 }
 
 // Butterfly reductions across `width` consecutive lanes of a wave64.

@@ -229,10 +229,11 @@ __global__ __launch_bounds__(kRowThreads) void add_rmsnorm_kernel(
 // throughout, bf16 output. A head is handled by D/8 lanes; each lane holds 4
 // columns of the first half (a) and the matching 4 of the second half (b).
 // POOL: the row's K goes to pool row dst[row] of kp (ko unused) and its V
-// (the qkv columns after the K heads) to the same row of vp, converted to
-// fp16 as qx_kv_scatter converts it; dst[row] < 0 writes neither. With dst2,
-// the same K and V rows also go to row dst2[row] (when >= 0) of kp2 / vp2.
-template <int D, bool CS_F32, bool POOL>
+// (the qkv columns after the K heads) to the same row of vp, as bf16 or,
+// with V_F16, as fp16 (pack2_f16_sat, as qx_kv_scatter converts it);
+// dst[row] < 0 writes neither. With dst2, the same K and V rows also go to
+// row dst2[row] (when >= 0) of kp2 / vp2.
+template <int D, bool CS_F32, bool POOL, bool V_F16 = false>
 __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
     const uint16_t* __restrict__ qkv, int64_t qkv_ld, uint16_t* __restrict__ qo, int64_t qo_ld,
     uint16_t* __restrict__ ko, int64_t ko_ld, const void* __restrict__ cs,
@@ -259,11 +260,7 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
       uint4* vd = drow >= 0 ? reinterpret_cast<uint4*>(vp + drow * kv_row) : nullptr;
       uint4* vd2 = drow2 >= 0 ? reinterpret_cast<uint4*>(vp2 + drow2 * kv_row) : nullptr;
       for (int c = threadIdx.x; c < (int)(kv_row >> 3); c += 256) {
-        uint4 w = vs[c];
-        w.x = pack2_f16(lo_bf16(w.x), hi_bf16(w.x));
-        w.y = pack2_f16(lo_bf16(w.y), hi_bf16(w.y));
-        w.z = pack2_f16(lo_bf16(w.z), hi_bf16(w.z));
-        w.w = pack2_f16(lo_bf16(w.w), hi_bf16(w.w));
+        const uint4 w = V_F16 ? bf16x8_to_f16(vs[c]) : vs[c];
         if (drow >= 0) vd[c] = w;
         if (drow2 >= 0) vd2[c] = w;
       }
@@ -385,9 +382,9 @@ __global__ __launch_bounds__(256) void group_quant_kernel(const uint16_t* __rest
 // ---------------------------------------------------------------------------
 // pool[dst[i]] = rows[src[i]] for K and V; dst < 0 writes nothing
 // (attention.py:885-897); without src and dst, row i goes to row i. One
-// wave per pair; rows are row_elems bf16.
-// V_F16: V source rows are bf16 and the V pool holds fp16 (round to nearest
-// even, exact for |v| in [2^-14, 65504]); otherwise both are copied as they are
+// wave per pair; rows are row_elems 16-bit values. V_F16: V source rows are
+// bf16 and the V pool holds fp16 (pack2_f16_sat: round to nearest even,
+// saturated at +-65504); otherwise both are copied as they are.
 template <bool V_F16>
 __global__ __launch_bounds__(256) void kv_scatter_kernel(
     const uint16_t* __restrict__ k, int64_t k_ld, const uint16_t* __restrict__ v, int64_t v_ld,
@@ -406,14 +403,7 @@ __global__ __launch_bounds__(256) void kv_scatter_kernel(
   const int nch = row_elems >> 3;
   for (int c = lane; c < nch; c += 64) {
     kd[c] = ks[c];
-    uint4 w = vs[c];
-    if (V_F16) {
-      w.x = pack2_f16(lo_bf16(w.x), hi_bf16(w.x));
-      w.y = pack2_f16(lo_bf16(w.y), hi_bf16(w.y));
-      w.z = pack2_f16(lo_bf16(w.z), hi_bf16(w.z));
-      w.w = pack2_f16(lo_bf16(w.w), hi_bf16(w.w));
-    }
-    vd[c] = w;
+    vd[c] = V_F16 ? bf16x8_to_f16(vs[c]) : vs[c];
   }
 }
 
@@ -524,24 +514,26 @@ int qk_norm_rope_launch(const void* qkv, int64_t qkv_ld, void* q_out, int64_t q_
                         const int64_t* positions, const void* q_w, const void* k_w, int64_t n,
                         int64_t HQ, int64_t HK, int64_t D, float eps, void* k_pool, void* v_pool,
                         const int64_t* dst, void* k_pool2, void* v_pool2, const int64_t* dst2,
-                        hipStream_t stream) {
+                        int v_f16, hipStream_t stream) {
   QX_CHECK(D == 64 || D == 128, "qk_norm_rope: head_dim %lld (64 or 128)", (long long)D);
   QX_CHECK(HQ > 0 && HK > 0, "qk_norm_rope: heads");
   QX_CHECK(qkv_ld % 4 == 0 && q_ld % 4 == 0 && k_ld % 4 == 0, "qk_norm_rope: strides");
   if (n == 0) return QX_OK;
   dim3 grid((unsigned)n), block(256);
-#define QX_QK(DD, F32, P)                                                                      \
-  hipLaunchKernelGGL((qk_norm_rope_kernel<DD, F32, P>), grid, block, 0, stream,                \
+#define QX_QK(DD, F32, P, VF)                                                                  \
+  hipLaunchKernelGGL((qk_norm_rope_kernel<DD, F32, P, VF>), grid, block, 0, stream,            \
                      (const uint16_t*)qkv, qkv_ld, (uint16_t*)q_out, q_ld, (uint16_t*)k_out,  \
                      k_ld, cos_sin, positions, (const uint16_t*)q_w, (const uint16_t*)k_w,    \
                      (int)n, (int)HQ, (int)HK, eps, (uint16_t*)k_pool, (uint16_t*)v_pool, dst, \
                      (uint16_t*)k_pool2, (uint16_t*)v_pool2, dst2)
-#define QX_QK_D(DD, P) \
-  if (cs_is_f32) QX_QK(DD, true, P); else QX_QK(DD, false, P);
-  if (dst) {
-    if (D == 128) { QX_QK_D(128, true) } else { QX_QK_D(64, true) }
+#define QX_QK_D(DD, P, VF) \
+  if (cs_is_f32) QX_QK(DD, true, P, VF); else QX_QK(DD, false, P, VF);
+  if (dst && v_f16) {
+    if (D == 128) { QX_QK_D(128, true, true) } else { QX_QK_D(64, true, true) }
+  } else if (dst) {
+    if (D == 128) { QX_QK_D(128, true, false) } else { QX_QK_D(64, true, false) }
   } else {
-    if (D == 128) { QX_QK_D(128, false) } else { QX_QK_D(64, false) }
+    if (D == 128) { QX_QK_D(128, false, false) } else { QX_QK_D(64, false, false) }
   }
 #undef QX_QK_D
 #undef QX_QK
@@ -557,14 +549,15 @@ int qx_qk_norm_rope(const void* qkv, int64_t qkv_ld, void* q_out, int64_t q_ld, 
            "qk_norm_rope: null pointer");
   return qk_norm_rope_launch(qkv, qkv_ld, q_out, q_ld, k_out, k_ld, cos_sin, cs_is_f32,
                              positions, q_w, k_w, n, HQ, HK, D, eps, nullptr, nullptr, nullptr,
-                             nullptr, nullptr, nullptr, stream);
+                             nullptr, nullptr, nullptr, 0, stream);
 }
 
 int qx_qk_norm_rope_kv(const void* qkv, int64_t qkv_ld, void* q_out, int64_t q_ld, void* k_pool,
                        void* v_pool, const int64_t* dst, void* k_pool2, void* v_pool2,
                        const int64_t* dst2, const void* cos_sin, int cs_is_f32,
                        const int64_t* positions, const void* q_w, const void* k_w, int64_t n,
-                       int64_t HQ, int64_t HK, int64_t D, float eps, hipStream_t stream) {
+                       int64_t HQ, int64_t HK, int64_t D, float eps, int v_f16,
+                       hipStream_t stream) {
   QX_CHECK(qkv && q_out && k_pool && v_pool && dst && cos_sin && positions && q_w && k_w,
            "qk_norm_rope_kv: null pointer");
   QX_CHECK(!dst2 || (k_pool2 && v_pool2), "qk_norm_rope_kv: second destination pools");
@@ -573,7 +566,7 @@ int qx_qk_norm_rope_kv(const void* qkv, int64_t qkv_ld, void* q_out, int64_t q_l
            "qk_norm_rope_kv: alignment");
   return qk_norm_rope_launch(qkv, qkv_ld, q_out, q_ld, nullptr, 0, cos_sin, cs_is_f32, positions,
                              q_w, k_w, n, HQ, HK, D, eps, k_pool, v_pool, dst, k_pool2, v_pool2,
-                             dst2, stream);
+                             dst2, v_f16, stream);
 }
 
 int qx_silu_mul_quant(const void* gate_up, int64_t gu_ld, void* q, int64_t q_ld, float* scales,
@@ -616,17 +609,16 @@ int qx_kv_scatter(const void* k, int64_t k_ld, const void* v, int64_t v_ld, void
                aligned16(v_pool),
            "kv_scatter: alignment");
   if (count == 0) return QX_OK;
-  if (v_to_f16) {
+  if (v_to_f16)
     hipLaunchKernelGGL(kv_scatter_kernel<true>, dim3((unsigned)((count + 3) / 4)), dim3(256), 0,
                        stream, (const uint16_t*)k, k_ld, (const uint16_t*)v, v_ld,
                        (uint16_t*)k_pool, (uint16_t*)v_pool, src, dst, (int)count,
                        (int)row_elems);
-  } else {
+  else
     hipLaunchKernelGGL(kv_scatter_kernel<false>, dim3((unsigned)((count + 3) / 4)), dim3(256), 0,
                        stream, (const uint16_t*)k, k_ld, (const uint16_t*)v, v_ld,
                        (uint16_t*)k_pool, (uint16_t*)v_pool, src, dst, (int)count,
                        (int)row_elems);
-  }
   QX_LAUNCH_STATUS();
 }
 

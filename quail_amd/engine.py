@@ -24,23 +24,20 @@ from quail_amd import _lib
 
 GROUP = 128
 
-# GEMM tile configurations (see csrc/gemm_fp8.hip); every one computes each
-# output element with the same operations in the same order, so the choice
-# never changes a result bit. 10 = 256 tokens x 256 weights, 8 waves, two
-# 128-byte K stages (128 KiB LDS) is fastest on all four Qwen3-4B
-# projections inside the prefill pass at ~16k tokens (128 x 256 tiles,
-# config 14, fill the 2.5 waves of the narrow projections better in
-# isolation but measured slower in the pass); 5 = 256 x 128, 4 waves,
-# 64-byte stages, takes widths that are not multiples of 256.
-# QUAIL_GEMM_CONFIG forces one.
+# GEMM tile configurations (csrc/gemm_fp8.hip); each computes every output
+# element with the same operations in the same order, so the choice never
+# changes a result bit. 10 = 256 tokens x 256 weights, 8 waves, two 128-K
+# stages (128 KiB LDS), one workgroup per tile; 11 = 256 x 128, 4 waves,
+# takes widths that are not multiples of 256; 22 = config 10's tiles on a
+# persistent grid with the K pipeline running across tiles: faster when the
+# 256 x 256 tiles fill whole waves of the 256 CUs (the fill and epilogue of
+# one tile overlap the next), slower on a partial last wave, which one
+# workgroup per tile spreads better. QUAIL_GEMM_CONFIG forces one.
 GEMM_CONFIG_ENV = "QUAIL_GEMM_CONFIG"
+GEMM_CONFIGS = (10, 11, 22)
 GEMM_DEFAULT_CONFIG = 10
 SWIGLU_DEFAULT_CONFIG = 10
-GEMM_ODD_WIDTH_CONFIG = 5
-# 22 = config 10's tiles on a persistent grid with the K pipeline running
-# across tiles: faster when the 256 x 256 tiles fill whole waves of the 256
-# CUs (the fill and epilogue of one tile overlap the next), slower on a
-# partial last wave, which one workgroup per tile spreads better
+GEMM_ODD_WIDTH_CONFIG = 11
 GEMM_WHOLE_WAVES_CONFIG = 22
 CUS = 256
 
@@ -318,11 +315,11 @@ class Engine:
         return q, k
 
     def qk_norm_rope_rows(self, qkv, positions, attn, identity=None, meta=None):
-        """q, k and fp16 v rows in one pass over qkv (qx_qk_norm_rope_kv
-        with the identity row map; `identity` = arange(n) int64 on the
-        device, made here when not given): the tree path's call A reads K
-        and V of the pack's own rows contiguous, V in fp16 as the pages
-        hold it. With a tree pack's meta carrying `row_pool_dst` (pool row
+        """q, k and v rows in one pass over qkv (qx_qk_norm_rope_kv with the
+        identity row map; `identity` = arange(n) int64 on the device, made
+        here when not given): the tree path's call A reads K and V of the
+        pack's own rows contiguous, V of the arena's V type. With a tree
+        pack's meta carrying `row_pool_dst` (pool row
         per pack row, -1 for none), the same pass also writes the pack's KV
         into the arena pages of meta's layer (the kv_src -> kv_dst writes,
         attention.py:1405)."""
@@ -333,7 +330,8 @@ class Engine:
         dev = qkv.device
         q = torch.empty((n, hq * d), dtype=torch.bfloat16, device=dev)
         k = torch.empty((n, hk * d), dtype=torch.bfloat16, device=dev)
-        v = torch.empty((n, hk * d), dtype=torch.float16, device=dev)
+        v_dtype = self._v_dtype()
+        v = torch.empty((n, hk * d), dtype=v_dtype, device=dev)
         rows = identity if identity is not None else torch.arange(n, dtype=torch.int64,
                                                                    device=dev)
         if rows.shape[0] != n or rows.dtype != torch.int64:
@@ -345,14 +343,13 @@ class Engine:
             if dst2.shape[0] != n:
                 raise ValueError(f"row_pool_dst has {dst2.shape[0]} rows, qkv {n}")
             pools = self.arena.layer_kv(meta["layer"])
-            if pools[1].dtype != torch.float16:
-                raise ValueError(f"V pool dtype {pools[1].dtype}: this engine keeps V pages "
-                                 f"in fp16")
+            self._check_pools(*pools)
         _lib.call("qx_qk_norm_rope_kv", _ptr(qkv), qkv.stride(0), _ptr(q), q.stride(0), _ptr(k),
                   _ptr(v), _ptr(rows), _ptr(pools[0]), _ptr(pools[1]), _ptr(dst2), _ptr(cache),
                   int(cache.dtype == torch.float32),
                   _ptr(positions), _ptr(attn.q_norm.weight), _ptr(attn.k_norm.weight), n, hq,
-                  hk, d, float(attn.q_norm.variance_epsilon), _stream())
+                  hk, d, float(attn.q_norm.variance_epsilon), int(v_dtype == torch.float16),
+                  _stream())
         if dst2 is not None:
             meta["kv_fresh_layer"] = meta["layer"]
         return q, k, v
@@ -372,33 +369,48 @@ class Engine:
             raise ValueError(f"row_dst has {dst.shape[0]} rows, qkv {n}")
         layer = meta["layer"]
         k_pool, v_pool = self.arena.layer_kv(layer)
-        if v_pool.dtype != torch.float16:
-            raise ValueError(f"V pool dtype {v_pool.dtype}: this engine keeps V pages in fp16")
+        self._check_pools(k_pool, v_pool)
         q = torch.empty((n, hq * d), dtype=torch.bfloat16, device=qkv.device)
         cache = self._rope_cache()
         _lib.call("qx_qk_norm_rope_kv", _ptr(qkv), qkv.stride(0), _ptr(q), q.stride(0),
                   _ptr(k_pool), _ptr(v_pool), _ptr(dst), None, None, None, _ptr(cache),
                   int(cache.dtype == torch.float32), _ptr(positions), _ptr(attn.q_norm.weight),
                   _ptr(attn.k_norm.weight), n, hq, hk, d, float(attn.q_norm.variance_epsilon),
-                  _stream())
+                  int(v_pool.dtype == torch.float16), _stream())
         meta["kv_fresh_layer"] = layer
         return q
 
+    @staticmethod
+    def _check_pools(k_pool, v_pool):
+        """K pools are bf16; V pools bf16 (the reference KVArena's,
+        arena.py:111-121) or fp16 (an arena of this engine's own that keeps
+        V in fp16: the PV product then runs with fp16 probabilities)."""
+        if k_pool.dtype != torch.bfloat16:
+            raise ValueError(f"K pool dtype {k_pool.dtype}: K pages are bf16")
+        if v_pool.dtype not in (torch.bfloat16, torch.float16):
+            raise ValueError(f"V pool dtype {v_pool.dtype}: V pages are bf16 or fp16")
+
+    def _v_dtype(self):
+        return self.arena.layer_kv(0)[1].dtype
+
     def kv_row_scatter(self, k3, v3, src, dst, layer):
         """Scatter KV rows into the layer's arena pages; dst < 0 is padding.
-
-        The V pages hold fp16 (the PV product runs in fp16): bf16 V rows are
-        converted as they are written; rows already in the pools (the tail
-        copy, v3 of dtype float16) are copied unchanged."""
+        bf16 V rows going to an fp16 V pool are converted (saturated at
+        +-65504); rows already of the pool's type (the tail copy) are copied."""
         count = src.shape[0]
         row = self.num_kv_heads * self.head_dim
         k_pool, v_pool = self.arena.layer_kv(layer)
-        if v_pool.dtype != torch.float16:
-            raise ValueError(f"V pool dtype {v_pool.dtype}: this engine keeps V pages in fp16")
-        k_ld = k3.stride(0)
-        v_ld = v3.stride(0)
-        _lib.call("qx_kv_scatter", _ptr(k3), k_ld, _ptr(v3), v_ld, _ptr(k_pool), _ptr(v_pool),
-                  _ptr(src), _ptr(dst), count, row, int(v3.dtype != torch.float16), _stream())
+        self._check_pools(k_pool, v_pool)
+        if k3.dtype != torch.bfloat16:
+            raise ValueError(f"K rows dtype {k3.dtype}: K pages are bf16")
+        if v3.dtype == v_pool.dtype:
+            convert = 0
+        elif v3.dtype == torch.bfloat16 and v_pool.dtype == torch.float16:
+            convert = 1
+        else:
+            raise ValueError(f"V rows of {v3.dtype} cannot go to a {v_pool.dtype} pool")
+        _lib.call("qx_kv_scatter", _ptr(k3), k3.stride(0), _ptr(v3), v3.stride(0), _ptr(k_pool),
+                  _ptr(v_pool), _ptr(src), _ptr(dst), count, row, convert, _stream())
 
     def write_kv(self, k3, v3, meta, *, copy_tail=True):
         """Write fresh rows and retained partial pages (attention.py:1175-1195)."""
@@ -463,17 +475,18 @@ class Engine:
         written = meta.pop("kv_fresh_layer", None) == layer   # by qk_norm_rope_rows
         if meta.get("kv_src") is not None and meta["kv_src"].numel() and not written:
             self.kv_row_scatter(k3, v3, meta["kv_src"], meta["kv_dst"], layer)
-        # call A reads the pack's own K and V rows: contiguous, V in fp16 as
-        # the pages hold it (as qk_norm_rope_rows gives them, else one
-        # identity scatter)
+        # call A reads the pack's own K and V rows contiguous (as
+        # qk_norm_rope_rows gives them, else one identity scatter)
         row = hk * d
-        if (v3.dtype == torch.float16 and k3.is_contiguous() and v3.is_contiguous()):
+        v_dtype = self._v_dtype()
+        if k3.is_contiguous() and v3.is_contiguous() and v3.dtype == v_dtype:
             k_rows, v_rows = k3.reshape(n, row), v3.reshape(n, row)
         else:
             k_rows = torch.empty((n, row), dtype=torch.bfloat16, device=dev)
-            v_rows = torch.empty((n, row), dtype=torch.float16, device=dev)
+            v_rows = torch.empty((n, row), dtype=v_dtype, device=dev)
             _lib.call("qx_kv_scatter", _ptr(k3), k3.stride(0), _ptr(v3), v3.stride(0),
-                      _ptr(k_rows), _ptr(v_rows), None, None, n, row, 1, _stream())
+                      _ptr(k_rows), _ptr(v_rows), None, None, n, row,
+                      int(v3.dtype != v_dtype), _stream())
         scale = float(d ** -0.5)
         seg = meta["segments"]
         out_a = torch.empty((n, hq * d), dtype=torch.bfloat16, device=dev)
@@ -523,7 +536,7 @@ class Engine:
         nk = nodes["key_rows"].shape[0]
         row = hk * d
         k_c = torch.empty((nk, row), dtype=torch.bfloat16, device=dev)
-        v_c = torch.empty((nk, row), dtype=torch.float16, device=dev)
+        v_c = torch.empty((nk, row), dtype=v_rows.dtype, device=dev)
         into = nodes.get("gather_rows")
         if not torch.is_tensor(into):
             into = torch.arange(nk, dtype=torch.int64, device=dev)
@@ -553,7 +566,7 @@ class Engine:
                   table.stride(0) if table is not None else 0, _ptr(cu_k), seqs,
                   int(tables["max_q"]), int(tables["max_used"]), hq, hk, d, scale,
                   int(tables.get("causal", True)), _ptr(out), out.stride(0), _ptr(lse),
-                  lse.stride(0), _ptr(work), n_work, _stream())
+                  lse.stride(0), _ptr(work), n_work, int(v.dtype == torch.bfloat16), _stream())
 
     def attention_unified(self, q3, k3, v3, meta, *, softmax_scale=None, output=None):
         """Write the chunk's KV to its pages, then one paged causal call with
@@ -590,6 +603,8 @@ class Engine:
         n = q3.shape[0]
         hq, hk, d = self.num_q_heads, self.num_kv_heads, self.head_dim
         k_pool, v_pool = self.arena.layer_kv(layer)
+        self._check_pools(k_pool, v_pool)
+        v_bf16 = int(v_pool.dtype == torch.bfloat16)
         scale = d ** -0.5 if softmax_scale is None else softmax_scale
         table = tables["table"]
         if output is not None:
@@ -611,12 +626,12 @@ class Engine:
         if d == GROUP:
             _lib.call("qx_paged_attention", _ptr(q3), q_ld, *args, None, _ptr(o_q),
                       o_q.stride(0), _ptr(o_s), self._scale_ld(o_s), _ptr(work), n_work,
-                      _stream())
+                      v_bf16, _stream())
         else:
             # a 128-column FP8 group spans several heads: bf16 out, then quant
             o = torch.empty((n, hq * d), dtype=torch.bfloat16, device=q3.device)
             _lib.call("qx_paged_attention", _ptr(q3), q_ld, *args, _ptr(o), None, o.stride(0),
-                      None, 0, _ptr(work), n_work, _stream())
+                      None, 0, _ptr(work), n_work, v_bf16, _stream())
             self.quant(o, output=(o_q, o_s))
         return o_q, o_s
 
@@ -633,5 +648,6 @@ class Engine:
                   unified["used"].shape[0], int(unified["max_q"]), int(unified["max_used"]),
                   hq, hk, d,
                   self.arena.page_tokens, float(d ** -0.5), int(unified.get("causal", True)),
-                  _ptr(o), None, o.stride(0), None, 0, None, 0, _stream())
+                  _ptr(o), None, o.stride(0), None, 0, None, 0,
+                  int(v_pool.dtype == torch.bfloat16), _stream())
         return o

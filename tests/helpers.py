@@ -28,9 +28,10 @@ def ref_model(model) -> ref.RefModel:
 
 
 def run_stage(model, workload, readout_kind="margins", num_pages=None, use_tree=True,
-              attention_mode="unified", fuse_kv_write=None):
+              attention_mode="unified", fuse_kv_write=None, v_dtype=None):
     """Run one stage of the workload through the GPU engine; returns
-    (results per document, StageRun)."""
+    (results per document, StageRun). v_dtype: the arena's V page type
+    (its default, fp16, when None; bf16 is the reference arena's)."""
     from quail_amd.arena import KVArena
     from quail_amd.executor import StageRun
     from quail_amd.model import retain_answer_head
@@ -42,7 +43,8 @@ def run_stage(model, workload, readout_kind="margins", num_pages=None, use_tree=
         num_pages = 3 * workload.chunk_budget // workload.page_tokens + 64
     arena = KVArena(cfg.layers if len(model.model.layers) == cfg.layers else
                     len(model.model.layers), num_pages, workload.page_tokens,
-                    cfg.kv_heads, cfg.head_dim)
+                    cfg.kv_heads, cfg.head_dim,
+                    **({} if v_dtype is None else dict(v_dtype=v_dtype)))
     pipe = Qwen3Pipeline(model, arena)
     if fuse_kv_write is not None:
         pipe.fuse_kv_write = fuse_kv_write

@@ -98,7 +98,10 @@ def test_gemm_small_shapes_match_dequantized_matmul(m, n, k):
     _bf16_close(out, want)
 
 
-@pytest.mark.parametrize("config", list(range(23)))
+GEMM_CONFIGS = (10, 11, 22)
+
+
+@pytest.mark.parametrize("config", GEMM_CONFIGS)
 def test_gemm_tile_configs_agree(config, monkeypatch):
     q, s, wq, ws = _gemm_case(300, 512, 512, seed=9)
     monkeypatch.setenv("QUAIL_GEMM_CONFIG", str(config))
@@ -112,27 +115,28 @@ def test_gemm_configs_are_bit_identical(monkeypatch):
     operations in the same order (the engine picks configs by shape, and a
     row's result must not depend on it)."""
     q, s, wq, ws = _gemm_case(700, 1024, 1024, seed=11)
-    outs = []
-    for config in range(23):
-        monkeypatch.setenv("QUAIL_GEMM_CONFIG", str(config))
-        outs.append(_run_gemm(q, s, wq, ws).cpu())
-    for config, out in enumerate(outs):
-        assert torch.equal(out, outs[0]), config
-
-
-def test_gemm_persistent_configs_with_several_tiles_per_workgroup(monkeypatch):
-    """More tiles than CUs (9 x 16 tiles of 256x256, 9 x 32 of 256x128, a
-    partial last row of tiles): the persistent configurations (16, 17) walk
-    several tiles per workgroup and must equal the one-tile-per-workgroup
-    configuration bit for bit, and the oracle to the bf16 tolerance."""
-    q, s, wq, ws = _gemm_case(2125, 4096, 384, seed=13)
     outs = {}
-    for config in (10, 5, 16, 17, 18, 19, 20, 21, 22):
+    for config in GEMM_CONFIGS:
         monkeypatch.setenv("QUAIL_GEMM_CONFIG", str(config))
         outs[config] = _run_gemm(q, s, wq, ws).cpu()
-    for config in (5, 16, 17, 18, 19, 20, 21, 22):
+    for config, out in outs.items():
+        assert torch.equal(out, outs[10]), config
+
+
+def test_gemm_persistent_config_with_several_tiles_per_workgroup(monkeypatch):
+    """More tiles than CUs (20 x 16 = 320 tiles of 256x256 on a persistent
+    grid of 256 workgroups, a partial last row of tiles at M = 5000, an even
+    number of 128-K blocks so the cross-tile pipeline runs): config 22 walks
+    several tiles per workgroup and equals the one-tile-per-workgroup
+    configuration bit for bit, and the oracle to the bf16 tolerance."""
+    q, s, wq, ws = _gemm_case(5000, 4096, 512, seed=13)
+    outs = {}
+    for config in GEMM_CONFIGS:
+        monkeypatch.setenv("QUAIL_GEMM_CONFIG", str(config))
+        outs[config] = _run_gemm(q, s, wq, ws).cpu()
+    for config in GEMM_CONFIGS:
         assert torch.equal(outs[config], outs[10]), config
-    _bf16_close(outs[16], ref.gemm(q, s, ref.RefLinear(wq, ws)))
+    _bf16_close(outs[22], ref.gemm(q, s, ref.RefLinear(wq, ws)))
 
 
 def test_gemm_configs_agree_with_zero_weight_blocks(monkeypatch):
@@ -140,16 +144,14 @@ def test_gemm_configs_agree_with_zero_weight_blocks(monkeypatch):
     or run them on zero fragments, and all must agree bit for bit: zero
     blocks at the first and last K block, two in a row, and a whole
     128-row weight block column."""
-    q, s, wq, ws = _gemm_case(520, 768, 1024, seed=17)
+    q, s, wq, ws = _gemm_case(520, 1024, 1024, seed=17)
     ws = ws.clone()
     ws[0, 0] = 0.0
     ws[1, 7] = 0.0
     ws[2, 3] = ws[2, 4] = 0.0
     ws[5, :] = 0.0
     outs = {}
-    for config in range(23):
-        if config in (0, 1, 3, 7, 10, 13, 14, 15, 16, 18, 19, 20, 21, 22) and 768 % 256:
-            continue
+    for config in GEMM_CONFIGS:
         monkeypatch.setenv("QUAIL_GEMM_CONFIG", str(config))
         outs[config] = _run_gemm(q, s, wq, ws).cpu()
     for config, out in outs.items():
@@ -192,12 +194,14 @@ def test_gate_up_swiglu_quant_equals_gemm_then_activation_quant(m, i, k, zero_bl
     assert torch.equal(got_s, want_s)
 
 
-@pytest.mark.parametrize("m,n,k", [(16294, 6144, 2560), (16294, 2560, 9728), (4000, 19456, 640)])
+@pytest.mark.parametrize("m,n,k", [(16294, 6144, 2560), (16294, 2560, 9728), (4000, 19456, 768),
+                                   (4000, 19456, 640)])
 def test_gemm_persistent_cross_tile_pipeline_at_pack_shapes(m, n, k, monkeypatch):
     """Config 22 (persistent, the next tile's first block loaded during the
-    current tile's last) at a pack's qkv and down shapes, several tiles per
-    workgroup, and an odd number of 128-K blocks per tile (the stage parity
-    alternates from tile to tile): bit-identical to config 10."""
+    current tile's last) at a pack's qkv and down shapes and at a ragged M
+    with several tiles per workgroup (K = 768: six 128-K blocks): bit-identical
+    to config 10. At K = 640 (five blocks, an odd count) config 22 falls back
+    to config 10's one-tile-per-workgroup launch, which this case checks."""
     q, s, wq, ws = _gemm_case(m, n, k, seed=m + n + k)
     outs = {}
     for config in (10, 22):
@@ -209,11 +213,12 @@ def test_gemm_persistent_cross_tile_pipeline_at_pack_shapes(m, n, k, monkeypatch
 @pytest.mark.parametrize("k,n", [(2560, 6144), (4096, 2560), (2560, 19456), (9728, 2560)])
 def test_gemm_qwen3_4b_shapes_at_8192_tokens(k, n):
     """The GEMM-alone config: M=8192 at the four Qwen3-4B projection shapes,
-    against the fp32 matmul of the dequantized operands (computed on the GPU
-    in fp32 for time)."""
+    activations bf16 N(0, 1) quantized per token per 128 columns, weights
+    N(0, 0.02) per 128 x 128 block, against the fp32 matmul of the
+    dequantized operands (computed on the GPU in fp32 for time)."""
     m = 8192
     g = torch.Generator(device=DEV).manual_seed(k + n)
-    a = torch.randn(m, k, generator=g, device=DEV)
+    a = torch.randn(m, k, generator=g, device=DEV).to(torch.bfloat16).float()
     q, s = ofp8.group_quant(a)
     w = torch.randn(n, k, generator=g, device=DEV) * 0.02
     wq, ws = ofp8.quantize_weight_blocks(w)
@@ -333,12 +338,16 @@ def test_qk_norm_rope(hq, hk, d, cache_dtype):
     _bf16_close(k, k_ref, min_ulp1=0.998)
 
 
+V_DTYPES = [torch.bfloat16, torch.float16]
+
+
 @pytest.mark.parametrize("hq,hk,d", [(4, 2, 64), (32, 8, 128)])
 @pytest.mark.parametrize("cache_dtype", [torch.bfloat16, torch.float32])
-def test_qk_norm_rope_kv_equals_norm_rope_then_scatter(hq, hk, d, cache_dtype):
-    """The fused pass writes q, and K / fp16 V into pool rows dst[i], bit
-    for bit as qk_norm_rope followed by kv_row_scatter(src = 0..n-1);
-    dst < 0 rows write nothing."""
+@pytest.mark.parametrize("v_dtype", V_DTYPES)
+def test_qk_norm_rope_kv_equals_norm_rope_then_scatter(hq, hk, d, cache_dtype, v_dtype):
+    """The fused pass writes q, and K / V into pool rows dst[i], bit for bit
+    as qk_norm_rope followed by kv_row_scatter(src = 0..n-1); dst < 0 rows
+    write nothing."""
     n, pool_rows = 93, 320
     g = _gen(7 * hq + d)
     qkv = (torch.randn(n, (hq + 2 * hk) * d, generator=g) * 3).to(torch.bfloat16).to(DEV)
@@ -354,7 +363,7 @@ def test_qk_norm_rope_kv_equals_norm_rope_then_scatter(hq, hk, d, cache_dtype):
     pools = []
     for _ in range(2):
         kp = torch.full((pool_rows, hk, d), 7.0, dtype=torch.bfloat16, device=DEV)
-        vp = torch.full((pool_rows, hk, d), 7.0, dtype=torch.float16, device=DEV)
+        vp = torch.full((pool_rows, hk, d), 7.0, dtype=v_dtype, device=DEV)
         pools.append((kp, vp))
     sep = _engine(hq, hk, d, arena=_Arena(*pools[0], 16), cache=cache)
     q_ref, k = sep.qk_norm_rope(qkv, pos, attn)
@@ -370,8 +379,9 @@ def test_qk_norm_rope_kv_equals_norm_rope_then_scatter(hq, hk, d, cache_dtype):
     assert int((pools[1][0].view(pool_rows, -1) != 7.0).all(1).sum()) == n - 3
 
 
-def test_qk_norm_rope_rows_with_pages_equals_norm_rope_then_scatters():
-    """The tree path's pass: q, contiguous K and fp16 V rows, and the same
+@pytest.mark.parametrize("v_dtype", V_DTYPES)
+def test_qk_norm_rope_rows_with_pages_equals_norm_rope_then_scatters(v_dtype):
+    """The tree path's pass: q, contiguous K and V rows, and the same
     K/V into pool rows row_pool_dst[i] (none when negative), bit for bit as
     qk_norm_rope, then the identity and the page scatters."""
     hq, hk, d, n, pool_rows = 32, 8, 128, 70, 256
@@ -387,10 +397,10 @@ def test_qk_norm_rope_rows_with_pages_equals_norm_rope_then_scatters():
     dst = torch.randperm(pool_rows, generator=g)[:n].to(DEV)
     dst[::3] = -1
     pools = [(torch.zeros(pool_rows, hk, d, dtype=torch.bfloat16, device=DEV),
-              torch.zeros(pool_rows, hk, d, dtype=torch.float16, device=DEV)) for _ in range(2)]
+              torch.zeros(pool_rows, hk, d, dtype=v_dtype, device=DEV)) for _ in range(2)]
     sep = _engine(hq, hk, d, arena=_Arena(*pools[0], 16), cache=cache)
     q_ref, k_ref = sep.qk_norm_rope(qkv, pos, attn)
-    v_ref = qkv[:, (hq + hk) * d:].float().half()
+    v_ref = qkv[:, (hq + hk) * d:].to(v_dtype)
     keep = dst >= 0
     sep.kv_row_scatter(k_ref, qkv[:, (hq + hk) * d:], torch.arange(n, device=DEV)[keep],
                        dst[keep], 0)
@@ -413,14 +423,18 @@ class _Arena:
         return self.kp, self.vp
 
 
-def test_kv_scatter_is_bit_exact_and_skips_negative_rows():
+@pytest.mark.parametrize("v_dtype", V_DTYPES)
+def test_kv_scatter_is_bit_exact_and_skips_negative_rows(v_dtype):
+    """bf16 V pools take the rows as they are; fp16 V pools take them
+    rounded to nearest even (as torch converts) and saturated at +-65504
+    (torch would give inf), values below fp16's range flush as torch's do."""
     g = _gen(2)
     n, hk, d = 50, 8, 128
     qkv = torch.randn(n, 48 * 128, generator=g).to(torch.bfloat16).to(DEV)
     k = torch.randn(n, hk * d, generator=g).to(torch.bfloat16).to(DEV)
     v = qkv[:, 40 * 128:]                         # strided v slice of qkv
     kp = torch.zeros(256, hk, d, dtype=torch.bfloat16, device=DEV)
-    vp = torch.zeros(256, hk, d, dtype=torch.float16, device=DEV)   # V pages are fp16
+    vp = torch.zeros(256, hk, d, dtype=v_dtype, device=DEV)
     src = torch.arange(n, device=DEV)
     dst = torch.randperm(256, generator=g)[:n].to(DEV)
     dst[5] = -1
@@ -428,11 +442,23 @@ def test_kv_scatter_is_bit_exact_and_skips_negative_rows():
     eng.kv_row_scatter(k, v, src, dst, 0)
     ok = dst >= 0
     assert torch.equal(kp[dst[ok]], k.view(n, hk, d)[ok])
-    # bf16 -> fp16 round to nearest even, as torch converts
-    assert torch.equal(vp[dst[ok]], v.reshape(n, hk, d)[ok].float().half())
+    assert torch.equal(vp[dst[ok]], v.reshape(n, hk, d)[ok].to(v_dtype))
     written = torch.zeros(256, dtype=torch.bool, device=DEV)
     written[dst[ok]] = True
     assert torch.all(kp[~written] == 0)
+    # values past fp16's range, below it, and of both signs
+    big = torch.full((1, hk * d), 3.0e38, dtype=torch.bfloat16, device=DEV)
+    big[0, ::2] = 1.0e-30
+    big[0, 1::4] = -7.0e4
+    eng.kv_row_scatter(big, big, torch.zeros(1, dtype=torch.long, device=DEV),
+                       torch.full((1,), 3, dtype=torch.long, device=DEV), 0)
+    assert torch.equal(kp[3].reshape(1, -1), big)
+    if v_dtype == torch.bfloat16:
+        assert torch.equal(vp[3].reshape(1, -1), big)
+    else:
+        want = big.float().clamp(-65504, 65504).half()
+        assert torch.equal(vp[3].reshape(1, -1), want)
+        assert bool(torch.isfinite(vp[3]).all())
 
 
 def _paged_case(seed, hq, hk, d, page, seqs, pool_pages):
@@ -459,12 +485,13 @@ def _paged_case(seed, hq, hk, d, page, seqs, pool_pages):
 
 
 @pytest.mark.parametrize("hq,hk,d", [(4, 2, 64), (32, 8, 128), (64, 8, 128), (8, 8, 128)])
-def test_paged_attention_matches_exact_fp32(hq, hk, d):
+@pytest.mark.parametrize("v_dtype", V_DTYPES)
+def test_paged_attention_matches_exact_fp32(hq, hk, d, v_dtype):
     page = 16
     q, kp, vp, cu, used, table = _paged_case(hq + d, hq, hk, d, page, 6, 160)
     want = ref.paged_attention(q, kp, vp, cu, used, table, page)
-    # the engine's V pages hold fp16 (what qx_kv_scatter writes); the oracle reads bf16 V
-    eng = _engine(hq, hk, d, arena=_Arena(kp.to(DEV), vp.float().half().to(DEV), page))
+    # an fp16 V pool holds the bf16 values converted (exact at these magnitudes)
+    eng = _engine(hq, hk, d, arena=_Arena(kp.to(DEV), vp.to(v_dtype).to(DEV), page))
     meta = dict(unified=dict(cu_q=torch.tensor(cu, device=DEV),
                              used=torch.tensor(used, device=DEV),
                              table=torch.tensor(table, device=DEV),

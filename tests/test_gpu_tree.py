@@ -6,7 +6,7 @@ the reference's merge_attn_quant (attention.py:902-948), and whole packs
 in tree mode against the oracle and against the unified path.
 
 Tolerances: attention outputs are bf16 (one rounding, 2^-8 relative) and
-the PV product runs with fp16 probabilities, so outputs are compared at
+the PV product runs with bf16 probabilities, so outputs are compared at
 2e-2 absolute on O(1) values and log-sum-exps at 1e-3. The merge is the
 reference's sequence of fp32 operations with its two bf16 roundings; the
 kernel fuses a + (b - a) * w into one FMA, which moves a value across a
@@ -60,11 +60,12 @@ def _lse_call(q, q_ld, q_index, k, v, cu_q, used, table, cu_k, seqs, max_q, max_
     _lib.call("qx_attention_lse", _p(q), q_ld, _p(q_index), _p(k), _p(v), _p(cu_q), _p(used),
               _p(table), table.stride(0) if table is not None else 0, _p(cu_k), seqs, max_q,
               max_used, hq, hk, d, float(d ** -0.5), int(causal), _p(out), out.stride(0),
-              _p(lse), lse.stride(0), None, 0, _stream())
+              _p(lse), lse.stride(0), None, 0, int(v.dtype == torch.bfloat16), _stream())
 
 
 @pytest.mark.parametrize("hq,hk,d", [(32, 8, 128), (4, 2, 64)])
-def test_segments_call_matches_float32(hq, hk, d):
+@pytest.mark.parametrize("v_dtype", [torch.bfloat16, torch.float16])
+def test_segments_call_matches_float32(hq, hk, d, v_dtype):
     """Call A: causal over contiguous rows in cu_k segments (a zero-length one,
     one shorter than a KV tile, several tiles long)."""
     g = torch.Generator(device=DEV).manual_seed(hq + d)
@@ -73,7 +74,7 @@ def test_segments_call_matches_float32(hq, hk, d):
     n = int(cu[-1])
     q = torch.randn(n, hq * d, generator=g, device=DEV).to(torch.bfloat16)
     k = torch.randn(n, hk * d, generator=g, device=DEV).to(torch.bfloat16)
-    v = torch.randn(n, hk * d, generator=g, device=DEV).to(torch.float16)
+    v = torch.randn(n, hk * d, generator=g, device=DEV).to(v_dtype)
     cu_t = torch.tensor(cu, device=DEV)
     used = torch.tensor(lengths, dtype=torch.int32, device=DEV)
     out = torch.full((n, hq * d), float("nan"), dtype=torch.bfloat16, device=DEV)
@@ -98,7 +99,7 @@ def test_page_reads_with_row_index_match_float32():
     g = torch.Generator(device=DEV).manual_seed(7)
     pages = 64
     kp = torch.randn(pages * page, hk * d, generator=g, device=DEV).to(torch.bfloat16)
-    vp = torch.randn(pages * page, hk * d, generator=g, device=DEV).to(torch.float16)
+    vp = torch.randn(pages * page, hk * d, generator=g, device=DEV).to(torch.bfloat16)
     n = 200
     q = torch.randn(n, hq * d, generator=g, device=DEV).to(torch.bfloat16)
     rng = np.random.default_rng(3)

@@ -28,7 +28,7 @@ def test_argument_errors_return_minus_one_with_a_message():
                   None)
     with pytest.raises(_lib.QxError, match="head_dim"):
         _lib.call("qx_paged_attention", 16, 8, 16, 16, 16, 16, 16, 1, 1, 1, 64, 4, 2, 96, 16,
-                  0.1, 1, 16, None, 8, None, 0, None, 0, None)
+                  0.1, 1, 16, None, 8, None, 0, None, 0, 1, None)
     with pytest.raises(_lib.QxError, match="1..16"):
         _lib.call("qx_answer_head", 16, 8, 16, 8, 17, 1, 8, 0, None, 1.0, None, None, None,
                   None, None)
@@ -57,7 +57,7 @@ def test_attention_work_list_is_heaviest_first_and_covers_every_tile():
 def test_gemm_config_choice_by_shape(monkeypatch):
     """Persistent config 22 where 256 x 256 tiles fill whole waves of the 256
     CUs (and K has an even number of 128-blocks), config 10 on a partial
-    last wave, config 5 for widths not a multiple of 256; the environment
+    last wave, config 11 for widths not a multiple of 256; the environment
     variable forces one."""
     from quail_amd.engine import GEMM_CONFIG_ENV, gemm_config
     monkeypatch.delenv(GEMM_CONFIG_ENV, raising=False)
@@ -67,9 +67,9 @@ def test_gemm_config_choice_by_shape(monkeypatch):
     assert gemm_config(6144, 2560, 12000) == 10     # 1128 tiles
     assert gemm_config(6144, 2688, 16294) == 10     # 21 K-blocks
     assert gemm_config(6144, 2560, 256) == 10       # fewer tiles than CUs
-    assert gemm_config(2688, 2560, 16294) == 5
-    monkeypatch.setenv(GEMM_CONFIG_ENV, "14")
-    assert gemm_config(6144, 2560, 16294) == 14
+    assert gemm_config(2688, 2560, 16294) == 11
+    monkeypatch.setenv(GEMM_CONFIG_ENV, "11")
+    assert gemm_config(6144, 2560, 16294) == 11
 
 
 def test_swiglu_config_choice_by_shape(monkeypatch):
