@@ -184,6 +184,25 @@ int qx_vocab_logprobs(const void* normed, int64_t n_ld, const void* head, int64_
                       hipStream_t stream);
 
 /*
+ * qx_vocab_logprobs without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc). No counterpart in the reference.
+ * The same kernels, the same results bit for bit, over a workspace of the
+ * library's own: one file-scope device array per GPU of
+ * qx_vocab_logprobs_noalloc_max_bytes() bytes (8 MiB), held until the
+ * process ends; its device address is looked up once per device with
+ * hipGetSymbolAddress. Calls whose qx_vocab_logprobs_workspace(n, V, t)
+ * exceeds it are rejected (-1 and a message). It allocates nothing and
+ * needs nothing cleared (every workspace byte is written before it is
+ * read). Every call on one GPU shares that GPU's array: calls that overlap
+ * on one GPU (several streams, several threads) race.
+ */
+int64_t qx_vocab_logprobs_noalloc_max_bytes(void);
+int qx_vocab_logprobs_noalloc(const void* normed, int64_t n_ld, const void* head, int64_t h_ld,
+                              const int64_t* targets, int64_t t, float* out, int64_t out_ld,
+                              int64_t n, int64_t V, int64_t H, hipStream_t stream);
+
+/*
  * Per-token 128-group e4m3 quant of bf16 rows. Replaces Engine.quant ->
  * vLLM per_token_group_quant_fp8 (attention.py:517-532).
  */

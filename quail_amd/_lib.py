@@ -41,6 +41,8 @@ SIGNATURES = {
     "qx_vocab_logprobs_workspace": [_i64, _i64, _i64],
     "qx_vocab_logprobs": [_p, _i64, _p, _i64, _p, _i64, _p, _i64, _i64, _i64, _i64, _p, _i64,
                           _p],
+    "qx_vocab_logprobs_noalloc_max_bytes": [],
+    "qx_vocab_logprobs_noalloc": [_p, _i64, _p, _i64, _p, _i64, _p, _i64, _i64, _i64, _i64, _p],
     "qx_group_quant": [_p, _i64, _p, _i64, _p, _i64, _i64, _i64, _p],
     "qx_kv_scatter": [_p, _i64, _p, _i64, _p, _p, _p, _p, _i64, _i64, _i32, _p],
     "qx_embed": [_p, _i64, _p, _p, _i64, _i64, _i64, _p],
@@ -78,7 +80,8 @@ SIGNATURES = {
 
 
 # entry points returning a count (>= 0) or -1 instead of a status
-RETURNS_COUNT = {"qx_paged_attention_work", "qx_vocab_logprobs_workspace"}
+RETURNS_COUNT = {"qx_paged_attention_work", "qx_vocab_logprobs_workspace",
+                 "qx_vocab_logprobs_noalloc_max_bytes"}
 
 
 class QxUnavailable(RuntimeError):

@@ -18,6 +18,8 @@
 //     into the logsumexp and subtracts it from the target logits.
 // The head (V x H bf16, 778 MB for Qwen3) is read once per 128 tokens, so a
 // launch over a pack's final rows is bound by streaming it from HBM.
+#include <mutex>
+
 #include "qx_common.h"
 #include "qx_status.h"
 
@@ -218,6 +220,90 @@ int64_t workspace_bytes(int64_t n, int64_t V, int64_t t) {
 }  // namespace
 }  // namespace qx
 
+namespace qx {
+namespace {
+
+// Both entry points: argument checks, then the two launches over `workspace`
+// (workspace_bytes(n, V, t) bytes, every byte written before it is read).
+int vocab_run(const void* normed, int64_t n_ld, const void* head, int64_t h_ld,
+              const int64_t* targets, int64_t t, float* out, int64_t out_ld, int64_t n, int64_t V,
+              int64_t H, void* workspace, int64_t workspace_size, hipStream_t stream) {
+  QX_CHECK(normed && head && targets && out && workspace, "vocab_logprobs: null pointer");
+  QX_CHECK(t >= 1 && t <= kMaxTargets, "vocab_logprobs: %lld targets (1..16)", (long long)t);
+  QX_CHECK(H > 0 && H % 64 == 0, "vocab_logprobs: hidden %lld not a multiple of 64",
+           (long long)H);
+  QX_CHECK(V >= 1 && V < (1LL << 31) && n >= 0 && n < (1LL << 31), "vocab_logprobs: sizes");
+  QX_CHECK(n_ld >= H && h_ld >= H && n_ld % 8 == 0 && h_ld % 8 == 0 && out_ld >= t,
+           "vocab_logprobs: strides");
+  QX_CHECK(((uintptr_t)normed & 15) == 0 && ((uintptr_t)head & 15) == 0 &&
+               ((uintptr_t)workspace & 15) == 0,
+           "vocab_logprobs: alignment");
+  QX_CHECK(workspace_size >= workspace_bytes(n, V, t), "vocab_logprobs: workspace of %lld "
+           "bytes, needs %lld", (long long)workspace_size, (long long)workspace_bytes(n, V, t));
+  if (n == 0) return QX_OK;
+  const int rows = block_rows(n);
+  const int nblk = (int)((V + rows - 1) / rows);
+  float2* part = reinterpret_cast<float2*>(workspace);
+  float* tlogit = reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) +
+                                           (int64_t)nblk * n * sizeof(float2));
+  const int tm = n <= 32 ? 1 : n <= 64 ? 2 : 4;
+  const dim3 grid(nblk, (unsigned)((n + 32 * tm - 1) / (32 * tm)));
+  const auto* xp = reinterpret_cast<const uint16_t*>(normed);
+  const auto* hp = reinterpret_cast<const uint16_t*>(head);
+  if (tm == 1) {
+    hipLaunchKernelGGL(vocab_lse_kernel<1>, grid, dim3(256), 0, stream, xp, n_ld, hp, h_ld,
+                       targets, (int)t, part, tlogit, (int)n, (int)V, (int)H);
+  } else if (tm == 2) {
+    hipLaunchKernelGGL(vocab_lse_kernel<2>, grid, dim3(256), 0, stream, xp, n_ld, hp, h_ld,
+                       targets, (int)t, part, tlogit, (int)n, (int)V, (int)H);
+  } else {
+    hipLaunchKernelGGL(vocab_lse_kernel<4>, grid, dim3(256), 0, stream, xp, n_ld, hp, h_ld,
+                       targets, (int)t, part, tlogit, (int)n, (int)V, (int)H);
+  }
+  {
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return (int)e;
+  }
+  hipLaunchKernelGGL(vocab_finish_kernel, dim3((unsigned)n), dim3(64), 0, stream, part, nblk,
+                     tlogit, (int)t, out, out_ld, (int)n);
+  QX_LAUNCH_STATUS();
+}
+
+// The allocation-free entry point's workspace: one array per GPU, held until
+// the process ends. In host code `scratch` names a host-side stand-in, not a
+// device address: its address on each device comes from hipGetSymbolAddress,
+// taken once per device with that device current.
+constexpr int64_t kScratchBytes = 8 << 20;
+constexpr int kMaxDevices = 64;
+__device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+std::mutex scratch_mutex;
+void* scratch_ptr[kMaxDevices] = {};
+
+// this device's address of `scratch` (nullptr and the error text on failure)
+void* scratch_on_current_device() {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    set_error("vocab_logprobs_noalloc: no current device (or device id %d >= %d)", dev,
+              kMaxDevices);
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(scratch_mutex);
+  if (!scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr) {
+      set_error("vocab_logprobs_noalloc: hipGetSymbolAddress: %s", hipGetErrorString(e));
+      return nullptr;
+    }
+    scratch_ptr[dev] = ptr;
+  }
+  return scratch_ptr[dev];
+}
+
+}  // namespace
+}  // namespace qx
+
 extern "C" {
 
 int64_t qx_vocab_logprobs_workspace(int64_t n, int64_t V, int64_t t) {
@@ -229,45 +315,25 @@ int qx_vocab_logprobs(const void* normed, int64_t n_ld, const void* head, int64_
                       const int64_t* targets, int64_t t, float* out, int64_t out_ld, int64_t n,
                       int64_t V, int64_t H, void* workspace, int64_t workspace_bytes,
                       hipStream_t stream) {
-  QX_CHECK(normed && head && targets && out && workspace, "vocab_logprobs: null pointer");
-  QX_CHECK(t >= 1 && t <= qx::kMaxTargets, "vocab_logprobs: %lld targets (1..16)", (long long)t);
-  QX_CHECK(H > 0 && H % 64 == 0, "vocab_logprobs: hidden %lld not a multiple of 64",
-           (long long)H);
-  QX_CHECK(V >= 1 && V < (1LL << 31) && n >= 0 && n < (1LL << 31), "vocab_logprobs: sizes");
-  QX_CHECK(n_ld >= H && h_ld >= H && n_ld % 8 == 0 && h_ld % 8 == 0 && out_ld >= t,
-           "vocab_logprobs: strides");
-  QX_CHECK(((uintptr_t)normed & 15) == 0 && ((uintptr_t)head & 15) == 0 &&
-               ((uintptr_t)workspace & 15) == 0,
-           "vocab_logprobs: alignment");
-  QX_CHECK(workspace_bytes >= qx::workspace_bytes(n, V, t), "vocab_logprobs: workspace of %lld "
-           "bytes, needs %lld", (long long)workspace_bytes, (long long)qx::workspace_bytes(n, V, t));
-  if (n == 0) return QX_OK;
-  const int rows = qx::block_rows(n);
-  const int nblk = (int)((V + rows - 1) / rows);
-  float2* part = reinterpret_cast<float2*>(workspace);
-  float* tlogit = reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) +
-                                           (int64_t)nblk * n * sizeof(float2));
-  const int tm = n <= 32 ? 1 : n <= 64 ? 2 : 4;
-  const dim3 grid(nblk, (unsigned)((n + 32 * tm - 1) / (32 * tm)));
-  const auto* xp = reinterpret_cast<const uint16_t*>(normed);
-  const auto* hp = reinterpret_cast<const uint16_t*>(head);
-  if (tm == 1) {
-    hipLaunchKernelGGL(qx::vocab_lse_kernel<1>, grid, dim3(256), 0, stream, xp, n_ld, hp, h_ld,
-                       targets, (int)t, part, tlogit, (int)n, (int)V, (int)H);
-  } else if (tm == 2) {
-    hipLaunchKernelGGL(qx::vocab_lse_kernel<2>, grid, dim3(256), 0, stream, xp, n_ld, hp, h_ld,
-                       targets, (int)t, part, tlogit, (int)n, (int)V, (int)H);
-  } else {
-    hipLaunchKernelGGL(qx::vocab_lse_kernel<4>, grid, dim3(256), 0, stream, xp, n_ld, hp, h_ld,
-                       targets, (int)t, part, tlogit, (int)n, (int)V, (int)H);
-  }
-  {
-    const hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return (int)e;
-  }
-  hipLaunchKernelGGL(qx::vocab_finish_kernel, dim3((unsigned)n), dim3(64), 0, stream, part, nblk,
-                     tlogit, (int)t, out, out_ld, (int)n);
-  QX_LAUNCH_STATUS();
+  return qx::vocab_run(normed, n_ld, head, h_ld, targets, t, out, out_ld, n, V, H, workspace,
+                       workspace_bytes, stream);
+}
+
+int64_t qx_vocab_logprobs_noalloc_max_bytes(void) { return qx::kScratchBytes; }
+
+int qx_vocab_logprobs_noalloc(const void* normed, int64_t n_ld, const void* head, int64_t h_ld,
+                              const int64_t* targets, int64_t t, float* out, int64_t out_ld,
+                              int64_t n, int64_t V, int64_t H, hipStream_t stream) {
+  QX_CHECK(n >= 0 && V >= 1 && t >= 1, "vocab_logprobs_noalloc: sizes");
+  const int64_t need = qx::workspace_bytes(n, V, t);
+  QX_CHECK(need <= qx::kScratchBytes, "vocab_logprobs_noalloc: %lld rows x %lld vocabulary "
+           "need %lld bytes of workspace, more than its %lld (call qx_vocab_logprobs with a "
+           "workspace, or fewer rows per call)", (long long)n, (long long)V, (long long)need,
+           (long long)qx::kScratchBytes);
+  void* ws = qx::scratch_on_current_device();
+  if (!ws) return QX_EINVAL;
+  return qx::vocab_run(normed, n_ld, head, h_ld, targets, t, out, out_ld, n, V, H, ws,
+                       qx::kScratchBytes, stream);
 }
 
 }  // extern "C"
