@@ -1,7 +1,8 @@
-"""The torch "dequantized path" of the Qwen3 FP8 prefill pass, on CPU.
+"""The torch "dequantized path" of the Qwen3 FP8 prefill pass.
 
 Test infrastructure (see oracle/__init__.py). It restates, in plain torch on
-the CPU, the arithmetic of the reference path:
+the CPU (or on a GPU, as the checker of full-size models: every tensor it
+makes follows its inputs' device), the arithmetic of the reference path:
 
   layer loop and final rows        quail/backends/quail/executor/models/qwen3.py:45-68, 120-135
   norm_quant (layer 0, vLLM)       attention.py:1237-1240 -> rms_norm :539-556 + quant :517-532
@@ -39,11 +40,20 @@ from oracle.fp8 import dequant_rows, dequant_weight, group_quant
 # each point where the reference stores bf16); the timed CPU baseline uses
 # float32, the reference torch path's own type.
 ACCUM = torch.float64
+# keep each layer's dequantized weights (CPU runs); False dequantizes them at
+# every use, for checks on the GPU at model sizes whose fp32 weights would
+# not fit
+CACHE_WEIGHTS = True
 
 
 def set_precision(dtype) -> None:
     global ACCUM
     ACCUM = dtype
+
+
+def set_weight_cache(enabled: bool) -> None:
+    global CACHE_WEIGHTS
+    CACHE_WEIGHTS = enabled
 
 
 @dataclass
@@ -52,6 +62,8 @@ class RefLinear:
     scale_inv: torch.Tensor     # (N/128, K/128) fp32
 
     def dequant(self) -> torch.Tensor:
+        if not CACHE_WEIGHTS:
+            return dequant_weight(self.weight, self.scale_inv).to(ACCUM)
         cache = self.__dict__.setdefault("_w", {})
         if ACCUM not in cache:
             cache[ACCUM] = dequant_weight(self.weight, self.scale_inv).to(ACCUM)
@@ -169,21 +181,23 @@ def paged_attention(q3, k_pool, v_pool, cu_q, used, table, page, causal=True, sc
     kv_heads = k_pool.shape[1]
     group = heads // kv_heads
     scale = dim ** -0.5 if scale is None else scale
-    out = torch.zeros((n, heads, dim), dtype=ACCUM)
+    dev = q3.device
+    out = torch.zeros((n, heads, dim), dtype=ACCUM, device=dev)
     for s in range(len(used)):
         r0, r1 = int(cu_q[s]), int(cu_q[s + 1])
         q_len, seen = r1 - r0, int(used[s])
         if q_len == 0:
             continue
         pages = [int(p) for p in table[s][: -(-seen // page)]]
-        rows = torch.tensor([p * page + j for p in pages for j in range(page)])[:seen]
+        rows = torch.tensor([p * page + j for p in pages for j in range(page)],
+                            device=k_pool.device)[:seen]
         k = k_pool[rows].to(ACCUM).repeat_interleave(group, dim=1)   # (seen, H, D)
         v = v_pool[rows].to(ACCUM).repeat_interleave(group, dim=1)
         qs = q3[r0:r1].to(ACCUM)                                     # (q_len, H, D)
         scores = torch.einsum("qhd,khd->hqk", qs, k) * scale
         if causal:
-            qi = torch.arange(q_len)[:, None]
-            kj = torch.arange(seen)[None, :]
+            qi = torch.arange(q_len, device=dev)[:, None]
+            kj = torch.arange(seen, device=dev)[None, :]
             mask = kj < (seen - q_len + qi + 1)
             scores = scores.masked_fill(~mask[None], float("-inf"))
         w = scores.softmax(-1)
@@ -196,14 +210,14 @@ def varlen_attention(q3, k3, v3, cu):
     unpaged branch of attention_unified (attention.py:1517-1534)."""
     n, heads, dim = q3.shape
     group = heads // k3.shape[1]
-    out = torch.zeros((n, heads, dim), dtype=ACCUM)
+    out = torch.zeros((n, heads, dim), dtype=ACCUM, device=q3.device)
     for s in range(len(cu) - 1):
         r0, r1 = int(cu[s]), int(cu[s + 1])
         L = r1 - r0
         k = k3[r0:r1].to(ACCUM).repeat_interleave(group, dim=1)
         v = v3[r0:r1].to(ACCUM).repeat_interleave(group, dim=1)
         scores = torch.einsum("qhd,khd->hqk", q3[r0:r1].to(ACCUM), k) * dim ** -0.5
-        mask = torch.tril(torch.ones(L, L, dtype=torch.bool))
+        mask = torch.tril(torch.ones(L, L, dtype=torch.bool, device=q3.device))
         scores = scores.masked_fill(~mask[None], float("-inf"))
         out[r0:r1] = torch.einsum("hqk,khd->qhd", scores.softmax(-1), v)
     return out.to(torch.bfloat16)
@@ -281,8 +295,9 @@ def forward_documents(m: RefModel, documents, layers=None):
     the same rows."""
     hq, hk, d = m.num_heads, m.num_kv_heads, m.head_dim
     lengths = [len(doc) for doc in documents]
-    ids = torch.tensor([t for doc in documents for t in doc], dtype=torch.long)
-    positions = torch.cat([torch.arange(L) for L in lengths])
+    dev = m.embed.device
+    ids = torch.tensor([int(t) for doc in documents for t in doc], dtype=torch.long, device=dev)
+    positions = torch.cat([torch.arange(L, device=dev) for L in lengths])
     cu = [0]
     for L in lengths:
         cu.append(cu[-1] + L)
@@ -294,7 +309,7 @@ def forward_documents(m: RefModel, documents, layers=None):
         q, k, v, residual = _layer_front(m, layer, hidden, residual, positions)
         attn = varlen_attention(q.view(n, hq, d), k.view(n, hk, d), v.reshape(n, hk, d), cu)
         hidden, residual = _layer_back(m, layer, attn.view(n, hq * d), residual)
-    final = torch.tensor([c - 1 for c in cu[1:]], dtype=torch.long)
+    final = torch.tensor([c - 1 for c in cu[1:]], dtype=torch.long, device=dev)
     normed, _ = fused_add_rms_norm(hidden[final], residual[final], m.norm, m.eps)
     return normed
 

@@ -5,10 +5,11 @@ import torch
 from oracle import qwen3_ref as ref
 
 
-def ref_model(model) -> ref.RefModel:
-    """The oracle's CPU copy of a model built by quail_amd.model."""
+def ref_model(model, device="cpu") -> ref.RefModel:
+    """The oracle's copy of a model built by quail_amd.model (on the CPU, or
+    on `device` for checks at model sizes the CPU would take too long on)."""
     inner = model.model
-    cpu = lambda t: t.detach().to("cpu")
+    cpu = lambda t: t.detach().to(device)
     layers = []
     for layer in inner.layers:
         a, m = layer.self_attn, layer.mlp
