@@ -44,6 +44,12 @@ def config_from_json(config: dict, name: str = "checkpoint") -> Qwen3Config:
                          f"dynamic activation scales, got quantization_config={quant}")
     if config.get("rope_scaling"):
         raise ValueError(f"{name}: rope_scaling {config['rope_scaling']} is not supported")
+    # transformers 5 writes the rotary settings as rope_parameters
+    # {"rope_type", "rope_theta", ...} instead of a top-level rope_theta
+    rope = config.get("rope_parameters") or {}
+    if rope.get("rope_type", "default") != "default":
+        raise ValueError(f"{name}: rope_parameters {rope} is not supported (only default rope)")
+    theta = config.get("rope_theta", rope.get("rope_theta"))
     if config.get("use_sliding_window"):
         raise ValueError(f"{name}: sliding-window attention is not supported")
     if config.get("attention_bias"):
@@ -62,7 +68,7 @@ def config_from_json(config: dict, name: str = "checkpoint") -> Qwen3Config:
         intermediate=int(config["intermediate_size"]),
         vocab=int(config["vocab_size"]),
         eps=float(config.get("rms_norm_eps", 1e-6)),
-        theta=float(config.get("rope_theta", 10000.0)),
+        theta=float(10000.0 if theta is None else theta),
         max_positions=int(config.get("max_position_embeddings", 40960)),
         tied_head=bool(config.get("tie_word_embeddings", False)),
     )

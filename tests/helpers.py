@@ -134,6 +134,55 @@ def write_hf_checkpoint(model, cfg, path, shards=2):
     return path
 
 
+def write_transformers_fp8_checkpoint(cfg, path, seed=0, shard_bytes=400_000):
+    """A Qwen3 FP8 checkpoint written by code independent of this package:
+    transformers' Qwen3ForCausalLM (its own tensor names and random init,
+    norms set to 1 + N(0, 0.1) so that a swapped norm shows), every layer
+    projection quantized to e4m3 in 128x128 blocks by transformers'
+    Fp8Quantize (the fine-grained FP8 format: `weight` and per-block
+    `weight_scale_inv`, the value being weight * scale), the tensors sharded
+    by huggingface_hub.save_torch_state_dict (tied head left out, as
+    save_pretrained does) and config.json written by transformers with a
+    FineGrainedFP8Config. Returns the directory."""
+    import types
+    from pathlib import Path
+
+    from huggingface_hub import save_torch_state_dict
+    from transformers import FineGrainedFP8Config, Qwen3Config, Qwen3ForCausalLM
+    from transformers.integrations.finegrained_fp8 import Fp8Quantize
+
+    path = Path(path)
+    path.mkdir(parents=True, exist_ok=True)
+    hcfg = Qwen3Config(vocab_size=cfg.vocab, hidden_size=cfg.hidden,
+                       intermediate_size=cfg.intermediate, num_hidden_layers=cfg.layers,
+                       num_attention_heads=cfg.heads, num_key_value_heads=cfg.kv_heads,
+                       head_dim=cfg.head_dim, rms_norm_eps=cfg.eps, rope_theta=cfg.theta,
+                       tie_word_embeddings=cfg.tied_head,
+                       max_position_embeddings=cfg.max_positions)
+    torch.manual_seed(seed)
+    model = Qwen3ForCausalLM(hcfg)
+    with torch.no_grad():
+        for name, p in model.named_parameters():
+            if name.endswith("norm.weight"):
+                p.copy_(1 + 0.1 * torch.randn_like(p))
+    model = model.to(torch.bfloat16)
+    qcfg = FineGrainedFP8Config(weight_block_size=(128, 128))
+    quantize = Fp8Quantize(types.SimpleNamespace(quantization_config=qcfg))
+    state = {}
+    for name, t in model.state_dict().items():
+        if cfg.tied_head and name == "lm_head.weight":
+            continue
+        if ".layers." in name and name.endswith("_proj.weight"):
+            state.update(quantize._quantize_one(name, t))
+        else:
+            state[name] = t
+    save_torch_state_dict(state, path, max_shard_size=shard_bytes)
+    model.config.architectures = ["Qwen3ForCausalLM"]
+    model.config.quantization_config = qcfg
+    model.config.save_pretrained(path)
+    return path
+
+
 def exact_contractions(monkeypatch):
     """Replace the engine's two MFMA contractions with exact float64 torch
     computations on the GPU, for decomposition tests only: every FP8 GEMM

@@ -9,7 +9,9 @@ Hugging Face layout (tests/helpers.py: write_hf_checkpoint, split back into
 q/k/v and gate/up over two shards) must load back bit for bit.
 tests/golden/qwen3-4b-fp8.config.json is the reference's own fixture
 (tests/fixtures/qwen3_configs/qwen3-4b-fp8.json, the published
-Qwen/Qwen3-4B-FP8 config.json).
+Qwen/Qwen3-4B-FP8 config.json). A checkpoint written by transformers and
+huggingface_hub (not by this package) must load to what transformers itself
+reads from it.
 """
 
 import dataclasses
@@ -70,6 +72,78 @@ def test_checkpoint_round_trip_is_bit_exact(tmp_path, tied):
     assert _same(loaded.model.norm.weight, model.model.norm.weight)
     assert _same(loaded.lm_head.weight, model.lm_head.weight)
     assert (loaded.lm_head.weight is loaded.model.embed_tokens.weight) == tied
+
+
+@pytest.mark.parametrize("tied", [True, False])
+def test_checkpoint_written_by_transformers(tmp_path, monkeypatch, tied):
+    """A checkpoint written by independent code (transformers' Qwen3 names,
+    its Fp8Quantize block quantization, huggingface_hub sharding, its
+    config.json with rope_parameters and a FineGrainedFP8Config) read by
+    the loader, against transformers' own reading of the same files
+    (from_pretrained without a GPU dequantizes the FP8 weights, value =
+    weight * weight_scale_inv per 128x128 block): every merged projection,
+    norm, embedding and head equal, and the oracle's forward over the
+    loaded model (FP8 activation quantization off, as transformers has
+    none) equal to transformers' forward within the few bf16 ulps of the
+    oracle's storage roundings."""
+    from transformers import Qwen3ForCausalLM
+
+    from oracle import qwen3_ref as ref
+    from oracle.fp8 import dequant_weight
+    from quail_amd.workload import make_workload
+    from tests.helpers import ref_model, write_transformers_fp8_checkpoint
+
+    cfg = dataclasses.replace(CONFIGS["tiny"], tied_head=tied)
+    path = write_transformers_fp8_checkpoint(cfg, tmp_path / "ckpt", seed=3)
+    assert len(list(path.glob("*.safetensors"))) > 1
+    assert read_config(path) == dataclasses.replace(cfg, name="ckpt")
+    loaded = load_qwen3_fp8(path, device="cpu")
+    theirs = Qwen3ForCausalLM.from_pretrained(path, dtype=torch.float32).eval()
+    theirs.config._attn_implementation = "eager"
+    d, hq, hk, inter = cfg.head_dim, cfg.heads, cfg.kv_heads, cfg.intermediate
+    dq = lambda lin: dequant_weight(lin.weight, lin.weight_scale_inv)
+    for mine, th in zip(loaded.model.layers, theirs.model.layers):
+        a, ta = mine.self_attn, th.self_attn
+        assert torch.equal(dq(a.qkv_proj), torch.cat([ta.q_proj.weight, ta.k_proj.weight,
+                                                      ta.v_proj.weight]))
+        assert torch.equal(dq(a.o_proj), ta.o_proj.weight)
+        assert torch.equal(dq(mine.mlp.gate_up_proj),
+                           torch.cat([th.mlp.gate_proj.weight, th.mlp.up_proj.weight]))
+        assert torch.equal(dq(mine.mlp.down_proj), th.mlp.down_proj.weight)
+        for n in ("q_norm", "k_norm"):
+            assert torch.equal(getattr(a, n).weight.float(), getattr(ta, n).weight)
+        for n in ("input_layernorm", "post_attention_layernorm"):
+            assert torch.equal(getattr(mine, n).weight.float(), getattr(th, n).weight)
+        assert a.qkv_proj.weight.shape == ((hq + 2 * hk) * d, cfg.hidden)
+        assert mine.mlp.gate_up_proj.weight.shape == (2 * inter, cfg.hidden)
+    assert torch.equal(loaded.model.embed_tokens.weight.float(), theirs.model.embed_tokens.weight)
+    assert torch.equal(loaded.model.norm.weight.float(), theirs.model.norm.weight)
+    assert torch.equal(loaded.lm_head.weight.float(), theirs.lm_head.weight)
+    docs = make_workload("tiny", seed=3).prompts[:4]
+    monkeypatch.setattr(ref, "group_quant",
+                        lambda y: (y.float(), torch.ones(y.shape[0], y.shape[1] // 128)))
+    got = ref.forward_documents(ref_model(loaded), docs).float()
+    with torch.no_grad():
+        want = torch.stack([theirs.model(input_ids=torch.tensor([list(doc)]))
+                            .last_hidden_state[0, -1] for doc in docs])
+    rel = (got - want).norm(dim=1) / want.norm(dim=1)
+    assert float(rel.max()) <= 0.02, rel
+    head = theirs.lm_head.weight.detach()
+    lg, lw = got @ head.T, want @ head.T
+    assert float((lg - lw).abs().max()) <= 0.02 * float(lw.abs().max()) + 0.01
+
+
+def test_rope_parameters_are_read_and_checked():
+    """transformers 5 writes the rotary base as rope_parameters.rope_theta;
+    a rope_type other than default is refused like rope_scaling."""
+    with open(GOLDEN / "qwen3-4b-fp8.config.json") as f:
+        config = json.load(f)
+    theta = config.pop("rope_theta")
+    config["rope_parameters"] = {"rope_type": "default", "rope_theta": theta}
+    assert config_from_json(config, name="qwen3-4b") == CONFIGS["qwen3-4b"]
+    config["rope_parameters"]["rope_type"] = "yarn"
+    with pytest.raises(ValueError, match="rope_parameters"):
+        config_from_json(config)
 
 
 def test_keeps_the_first_layers(tmp_path):
