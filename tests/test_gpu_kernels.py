@@ -508,6 +508,38 @@ def test_paged_attention_matches_exact_fp32(hq, hk, d, v_dtype):
         _fp8_close(o_q, o_s, q_ref, s_ref, min_equal=1.0)
 
 
+@pytest.mark.parametrize("v_dtype", V_DTYPES)
+def test_paged_attention_long_sequences_match_exact_fp32(v_dtype):
+    """Sequences past 4096 keys (more than 64 key tiles: the kernel re-reads
+    its page ids every 64 tiles), with ragged last pages and query tiles, in
+    a shuffled pool: against exact fp32 attention."""
+    hq, hk, d, page = 32, 8, 128, 16
+    rng = np.random.default_rng(41)
+    g = _gen(41)
+    q_lens = np.array([33, 64, 100, 7], dtype=np.int64)
+    used = np.array([4200, 4500, 5003, 8190], dtype=np.int64)
+    cu = np.concatenate([[0], np.cumsum(q_lens)]).astype(np.int32)
+    need = -(-used // page)
+    pool_pages = int(need.sum()) + 5
+    perm = rng.permutation(pool_pages)
+    table = np.zeros((len(used), int(need.max())), dtype=np.int32)
+    at = 0
+    for s_, k_ in enumerate(need):
+        table[s_, :k_] = perm[at:at + k_]
+        at += int(k_)
+    kp = torch.randn(pool_pages * page, hk, d, generator=g).to(torch.bfloat16)
+    vp = torch.randn(pool_pages * page, hk, d, generator=g).to(torch.bfloat16)
+    q = torch.randn(int(cu[-1]), hq, d, generator=g).to(torch.bfloat16)
+    want = ref.paged_attention(q, kp, vp, cu, used.astype(np.int32), table, page)
+    eng = _engine(hq, hk, d, arena=_Arena(kp.to(DEV), vp.to(v_dtype).to(DEV), page))
+    meta = dict(unified=dict(cu_q=torch.tensor(cu, device=DEV),
+                             used=torch.tensor(used.astype(np.int32), device=DEV),
+                             table=torch.tensor(table, device=DEV),
+                             max_q=int(q_lens.max()), max_used=int(used.max()), causal=True))
+    got = eng.attention_bf16(q.to(DEV), meta, 0)
+    torch.testing.assert_close(got.float().cpu().view_as(want), want.float(), rtol=2e-2, atol=2e-2)
+
+
 def test_answer_head_modes():
     g = _gen(13)
     n, h, t = 33, 2560, 6
