@@ -43,6 +43,9 @@ if str(ROOT) not in sys.path:
 METRIC = "AI.IF rows/sec + prefill tok/s, Qwen3-4B FP8, 1 MI355X; % FP8 MFMA peak"
 PEAK_FP8 = 5.0e15        # MI355X dense FP8 MFMA, FLOP/s
 PEAK_BF16 = 2.5e15       # dense bf16 MFMA
+PEAK_CLOCK_GHZ = 2.4     # the clock the dense peaks are quoted at
+XCDS = 8                 # MI355X: 8 XCDs of 32 CUs
+SIMDS = 1024             # 256 CUs x 4 SIMDs
 PEAK_HBM = 8.0e12        # HBM3E bytes/s
 WORKLOAD = "qwen3-4b"
 # HBM bytes per GEMM launch of this workload, from the FETCH_SIZE and
@@ -262,7 +265,7 @@ def summarize(directory: str, copy_mib: int) -> None:
             d = dispatch[(kernel, r["Dispatch_Id"])]
             d[r["Counter_Name"]] = float(r["Counter_Value"])
             d["_ns"] = float(r["End_Timestamp"]) - float(r["Start_Timestamp"])
-        if "MfmaUtil" in per or "SQ_INSTS_MFMA" in per:
+        if "MfmaUtil" in per or "SQ_INSTS_MFMA" in per or "GRBM_GUI_ACTIVE" in per:
             summarize_mfma(dispatch)
             continue
         for counter, kernels in per.items():
@@ -294,6 +297,9 @@ def summarize_mfma(dispatch) -> None:
     groups = defaultdict(list)
     for (kernel, _), d in dispatch.items():
         groups[kernel].append(d)
+    if any("GRBM_GUI_ACTIVE" in d for d in dispatch.values()):
+        summarize_clock(groups)
+        return
     cols = ("MfmaUtil", "VALUBusy", "SQ_INSTS_MFMA", "SQ_INSTS_VALU", "SQ_INSTS_LDS",
             "SQ_LDS_BANK_CONFLICT", "SQ_INSTS_VALU_MFMA_MOPS_F8",
             "SQ_INSTS_VALU_MFMA_MOPS_BF16", "SQ_INSTS_VALU_MFMA_MOPS_F16")
@@ -310,6 +316,33 @@ def summarize_mfma(dispatch) -> None:
         print(f"{len(ds):6d} {ns / 1e3:9.2f} {mean['MfmaUtil']:6.1f} {mean['VALUBusy']:6.1f} "
               f"{ratio:9.2f} {mean['SQ_INSTS_LDS']:10.3g} {mean['SQ_LDS_BANK_CONFLICT']:10.3g} "
               f"{tflops:8.1f}  {kernel}")
+
+
+def summarize_clock(groups) -> None:
+    """Per-kernel means of a clock pass: GRBM_GUI_ACTIVE (busy cycles at the
+    shader clock, summed by rocprofv3 over the 8 XCDs) over the dispatch's
+    duration gives the clock the kernel ran at; SQ_VALU_MFMA_BUSY_CYCLES
+    (summed over the 1024 SIMDs) over those cycles gives the fraction of
+    time the matrix cores were busy, and MOPS x 512 over the duration the
+    achieved TFLOP/s; the clocked peak is the dense peak scaled by the clock
+    over 2.4 GHz."""
+    print(f"{'calls':>6} {'avg us':>9} {'clock GHz':>9} {'MFMA busy':>9} {'TFLOP/s':>8} "
+          f"{'of peak':>7} {'of clocked':>10}  kernel")
+    for kernel, ds in sorted(groups.items(), key=lambda kv: -sum(d["_ns"] for d in kv[1])):
+        ns = sum(d["_ns"] for d in ds) / len(ds)
+        grbm = sum(d.get("GRBM_GUI_ACTIVE", 0.0) for d in ds) / len(ds) / XCDS
+        busy = sum(d.get("SQ_VALU_MFMA_BUSY_CYCLES", 0.0) for d in ds) / len(ds)
+        f8 = sum(d.get("SQ_INSTS_VALU_MFMA_MOPS_F8", 0.0) for d in ds) / len(ds)
+        b16 = sum(d.get("SQ_INSTS_VALU_MFMA_MOPS_BF16", 0.0) + d.get("SQ_INSTS_VALU_MFMA_MOPS_F16", 0.0)
+                  for d in ds) / len(ds)
+        clock = grbm / ns if ns else 0.0
+        mfma = busy / (grbm * SIMDS) if grbm else 0.0
+        tflops = (f8 + b16) * 512 / (ns * 1e-9) / 1e12 if ns else 0.0
+        peak = PEAK_FP8 if f8 >= b16 else PEAK_BF16
+        frac = tflops * 1e12 / peak
+        clocked = frac * PEAK_CLOCK_GHZ / clock if clock else 0.0
+        print(f"{len(ds):6d} {ns / 1e3:9.2f} {clock:9.3f} {mfma:9.1%} {tflops:8.1f} {frac:7.1%} "
+              f"{clocked:10.1%}  {kernel}")
 
 
 def load_traffic():
