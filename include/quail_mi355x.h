@@ -242,26 +242,43 @@ int qx_embed(const void* table, int64_t t_ld, const int64_t* ids, void* out, int
  * FA's max_seqlen_q / max_seqlen_k (max_used <= 2048 * page). With out_fp8 it also
  * performs Engine.quant of the bf16 result (attention.py:1274-1275): e4m3
  * rows plus scales[h*s_ld + row] (one group per head, D == 128).
+ * work/n_work: the work list (below) or NULL/0; tile_rows: the query rows
+ * per workgroup it was built for (0: the default for (HQ / HK, D); 32 is
+ * also accepted for D == 128 with HQ / HK a multiple of 4).
  */
 int qx_paged_attention(const void* q, int64_t q_ld, const void* k_pool, const void* v_pool,
                        const int* cu_q, const int* used, const int* table, int64_t table_ld,
                        int64_t seqs, int64_t max_q, int64_t max_used, int64_t HQ, int64_t HK,
                        int64_t D, int64_t page, float scale, int causal, void* out_bf16,
                        void* out_fp8, int64_t o_ld, float* scales, int64_t s_ld,
-                       const int* work, int64_t n_work, int v_bf16, hipStream_t stream);
+                       const int* work, int64_t n_work, int64_t tile_rows, int v_bf16,
+                       hipStream_t stream);
+
+/*
+ * Host function: the query rows per workgroup (work-list tile height) that a
+ * paged call over these sequences runs best with: 32 where qx_paged_attention
+ * accepts it and the default-height work items read at most 8 64-key tiles
+ * on average (short documents: two 4-wave workgroups per CU hide each
+ * other's fixed cost), else the default. cu_q and used are host copies.
+ * Returns the rows or -1. No reference counterpart (FlashAttention's varlen
+ * grid has one tile height).
+ */
+int64_t qx_paged_attention_tile_rows(const int* cu_q, const int* used, int64_t seqs, int64_t HQ,
+                                     int64_t HK, int64_t D, int causal);
 
 /*
  * Host function: the work list for qx_paged_attention's `work` argument
  * (device copy of it, n_work = the return value): one (sequence, query tile)
- * int pair per query tile that holds rows, in the tile size the call uses for
- * (HQ / HK, D), heaviest first (most keys to read). With work == NULL the
+ * int pair per query tile of tile_rows rows (0: the default for (HQ / HK, D);
+ * the call takes the same tile_rows) that holds rows, heaviest first (most
+ * keys to read). With work == NULL the
  * call launches its full (max_q tiles x seqs) grid instead, whose tiles past
  * a sequence's rows exit at once. cu_q and used are host copies. Returns the
  * item count (<= capacity) or -1. No reference counterpart: FlashAttention's
  * varlen grid is the full one.
  */
 int64_t qx_paged_attention_work(const int* cu_q, const int* used, int64_t seqs, int64_t HQ,
-                                int64_t HK, int64_t D, int causal, int* work,
+                                int64_t HK, int64_t D, int causal, int64_t tile_rows, int* work,
                                 int64_t capacity);
 
 /*
@@ -278,7 +295,8 @@ int64_t qx_paged_attention_work(const int* cu_q, const int* used, int64_t seqs, 
  *     used[s] <= cu_k[s+1] - cu_k[s].
  * q_index (may be NULL): query i reads Q row q_index[i] (the reference's
  * q3.index_select(0, reads["rows"]), without the copy). causal aligns
- * bottom-right as in qx_paged_attention. work/n_work as there.
+ * bottom-right as in qx_paged_attention. work/n_work as there, built for the
+ * default tile height (tile_rows 0).
  */
 int qx_attention_lse(const void* q, int64_t q_ld, const int64_t* q_index, const void* k,
                      const void* v, const int* cu_q, const int* used, const int* table,

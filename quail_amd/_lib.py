@@ -47,8 +47,10 @@ SIGNATURES = {
     "qx_kv_scatter": [_p, _i64, _p, _i64, _p, _p, _p, _p, _i64, _i64, _i32, _p],
     "qx_embed": [_p, _i64, _p, _p, _i64, _i64, _i64, _p],
     "qx_paged_attention": [_p, _i64, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64,
-                           _i64, _i64, _f32, _i32, _p, _p, _i64, _p, _i64, _p, _i64, _i32, _p],
-    "qx_paged_attention_work": [_p, _p, _i64, _i64, _i64, _i64, _i32, _p, _i64],
+                           _i64, _i64, _f32, _i32, _p, _p, _i64, _p, _i64, _p, _i64, _i64, _i32,
+                           _p],
+    "qx_paged_attention_tile_rows": [_p, _p, _i64, _i64, _i64, _i64, _i32],
+    "qx_paged_attention_work": [_p, _p, _i64, _i64, _i64, _i64, _i32, _i64, _p, _i64],
     "qx_attention_lse": [_p, _i64, _p, _p, _p, _p, _p, _p, _i64, _p, _i64, _i64, _i64, _i64,
                          _i64, _i64, _f32, _i32, _p, _i64, _p, _i64, _p, _i64, _i32, _p],
     "qx_merge_attn_quant": [_p, _i64, _p, _i64, _p, _i64, _p, _i64, _p, _i64, _i64, _i64, _p,
@@ -80,7 +82,7 @@ SIGNATURES = {
 
 
 # entry points returning a count (>= 0) or -1 instead of a status
-RETURNS_COUNT = {"qx_paged_attention_work", "qx_vocab_logprobs_workspace",
+RETURNS_COUNT = {"qx_paged_attention_work", "qx_paged_attention_tile_rows", "qx_vocab_logprobs_workspace",
                  "qx_vocab_logprobs_noalloc_max_bytes"}
 
 

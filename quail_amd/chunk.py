@@ -239,7 +239,8 @@ def pack_chunk(arena, groups, *, attention_mode="unified", mask="causal", timing
     if attention_heads is not None:
         for tables in (unified, meta["final_query"]):
             if tables is not None:
-                tables["work"], tables["n_work"] = _work_list(tables, attention_heads)
+                tables["work"], tables["n_work"], tables["work_rows"] = _work_list(
+                    tables, attention_heads, choose_rows=True)
     if timing is not None:
         timing["pack_py"] = timing.get("pack_py", 0.0) + (t1 - t0)
         timing["pack_unified"] = timing.get("pack_unified", 0.0) + (time.perf_counter() - t1)
@@ -456,7 +457,7 @@ def _pack_tree(arena, groups, *, timing=None, attention_heads=None):
     if attention_heads is not None:
         for tables in (segments, reads, reads and reads.get("nodes")):
             if tables:
-                tables["work"], tables["n_work"] = _work_list(tables, attention_heads)
+                tables["work"], tables["n_work"], _ = _work_list(tables, attention_heads)
     ids = _cat(id_parts)
     positions = _cat(pos_parts)
     final = _cat(finals)
@@ -473,18 +474,26 @@ def _pack_tree(arena, groups, *, timing=None, attention_heads=None):
                  host_ids=ids, host_positions=positions)
 
 
-def _work_list(tables, heads):
-    """(work pairs, count) of a paged call over `tables` (host arrays)."""
+def _work_list(tables, heads, choose_rows=False):
+    """(work pairs, count, query rows per item) of a paged call over `tables`
+    (host arrays). choose_rows: the tile height qx_paged_attention_tile_rows
+    picks for these sequences (the call must then pass it); otherwise the
+    default (0)."""
     from quail_amd import _lib
     hq, hk, d = heads
     cu_q = np.ascontiguousarray(tables["cu_q"], dtype=np.int32)
     used = np.ascontiguousarray(tables["used"], dtype=np.int32)
     seqs = len(used)
+    causal = int(tables.get("causal", True))
+    rows = 0
+    if choose_rows:
+        rows = _lib.count("qx_paged_attention_tile_rows", cu_q.ctypes.data, used.ctypes.data,
+                          seqs, hq, hk, d, causal)
     cap = int(cu_q[-1]) + seqs if seqs else 1
     work = np.zeros(2 * max(cap, 1), dtype=np.int32)
     n = _lib.count("qx_paged_attention_work", cu_q.ctypes.data, used.ctypes.data, seqs, hq, hk,
-                   d, int(tables.get("causal", True)), work.ctypes.data, cap)
-    return work[:2 * n], n
+                   d, causal, rows, work.ctypes.data, cap)
+    return work[:2 * n], n, rows
 
 
 def _final_query(cu_q, used, table, final):

@@ -74,8 +74,10 @@ __device__ __forceinline__ int vswz(int key) { return D == 128 ? ((key & 3) << 2
 // bf16); otherwise V holds fp16 and P is rounded to fp16 (11 significant
 // bits against bf16's 8: the closer result, for an arena of this engine's
 // own that stores V in fp16).
+// Registers for two waves per SIMD: one 8-wave workgroup per CU, or two of
+// 4 waves.
 template <int D, int HPB, int QSUB, bool QUANT, bool CONTIG, bool VBF>
-__global__ __launch_bounds__(HPB * QSUB * 64) void paged_attention_kernel(
+__global__ __launch_bounds__(HPB * QSUB * 64, 8 / (HPB * QSUB)) void paged_attention_kernel(
     const uint16_t* __restrict__ q, int64_t q_ld, const int64_t* __restrict__ q_index,
     const uint16_t* __restrict__ kp, const uint16_t* __restrict__ vp,
     const int* __restrict__ cu_q, const int* __restrict__ used, const int* __restrict__ table,
@@ -604,13 +606,24 @@ __global__ __launch_bounds__(256) void merge_attn_quant_kernel(
   if ((lane & 15) == 0) scales[(int64_t)head * s_ld + row] = scale;
 }
 
-// Query rows per workgroup of the configuration dispatched for (D, G):
-// 32 * QSUB with HPB * QSUB = 8 waves.
-inline int attn_query_tile(int64_t D, int64_t G) {
-  (void)D;
-  const int hpb = G % 4 == 0 ? 4 : (G % 2 == 0 ? 2 : 1);
-  return 32 * (8 / hpb);
+// Query heads per workgroup for (G = HQ / HK): the largest of 4, 2, 1
+// dividing G.
+inline int attn_heads_per_group(int64_t G) { return G % 4 == 0 ? 4 : (G % 2 == 0 ? 2 : 1); }
+
+// Query rows per workgroup (work-list tile height) of a call: by default
+// 32 * QSUB with HPB * QSUB = 8 waves, one workgroup per CU; with D = 128 and
+// 4 heads per workgroup also 32 (4 waves, two workgroups per CU, which hide
+// each other's fixed cost on short documents).
+inline int attn_default_rows(int64_t G) { return 32 * (8 / attn_heads_per_group(G)); }
+inline bool attn_rows_ok(int64_t D, int64_t G, int64_t rows) {
+  return rows == attn_default_rows(G) || (D == 128 && attn_heads_per_group(G) == 4 && rows == 32);
 }
+
+// The 32-row tile is chosen when a pack's 64-row work items read at most
+// this many 64-key tiles on average (measured crossover on MI355X: 768-token
+// documents, 7.5 tiles per item, run 1.5% faster with it, 1024-token ones,
+// 9.5 tiles, 1.2% slower).
+constexpr double kShortItemTiles = 8.0;
 
 }  // namespace
 }  // namespace qx
@@ -624,7 +637,7 @@ int attention_impl(const void* q, int64_t q_ld, const int64_t* q_index, const vo
                    int64_t max_used, int64_t HQ, int64_t HK, int64_t D, int64_t page, float scale,
                    int causal, void* out_bf16, void* out_fp8, int64_t o_ld, float* scales,
                    int64_t s_ld, float* lse, int64_t lse_ld, const int* work, int64_t n_work,
-                   int v_bf16, hipStream_t stream) {
+                   int64_t tile_rows, int v_bf16, hipStream_t stream) {
   QX_CHECK(q && k_pool && v_pool && cu_q && used && (table || cu_k), "attention: null pointer");
   QX_CHECK(out_bf16 || out_fp8, "attention: no output");
   QX_CHECK(!(out_fp8 && (cu_k || lse || q_index)), "attention: fused quant is for the paged call");
@@ -638,9 +651,12 @@ int attention_impl(const void* q, int64_t q_ld, const int64_t* q_index, const vo
   QX_CHECK(!out_fp8 || (D == 128 && scales), "attention: fused quant needs D=128 and scales");
   QX_CHECK(seqs < 65536, "attention: %lld sequences exceed the grid", (long long)seqs);
   QX_CHECK(!work || (n_work >= 0 && n_work * HK * 8 < (1LL << 31)), "attention: work items");
-  if (seqs == 0 || max_q == 0 || (work && n_work == 0)) return QX_OK;
   const int G = (int)(HQ / HK);
-  const int hpb = G % 4 == 0 ? 4 : (G % 2 == 0 ? 2 : 1);
+  const int hpb = attn_heads_per_group(G);
+  const int64_t rows = tile_rows ? tile_rows : attn_default_rows(G);
+  QX_CHECK(attn_rows_ok(D, G, rows), "attention: %lld query rows per workgroup (D=%lld, G=%d)",
+           (long long)rows, (long long)D, G);
+  if (seqs == 0 || max_q == 0 || (work && n_work == 0)) return QX_OK;
   const int args_seqs = (int)seqs, args_mq = (int)max_q, args_mu = (int)max_used;
 #define QX_ATTN(DD, HPB_, QS_)                                                                 \
   return launch_attn<DD, HPB_, QS_>(q, q_ld, q_index, k_pool, v_pool, cu_q, used, table,       \
@@ -649,6 +665,7 @@ int attention_impl(const void* q, int64_t q_ld, const int64_t* q_index, const vo
                                     o_ld, scales, s_ld, lse, lse_ld, work, (int)n_work,        \
                                     v_bf16, stream)
   if (D == 128) {
+    if (hpb == 4 && rows == 32) QX_ATTN(128, 4, 1);
     if (hpb == 4) QX_ATTN(128, 4, 2);
     if (hpb == 2) QX_ATTN(128, 2, 4);
     QX_ATTN(128, 1, 8);
@@ -676,12 +693,13 @@ int qx_paged_attention(const void* q, int64_t q_ld, const void* k_pool, const vo
                        int64_t seqs, int64_t max_q, int64_t max_used, int64_t HQ, int64_t HK,
                        int64_t D, int64_t page, float scale, int causal, void* out_bf16,
                        void* out_fp8, int64_t o_ld, float* scales, int64_t s_ld,
-                       const int* work, int64_t n_work, int v_bf16, hipStream_t stream) {
+                       const int* work, int64_t n_work, int64_t tile_rows, int v_bf16,
+                       hipStream_t stream) {
   QX_CHECK(table, "attention: null pointer");
   return qx::attention_impl(q, q_ld, nullptr, k_pool, v_pool, cu_q, used, table, table_ld,
                             nullptr, seqs, max_q, max_used, HQ, HK, D, page, scale, causal,
                             out_bf16, out_fp8, o_ld, scales, s_ld, nullptr, 0, work, n_work,
-                            v_bf16, stream);
+                            tile_rows, v_bf16, stream);
 }
 
 // The tree path's two calls: bf16 output plus each row's log-sum-exp.
@@ -699,7 +717,7 @@ int qx_attention_lse(const void* q, int64_t q_ld, const int64_t* q_index, const 
   QX_CHECK((table == nullptr) != (cu_k == nullptr), "attention_lse: give a table or cu_k");
   return qx::attention_impl(q, q_ld, q_index, k, v, cu_q, used, table, table_ld, cu_k, seqs,
                             max_q, max_used, HQ, HK, D, qx::kPage, scale, causal, out_bf16,
-                            nullptr, o_ld, nullptr, 0, lse, lse_ld, work, n_work, v_bf16,
+                            nullptr, o_ld, nullptr, 0, lse, lse_ld, work, n_work, 0, v_bf16,
                             stream);
 }
 
@@ -752,18 +770,51 @@ int qx_merge_partial(void* out, int64_t o_ld, float* lse, int64_t lse_ld, const 
   QX_LAUNCH_STATUS();
 }
 
+// Host function: the query rows per workgroup a paged call over these
+// sequences runs best with (the tile height to build its work list and call
+// it with): 32 where the configuration allows it and the 64-row work items
+// read at most kShortItemTiles 64-key tiles on average, else the default.
+int64_t qx_paged_attention_tile_rows(const int* cu_q, const int* used, int64_t seqs, int64_t HQ,
+                                     int64_t HK, int64_t D, int causal) {
+  if (!(cu_q && used && seqs >= 0 && HQ > 0 && HK > 0 && HQ % HK == 0)) {
+    qx::set_error("attention_tile_rows: arguments");
+    return QX_EINVAL;
+  }
+  const int64_t G = HQ / HK;
+  const int bq = qx::attn_default_rows(G);
+  if (!qx::attn_rows_ok(D, G, 32) || bq == 32) return bq;
+  int64_t items = 0, tiles = 0;
+  for (int64_t s = 0; s < seqs; ++s) {
+    const int q_len = cu_q[s + 1] - cu_q[s];
+    const int u = used[s];
+    for (int qt = 0; qt * bq < q_len; ++qt) {
+      const int last = std::min(qt * bq + bq, q_len) - 1;
+      const int keys = causal ? std::min(u, u - q_len + last + 1) : u;
+      tiles += (std::max(keys, 0) + 63) / 64;
+      ++items;
+    }
+  }
+  return items && (double)tiles <= qx::kShortItemTiles * (double)items ? 32 : bq;
+}
+
 // Host function: the work list of a paged call, one (sequence, query tile)
-// item per query tile holding rows, in the tile size the call dispatches
-// for (HQ / HK, D), heaviest first (most keys to read; ties in sequence and
+// item per query tile of tile_rows rows (0: the default for (HQ / HK, D))
+// that holds rows, heaviest first (most keys to read; ties in sequence and
 // tile order). Returns the number of items (<= capacity) or -1.
 int64_t qx_paged_attention_work(const int* cu_q, const int* used, int64_t seqs, int64_t HQ,
-                                int64_t HK, int64_t D, int causal, int* work,
+                                int64_t HK, int64_t D, int causal, int64_t tile_rows, int* work,
                                 int64_t capacity) {
   if (!(cu_q && used && work && seqs >= 0 && HQ > 0 && HK > 0 && HQ % HK == 0)) {
     qx::set_error("attention_work: arguments");
     return QX_EINVAL;
   }
-  const int bq = qx::attn_query_tile(D, HQ / HK);
+  const int64_t G = HQ / HK;
+  const int bq = (int)(tile_rows ? tile_rows : qx::attn_default_rows(G));
+  if (!qx::attn_rows_ok(D, G, bq)) {
+    qx::set_error("attention_work: %d query rows per workgroup (D=%lld, G=%lld)", bq,
+                  (long long)D, (long long)G);
+    return QX_EINVAL;
+  }
   struct Item { int64_t load; int s, qt; };
   std::vector<Item> items;
   for (int64_t s = 0; s < seqs; ++s) {

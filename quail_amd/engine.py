@@ -618,20 +618,22 @@ class Engine:
                 _ptr(table), table.stride(0), seqs, int(tables["max_q"]),
                 int(tables["max_used"]), hq, hk, d, self.arena.page_tokens, float(scale),
                 int(tables.get("causal", True)))
-        # the pack's work list (one item per real query tile), when it has one
+        # the pack's work list (one item per real query tile), when it has
+        # one, and the query rows per item it was built for
         work = tables.get("work")
         if not torch.is_tensor(work):
             work = None
         n_work = int(tables.get("n_work", 0)) if work is not None else 0
+        rows = int(tables.get("work_rows", 0)) if work is not None else 0
         if d == GROUP:
             _lib.call("qx_paged_attention", _ptr(q3), q_ld, *args, None, _ptr(o_q),
-                      o_q.stride(0), _ptr(o_s), self._scale_ld(o_s), _ptr(work), n_work,
+                      o_q.stride(0), _ptr(o_s), self._scale_ld(o_s), _ptr(work), n_work, rows,
                       v_bf16, _stream())
         else:
             # a 128-column FP8 group spans several heads: bf16 out, then quant
             o = torch.empty((n, hq * d), dtype=torch.bfloat16, device=q3.device)
             _lib.call("qx_paged_attention", _ptr(q3), q_ld, *args, _ptr(o), None, o.stride(0),
-                      None, 0, _ptr(work), n_work, v_bf16, _stream())
+                      None, 0, _ptr(work), n_work, rows, v_bf16, _stream())
             self.quant(o, output=(o_q, o_s))
         return o_q, o_s
 
@@ -648,6 +650,6 @@ class Engine:
                   unified["used"].shape[0], int(unified["max_q"]), int(unified["max_used"]),
                   hq, hk, d,
                   self.arena.page_tokens, float(d ** -0.5), int(unified.get("causal", True)),
-                  _ptr(o), None, o.stride(0), None, 0, None, 0,
+                  _ptr(o), None, o.stride(0), None, 0, None, 0, 0,
                   int(v_pool.dtype == torch.bfloat16), _stream())
         return o

@@ -18,7 +18,7 @@ import torch
 from oracle import fp8 as ofp8
 from oracle import qwen3_ref as ref
 from quail_amd import _lib
-from quail_amd.engine import Engine
+from quail_amd.engine import Engine, _ptr, _stream
 
 pytestmark = pytest.mark.gpu
 
@@ -538,6 +538,46 @@ def test_paged_attention_long_sequences_match_exact_fp32(v_dtype):
                              max_q=int(q_lens.max()), max_used=int(used.max()), causal=True))
     got = eng.attention_bf16(q.to(DEV), meta, 0)
     torch.testing.assert_close(got.float().cpu().view_as(want), want.float(), rtol=2e-2, atol=2e-2)
+
+
+@pytest.mark.parametrize("v_dtype", V_DTYPES)
+def test_paged_attention_32_row_workgroups_are_bit_identical(v_dtype):
+    """The 4-wave workgroups of 32 query rows (two per CU) that packs of short
+    documents take give every row of the 8-wave, 64-row workgroups bit for
+    bit: through work lists of either height, with bf16 output and with the
+    fused o_proj quant, and exact fp32 attention within the kernel
+    tolerance. The tile height comes from qx_paged_attention_tile_rows."""
+    from quail_amd import _lib
+    from quail_amd.chunk import _work_list
+
+    hq, hk, d, page = 32, 8, 128, 16
+    q, kp, vp, cu, used, table = _paged_case(91, hq, hk, d, page, 40, 1200)
+    want = ref.paged_attention(q, kp, vp, cu, used, table, page)
+    eng = _engine(hq, hk, d, arena=_Arena(kp.to(DEV), vp.to(v_dtype).to(DEV), page))
+    host = dict(cu_q=cu, used=used, causal=True)
+    assert _work_list(host, (hq, hk, d), choose_rows=True)[2] == 32
+    outs = {}
+    for rows in (0, 32):
+        work, n_work = _work_list(host, (hq, hk, d))[:2] if rows == 0 else \
+            _work_list(host, (hq, hk, d), choose_rows=True)[:2]
+        tables = dict(cu_q=torch.tensor(cu, device=DEV), used=torch.tensor(used, device=DEV),
+                      table=torch.tensor(table, device=DEV), max_q=int(np.diff(cu).max()),
+                      max_used=int(used.max()), causal=True,
+                      work=torch.tensor(work, device=DEV), n_work=n_work, work_rows=rows)
+        q3 = q.to(DEV)
+        o_q, o_s = eng._paged(q3, tables, 0, None, None)
+        o = torch.empty((q.shape[0], hq * d), dtype=torch.bfloat16, device=DEV)
+        _lib.call("qx_paged_attention", _ptr(q3), hq * d, _ptr(eng.arena.kp), _ptr(eng.arena.vp),
+                  _ptr(tables["cu_q"]), _ptr(tables["used"]), _ptr(tables["table"]),
+                  tables["table"].stride(0), len(used), tables["max_q"], tables["max_used"],
+                  hq, hk, d, page, float(d ** -0.5), 1, _ptr(o), None, o.stride(0), None, 0,
+                  _ptr(tables["work"]), n_work, rows, int(v_dtype == torch.bfloat16), _stream())
+        torch.cuda.synchronize()
+        outs[rows] = (o_q.view(torch.uint8).clone(), o_s.clone(), o.clone())
+    assert torch.equal(outs[0][0], outs[32][0]) and torch.equal(outs[0][1], outs[32][1])
+    assert torch.equal(outs[0][2], outs[32][2])
+    torch.testing.assert_close(outs[32][2].float().cpu().view_as(want), want.float(), rtol=2e-2,
+                               atol=2e-2)
 
 
 def test_answer_head_modes():

@@ -28,7 +28,10 @@ def test_argument_errors_return_minus_one_with_a_message():
                   None)
     with pytest.raises(_lib.QxError, match="head_dim"):
         _lib.call("qx_paged_attention", 16, 8, 16, 16, 16, 16, 16, 1, 1, 1, 64, 4, 2, 96, 16,
-                  0.1, 1, 16, None, 8, None, 0, None, 0, 1, None)
+                  0.1, 1, 16, None, 8, None, 0, None, 0, 0, 1, None)
+    with pytest.raises(_lib.QxError, match="query rows per workgroup"):
+        _lib.call("qx_paged_attention", 16, 8, 16, 16, 16, 16, 16, 1, 1, 1, 64, 4, 2, 64, 16,
+                  0.1, 1, 16, None, 8, None, 0, None, 0, 32, 1, None)
     with pytest.raises(_lib.QxError, match="1..16"):
         _lib.call("qx_answer_head", 16, 8, 16, 8, 17, 1, 8, 0, None, 1.0, None, None, None,
                   None, None)
@@ -41,7 +44,7 @@ def test_attention_work_list_is_heaviest_first_and_covers_every_tile():
     used = np.array([150, 40, 260], dtype=np.int32)
     work = np.zeros(2 * 16, dtype=np.int32)
     n = _lib.count("qx_paged_attention_work", cu_q.ctypes.data, used.ctypes.data, 3, 32, 8,
-                   128, 1, work.ctypes.data, 16)
+                   128, 1, 0, work.ctypes.data, 16)
     items = [tuple(work[2 * i:2 * i + 2]) for i in range(n)]
     # query tiles of 64 rows (G = 4): 2 + 1 + 4 of them
     assert sorted(items) == [(0, 0), (0, 1), (1, 0), (2, 0), (2, 1), (2, 2), (2, 3)]
@@ -51,7 +54,43 @@ def test_attention_work_list_is_heaviest_first_and_covers_every_tile():
     assert loads == sorted(loads, reverse=True)
     with pytest.raises(_lib.QxError, match="capacity"):
         _lib.count("qx_paged_attention_work", cu_q.ctypes.data, used.ctypes.data, 3, 32, 8,
-                   128, 1, work.ctypes.data, 3)
+                   128, 1, 0, work.ctypes.data, 3)
+
+
+def test_attention_tile_rows_choice_and_32_row_work_list():
+    """qx_paged_attention_tile_rows picks 32 query rows per workgroup for
+    packs whose 64-row items read few key tiles (at most 8 on average) and
+    the default 64 otherwise; only D = 128 with 4 heads per workgroup offers
+    32 (G = 2 keeps its default of 128). A 32-row work list covers every
+    32-row tile that holds rows, heaviest first."""
+    import numpy as np
+
+    def rows(q_lens, used, hq=32, hk=8, d=128):
+        cu_q = np.concatenate([[0], np.cumsum(q_lens)]).astype(np.int32)
+        used = np.asarray(used, dtype=np.int32)
+        return _lib.count("qx_paged_attention_tile_rows", cu_q.ctypes.data, used.ctypes.data,
+                          len(used), hq, hk, d, 1)
+
+    # 512-token documents after a 64-token prefix: 5.5 key tiles per item
+    assert rows([512] * 4, [576] * 4) == 32
+    # 1024-token documents: 9.5 key tiles per item
+    assert rows([1024] * 4, [1088] * 4) == 64
+    assert rows([512] * 4, [576] * 4, d=64) == 64
+    assert rows([512] * 4, [576] * 4, hq=16, hk=8) == 128
+    cu_q = np.array([0, 100, 101, 301], dtype=np.int32)
+    used = np.array([150, 40, 260], dtype=np.int32)
+    work = np.zeros(2 * 32, dtype=np.int32)
+    n = _lib.count("qx_paged_attention_work", cu_q.ctypes.data, used.ctypes.data, 3, 32, 8,
+                   128, 1, 32, work.ctypes.data, 32)
+    items = [tuple(work[2 * i:2 * i + 2]) for i in range(n)]
+    assert sorted(items) == sorted([(0, t) for t in range(4)] + [(1, 0)] +
+                                   [(2, t) for t in range(7)])
+    keys = [min(u, u - ql + min(qt * 32 + 32, ql)) for s_, qt in items
+            for u, ql in [(int(used[s_]), int(cu_q[s_ + 1] - cu_q[s_]))]]
+    assert keys == sorted(keys, reverse=True)
+    with pytest.raises(_lib.QxError, match="query rows per workgroup"):
+        _lib.count("qx_paged_attention_work", cu_q.ctypes.data, used.ctypes.data, 3, 16, 8,
+                   128, 1, 32, work.ctypes.data, 32)
 
 
 def test_gemm_config_choice_by_shape(monkeypatch):
