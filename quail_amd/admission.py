@@ -176,6 +176,14 @@ class StageAdmission:
         arena = self.arena
         while self.queue and room > 0:
             d = self.queue.popleft()
+            f = len(self.prefixes[d])
+            most = f + self.suffix_rows[d]  # its rows when it borrows nothing
+            if most <= self.chunk_budget and most - max(self.tree_shared[d], 0) > room:
+                # too big for the room however much it borrows (and never a
+                # long document): held, as the checks below would decide,
+                # without asking the arena what it could borrow
+                held.append(d)
+                continue
             reads = self._reads_from(d)
             if reads == WAIT:
                 held.append(d)

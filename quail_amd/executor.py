@@ -15,8 +15,6 @@ retained KV, or runs as two halves.
 import time
 from collections import deque
 
-import numpy as np
-
 from quail_amd.admission import StageAdmission
 from quail_amd.chunk import ArenaFullError, InputStaging, pack_chunk, upload
 from quail_amd.prefix import PrefixIndex
@@ -45,11 +43,9 @@ class StageRun:
         t0 = time.perf_counter()
         tree = None
         if self.use_tree:
-            prompts = [np.concatenate([np.asarray(p, dtype=np.int64)] +
-                                      [np.asarray(suf, dtype=np.int64).reshape(-1)
-                                       for suf in sufs])
-                       for p, sufs in zip(self.prefixes, self.suffixes)]
-            tree = PrefixIndex(prompts).tree(self.arena.page_tokens)
+            tree = PrefixIndex.from_parts(
+                [[p, *sufs] for p, sufs in zip(self.prefixes, self.suffixes)]
+            ).tree(self.arena.page_tokens)
         adm = StageAdmission(self.prefixes, self.suffixes, self.arena, self.chunk_budget,
                              tree=tree)
         self._adm = adm

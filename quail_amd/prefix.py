@@ -62,14 +62,43 @@ class PrefixIndex:
 
     def __init__(self, documents):
         docs = [np.asarray(d, dtype=np.int64).reshape(-1) for d in documents]
-        lengths = np.fromiter((len(d) for d in docs), dtype=np.int64, count=len(docs))
-        self._offsets = np.zeros(len(docs) + 1, dtype=np.int64)
-        np.cumsum(lengths, out=self._offsets[1:])
-        self._tokens = (np.concatenate(docs) if docs else np.zeros(0, dtype=np.int64))
+        self._set(docs, [len(d) for d in docs])
+
+    @classmethod
+    def from_parts(cls, documents):
+        """The index of documents given as lists of token pieces (a prompt's
+        prefix and suffixes), joined once into the flat token array."""
+        self = cls.__new__(cls)
+        pieces, lengths = [], []
+        for parts in documents:
+            arrays = [np.asarray(p, dtype=np.int64).reshape(-1) for p in parts]
+            pieces.extend(arrays)
+            lengths.append(sum(len(a) for a in arrays))
+        self._set(pieces, lengths)
+        return self
+
+    def _set(self, pieces, lengths):
+        self._offsets = np.zeros(len(lengths) + 1, dtype=np.int64)
+        np.cumsum(np.asarray(lengths, dtype=np.int64), out=self._offsets[1:])
+        self._tokens = (np.concatenate(pieces) if pieces else np.zeros(0, dtype=np.int64))
         self._tokens = np.ascontiguousarray(self._tokens, dtype=np.int64)
-        order, _, shared = self._native(1)
-        self.order = order.tolist()
-        self.shared = shared.tolist()
+        self._sorted = None
+
+    def _sorted_shares(self):
+        if self._sorted is None:
+            order, _, shared = self._native(1)
+            self._sorted = (order.tolist(), shared.tolist())
+        return self._sorted
+
+    @property
+    def order(self):
+        """Document positions in sorted token order."""
+        return self._sorted_shares()[0]
+
+    @property
+    def shared(self):
+        """Tokens each document shares with its predecessor in that order."""
+        return self._sorted_shares()[1]
 
     def _native(self, page_tokens):
         n = len(self._offsets) - 1
