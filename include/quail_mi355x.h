@@ -119,7 +119,9 @@ int qx_qk_norm_rope(const void* qkv, int64_t qkv_ld, void* q_out, int64_t q_ld, 
 
 /*
  * qx_qk_norm_rope with the row's KV written straight into arena pages: q as
- * above; the normed, rotated K of row i goes to pool row dst[i] of k_pool and
+ * above (q_out may be NULL: then only K and V are written, for
+ * qx_paged_attention_qnorm, which normalizes and rotates q itself); the
+ * normed, rotated K of row i goes to pool row dst[i] of k_pool and
  * its V (qkv columns (HQ+HK)*D .. (HQ+2*HK)*D, bf16) to the same row of
  * v_pool, as bf16, or with v_f16 as fp16 (round to nearest even, saturated
  * at +-65504); dst[i] < 0 writes neither. Pool rows are HK*D
@@ -253,6 +255,26 @@ int qx_paged_attention(const void* q, int64_t q_ld, const void* k_pool, const vo
                        void* out_fp8, int64_t o_ld, float* scales, int64_t s_ld,
                        const int* work, int64_t n_work, int64_t tile_rows, int v_bf16,
                        hipStream_t stream);
+
+/*
+ * qx_paged_attention (with the o_proj quant, D == 128) on q as the qkv
+ * projection leaves it: q (the first HQ*128 columns of the qkv rows, q_ld
+ * apart) is put through Qwen3's q-norm and neox RoPE per row as it is
+ * loaded, with positions[i] (query row i), the (max_pos, 128) [cos | sin]
+ * cache (fp32 with cs_is_f32, else bf16), the bf16 q-norm weight q_w and eps:
+ * bit for bit what qx_qk_norm_rope_kv writes as q_out, whose pass then
+ * writes K and V only (q_out NULL). Fuses the q half of Engine.qk_norm_rope
+ * (attention.py:1251-1255 -> :833-879) into the attention call it feeds
+ * (attention.py:1477-1573); saves q's write and re-read.
+ */
+int qx_paged_attention_qnorm(const void* q, int64_t q_ld, const void* k_pool, const void* v_pool,
+                             const int* cu_q, const int* used, const int* table,
+                             int64_t table_ld, int64_t seqs, int64_t max_q, int64_t max_used,
+                             int64_t HQ, int64_t HK, int64_t D, int64_t page, float scale,
+                             int causal, void* out_fp8, int64_t o_ld, float* scales, int64_t s_ld,
+                             const int* work, int64_t n_work, int64_t tile_rows, int v_bf16,
+                             const int64_t* positions, const void* cos_sin, int cs_is_f32,
+                             const void* q_w, float eps, hipStream_t stream);
 
 /*
  * Host function: the query rows per workgroup (work-list tile height) that a

@@ -50,6 +50,9 @@ SIGNATURES = {
                            _i64, _i64, _f32, _i32, _p, _p, _i64, _p, _i64, _p, _i64, _i64, _i32,
                            _p],
     "qx_paged_attention_tile_rows": [_p, _p, _i64, _i64, _i64, _i64, _i32],
+    "qx_paged_attention_qnorm": [_p, _i64, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64,
+                                 _i64, _i64, _i64, _f32, _i32, _p, _i64, _p, _i64, _p, _i64,
+                                 _i64, _i32, _p, _p, _i32, _p, _f32, _p],
     "qx_paged_attention_work": [_p, _p, _i64, _i64, _i64, _i64, _i32, _i64, _p, _i64],
     "qx_attention_lse": [_p, _i64, _p, _p, _p, _p, _p, _p, _i64, _p, _i64, _i64, _i64, _i64,
                          _i64, _i64, _f32, _i32, _p, _i64, _p, _i64, _p, _i64, _i32, _p],

@@ -67,6 +67,102 @@ __device__ __forceinline__ int kswz(int key) { return D == 128 ? (key & 15) : ((
 template <int D>
 __device__ __forceinline__ int vswz(int key) { return D == 128 ? ((key & 3) << 2) : (((key >> 1) & 1) << 2); }
 
+// QN != 0: q holds the raw (pre-norm) q columns of the qkv projection, and
+// the kernel applies each row's qk-norm and RoPE as it loads it: position
+// pos[row], the cos/sin cache cs ((max_pos, 128) [cos | sin], bf16 for
+// QN = 1, fp32 for QN = 2), the q-norm weight qw and eps.
+struct QNormArgs {
+  const int64_t* pos;
+  const void* cs;       // (positions, 128) cos | sin; bf16 (QN 1) or fp32 (QN 2)
+  const uint16_t* qw;  // the q-norm weight (128), bf16
+  float eps;
+};
+
+// The lane's 64 q columns (c*16 + half*8 + k, c, k < 8) of one head through
+// qk-norm and RoPE with the qk-norm-rope pass's arithmetic and summation
+// tree. The pass sums a head's 16 column groups j (columns 4j.. and
+// 64 + 4j..) with a butterfly over j (xor 8, 4, 2, 1); group j = 4c + 2 half
+// + e (c < 4) is this lane's columns c*16 + half*8 + 4e.., so the xor-8 and
+// xor-4 levels pair the lane's own groups (c ^ 2, c ^ 1), xor 2 pairs it
+// with lane ^ 32 and xor 1 its own e ^ 1: the same sums of the same terms,
+// and each addition commutes, so the rows come out bit for bit as the
+// pass writes them.
+template <int QN>
+__device__ __forceinline__ void q_norm_rope_frags(v8s (&qf)[8], const QNormArgs& qn, int64_t row,
+                                                  int half) {
+  // the loads first: the position, then that row's cos / sin of the lane's
+  // first-half columns; the q-norm weight of all its columns
+  const int64_t p = qn.pos[row];
+  uint4 wq[8];
+#pragma unroll
+  for (int c = 0; c < 8; ++c) wq[c] = *reinterpret_cast<const uint4*>(qn.qw + c * 16 + half * 8);
+  float cosv[4][2][4], sinv[4][2][4];
+  if constexpr (QN == 1) {
+    const uint16_t* row_cs = reinterpret_cast<const uint16_t*>(qn.cs) + p * 128;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const uint4 cw = *reinterpret_cast<const uint4*>(row_cs + c * 16 + half * 8);
+      const uint4 sw = *reinterpret_cast<const uint4*>(row_cs + 64 + c * 16 + half * 8);
+      bf16x4_to_f32(make_uint2(cw.x, cw.y), cosv[c][0]);
+      bf16x4_to_f32(make_uint2(cw.z, cw.w), cosv[c][1]);
+      bf16x4_to_f32(make_uint2(sw.x, sw.y), sinv[c][0]);
+      bf16x4_to_f32(make_uint2(sw.z, sw.w), sinv[c][1]);
+    }
+  } else {
+    const float* row_cs = reinterpret_cast<const float*>(qn.cs) + p * 128;
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const float4 cv = *reinterpret_cast<const float4*>(row_cs + c * 16 + half * 8 + e * 4);
+        const float4 sv =
+            *reinterpret_cast<const float4*>(row_cs + 64 + c * 16 + half * 8 + e * 4);
+        cosv[c][e][0] = cv.x; cosv[c][e][1] = cv.y; cosv[c][e][2] = cv.z; cosv[c][e][3] = cv.w;
+        sinv[c][e][0] = sv.x; sinv[c][e][1] = sv.y; sinv[c][e][2] = sv.z; sinv[c][e][3] = sv.w;
+      }
+  }
+  auto group = [&](const v8s& x, int e, float (&out)[4]) {
+    const uint4 w = __builtin_bit_cast(uint4, x);
+    bf16x4_to_f32(e ? make_uint2(w.z, w.w) : make_uint2(w.x, w.y), out);
+  };
+  float s[4][2];
+#pragma unroll
+  for (int c = 0; c < 4; ++c)
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      float a[4], b[4];
+      group(qf[c], e, a);
+      group(qf[c + 4], e, b);
+      s[c][e] = norm_part4(a, b);
+    }
+  float w[2];
+#pragma unroll
+  for (int e = 0; e < 2; ++e) w[e] = sum_halves((s[0][e] + s[2][e]) + (s[1][e] + s[3][e]));
+  const float rstd = norm_rstd<128>(w[0] + w[1], qn.eps);
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    uint4 lo = __builtin_bit_cast(uint4, qf[c]), hi = __builtin_bit_cast(uint4, qf[c + 4]);
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      float a[4], b[4], wa[4], wb[4], oa[4], ob[4];
+      group(qf[c], e, a);
+      group(qf[c + 4], e, b);
+      group(__builtin_bit_cast(v8s, wq[c]), e, wa);
+      group(__builtin_bit_cast(v8s, wq[c + 4]), e, wb);
+      norm_rope4(a, b, wa, wb, cosv[c][e], sinv[c][e], rstd, oa, ob);
+      const uint32_t o0 = pack2_bf16(oa[0], oa[1]), o1 = pack2_bf16(oa[2], oa[3]);
+      const uint32_t p0 = pack2_bf16(ob[0], ob[1]), p1 = pack2_bf16(ob[2], ob[3]);
+      if (e) {
+        lo.z = o0; lo.w = o1; hi.z = p0; hi.w = p1;
+      } else {
+        lo.x = o0; lo.y = o1; hi.x = p0; hi.y = p1;
+      }
+    }
+    qf[c] = __builtin_bit_cast(v8s, lo);
+    qf[c + 4] = __builtin_bit_cast(v8s, hi);
+  }
+}
+
 // CONTIG: keys are contiguous rows, key j of sequence s at row cu_k[s] + j
 // (no block table). q_index (optional): query row i reads Q row q_index[i].
 // lse (optional): lse[h * lse_ld + i] = ln(sum_j exp(scale * s_ij)) of row i.
@@ -76,7 +172,7 @@ __device__ __forceinline__ int vswz(int key) { return D == 128 ? ((key & 3) << 2
 // own that stores V in fp16).
 // Registers for two waves per SIMD: one 8-wave workgroup per CU, or two of
 // 4 waves.
-template <int D, int HPB, int QSUB, bool QUANT, bool CONTIG, bool VBF>
+template <int D, int HPB, int QSUB, bool QUANT, bool CONTIG, bool VBF, int QN = 0>
 __global__ __launch_bounds__(HPB * QSUB * 64, 8 / (HPB * QSUB)) void paged_attention_kernel(
     const uint16_t* __restrict__ q, int64_t q_ld, const int64_t* __restrict__ q_index,
     const uint16_t* __restrict__ kp, const uint16_t* __restrict__ vp,
@@ -84,7 +180,8 @@ __global__ __launch_bounds__(HPB * QSUB * 64, 8 / (HPB * QSUB)) void paged_atten
     int64_t table_ld, const int* __restrict__ cu_k, int max_used, int HQ, int HK,
     float scale_log2, int causal, uint16_t* __restrict__ out16, uint8_t* __restrict__ out8,
     int64_t o_ld, float* __restrict__ scales, int64_t s_ld, float* __restrict__ lse,
-    int64_t lse_ld, const int* __restrict__ work, int zgroups, int seqs) {
+    int64_t lse_ld, const int* __restrict__ work, int zgroups, int seqs, QNormArgs qn) {
+  static_assert(QN == 0 || (D == 128 && QUANT && !CONTIG), "q-norm on load: the paged D=128 call");
   constexpr int NW = HPB * QSUB;
   constexpr int NT = NW * 64;
   constexpr int BQ = 32 * QSUB;  // query rows per workgroup
@@ -152,13 +249,13 @@ __global__ __launch_bounds__(HPB * QSUB * 64, 8 / (HPB * QSUB)) void paged_atten
   // this lane's Q row (through q_index, which only the tree path's reads of
   // resident pages pass, before the table load so that its wait does not
   // also wait for that)
-  const uint16_t* qrow;
+  int64_t qr;
   {
     const int rr = r_ok ? r : q_len - 1;
     const int64_t* qi = QUANT ? nullptr : q_index;
-    const int64_t qr = qi ? qi[q0 + rr] : (int64_t)(q0 + rr);
-    qrow = q + qr * q_ld + head * D;
+    qr = qi ? qi[q0 + rr] : (int64_t)(q0 + rr);
   }
+  const uint16_t* qrow = q + qr * q_ld + head * D;
 
   // stage the page-table row straight into LDS (no VGPR round trip), in
   // flight together with the Q loads below: 64 entries per wave and pass,
@@ -177,6 +274,7 @@ __global__ __launch_bounds__(HPB * QSUB * 64, 8 / (HPB * QSUB)) void paged_atten
   {
 #pragma unroll
     for (int c = 0; c < ND16; ++c) qf[c] = *reinterpret_cast<const v8s*>(qrow + c * 16 + half * 8);
+    if constexpr (QN != 0) q_norm_rope_frags<QN>(qf, qn, qr, half);
     // consume the Q fragments here, before any KV load is issued: the
     // compiler's own waits for them would otherwise land inside the tile
     // loop, behind the KV loads it does not track, and drain those too
@@ -462,7 +560,8 @@ int launch_attn_v(const void* q, int64_t q_ld, const int64_t* q_index, const voi
                   int64_t table_ld, const int* cu_k, int seqs, int max_q, int max_used, int HQ,
                   int HK, int page, float scale, int causal, void* out16, void* out8,
                   int64_t o_ld, float* scales, int64_t s_ld, float* lse, int64_t lse_ld,
-                  const int* work, int n_work, hipStream_t stream) {
+                  const int* work, int n_work, const QNormArgs* qn, int qn_f32,
+                  hipStream_t stream) {
   const int G = HQ / HK;
   constexpr int BQ = 32 * QSUB;
   const int zgroups = HK * (G / HPB);
@@ -473,21 +572,40 @@ int launch_attn_v(const void* q, int64_t q_ld, const int64_t* q_index, const voi
   const uint16_t* q16 = (const uint16_t*)q;
   const uint16_t* k16 = (const uint16_t*)kp;
   const uint16_t* v16 = (const uint16_t*)vp;
-  if (out8) {
+  bool launched = false;
+  if constexpr (D == 128) {
+    if (out8 && qn) {
+      if (qn_f32)
+        hipLaunchKernelGGL((paged_attention_kernel<D, HPB, QSUB, true, false, VBF, 2>), grid,
+                           block, 0, stream, q16, q_ld, q_index, k16, v16, cu_q, used, table,
+                           table_ld, cu_k, max_used, HQ, HK, scale_log2, causal, nullptr,
+                           (uint8_t*)out8, o_ld, scales, s_ld, lse, lse_ld, work, zgroups, seqs,
+                           *qn);
+      else
+        hipLaunchKernelGGL((paged_attention_kernel<D, HPB, QSUB, true, false, VBF, 1>), grid,
+                           block, 0, stream, q16, q_ld, q_index, k16, v16, cu_q, used, table,
+                           table_ld, cu_k, max_used, HQ, HK, scale_log2, causal, nullptr,
+                           (uint8_t*)out8, o_ld, scales, s_ld, lse, lse_ld, work, zgroups, seqs,
+                           *qn);
+      launched = true;
+    }
+  }
+  if (launched) {
+  } else if (out8) {
     hipLaunchKernelGGL((paged_attention_kernel<D, HPB, QSUB, true, false, VBF>), grid, block, 0,
                        stream, q16, q_ld, q_index, k16, v16, cu_q, used, table, table_ld, cu_k,
                        max_used, HQ, HK, scale_log2, causal, nullptr, (uint8_t*)out8, o_ld,
-                       scales, s_ld, lse, lse_ld, work, zgroups, seqs);
+                       scales, s_ld, lse, lse_ld, work, zgroups, seqs, QNormArgs{});
   } else if (cu_k) {
     hipLaunchKernelGGL((paged_attention_kernel<D, HPB, QSUB, false, true, VBF>), grid, block, 0,
                        stream, q16, q_ld, q_index, k16, v16, cu_q, used, table, table_ld, cu_k,
                        max_used, HQ, HK, scale_log2, causal, (uint16_t*)out16, nullptr, o_ld,
-                       nullptr, 0, lse, lse_ld, work, zgroups, seqs);
+                       nullptr, 0, lse, lse_ld, work, zgroups, seqs, QNormArgs{});
   } else {
     hipLaunchKernelGGL((paged_attention_kernel<D, HPB, QSUB, false, false, VBF>), grid, block, 0,
                        stream, q16, q_ld, q_index, k16, v16, cu_q, used, table, table_ld, cu_k,
                        max_used, HQ, HK, scale_log2, causal, (uint16_t*)out16, nullptr, o_ld,
-                       nullptr, 0, lse, lse_ld, work, zgroups, seqs);
+                       nullptr, 0, lse, lse_ld, work, zgroups, seqs, QNormArgs{});
   }
   QX_LAUNCH_STATUS();
 }
@@ -498,16 +616,16 @@ int launch_attn(const void* q, int64_t q_ld, const int64_t* q_index, const void*
                 int64_t table_ld, const int* cu_k, int seqs, int max_q, int max_used, int HQ,
                 int HK, int page, float scale, int causal, void* out16, void* out8, int64_t o_ld,
                 float* scales, int64_t s_ld, float* lse, int64_t lse_ld, const int* work,
-                int n_work, int v_bf16, hipStream_t stream) {
+                int n_work, int v_bf16, const QNormArgs* qn, int qn_f32, hipStream_t stream) {
   if (v_bf16)
     return launch_attn_v<D, HPB, QSUB, true>(q, q_ld, q_index, kp, vp, cu_q, used, table,
                                              table_ld, cu_k, seqs, max_q, max_used, HQ, HK, page,
                                              scale, causal, out16, out8, o_ld, scales, s_ld, lse,
-                                             lse_ld, work, n_work, stream);
+                                             lse_ld, work, n_work, qn, qn_f32, stream);
   return launch_attn_v<D, HPB, QSUB, false>(q, q_ld, q_index, kp, vp, cu_q, used, table,
                                             table_ld, cu_k, seqs, max_q, max_used, HQ, HK, page,
                                             scale, causal, out16, out8, o_ld, scales, s_ld, lse,
-                                            lse_ld, work, n_work, stream);
+                                            lse_ld, work, n_work, qn, qn_f32, stream);
 }
 
 // The tree path's merge (attention.py:902-948, merge_attn_quant with QUANT):
@@ -637,7 +755,8 @@ int attention_impl(const void* q, int64_t q_ld, const int64_t* q_index, const vo
                    int64_t max_used, int64_t HQ, int64_t HK, int64_t D, int64_t page, float scale,
                    int causal, void* out_bf16, void* out_fp8, int64_t o_ld, float* scales,
                    int64_t s_ld, float* lse, int64_t lse_ld, const int* work, int64_t n_work,
-                   int64_t tile_rows, int v_bf16, hipStream_t stream) {
+                   int64_t tile_rows, int v_bf16, hipStream_t stream,
+                   const QNormArgs* qn = nullptr, int qn_f32 = 0) {
   QX_CHECK(q && k_pool && v_pool && cu_q && used && (table || cu_k), "attention: null pointer");
   QX_CHECK(out_bf16 || out_fp8, "attention: no output");
   QX_CHECK(!(out_fp8 && (cu_k || lse || q_index)), "attention: fused quant is for the paged call");
@@ -663,7 +782,7 @@ int attention_impl(const void* q, int64_t q_ld, const int64_t* q_index, const vo
                                     table_ld, cu_k, args_seqs, args_mq, args_mu, (int)HQ,      \
                                     (int)HK, (int)page, scale, causal, out_bf16, out_fp8,      \
                                     o_ld, scales, s_ld, lse, lse_ld, work, (int)n_work,        \
-                                    v_bf16, stream)
+                                    v_bf16, qn, qn_f32, stream)
   if (D == 128) {
     if (hpb == 4 && rows == 32) QX_ATTN(128, 4, 1);
     if (hpb == 4) QX_ATTN(128, 4, 2);
@@ -700,6 +819,29 @@ int qx_paged_attention(const void* q, int64_t q_ld, const void* k_pool, const vo
                             nullptr, seqs, max_q, max_used, HQ, HK, D, page, scale, causal,
                             out_bf16, out_fp8, o_ld, scales, s_ld, nullptr, 0, work, n_work,
                             tile_rows, v_bf16, stream);
+}
+
+// qx_paged_attention with the o_proj quant on q as the qkv projection left
+// it: q (qkv's first HQ*128 columns, rows of q_ld) is normalized and rotated
+// per row as it is loaded (the qk-norm-rope pass then writes K and V only).
+int qx_paged_attention_qnorm(const void* q, int64_t q_ld, const void* k_pool, const void* v_pool,
+                             const int* cu_q, const int* used, const int* table,
+                             int64_t table_ld, int64_t seqs, int64_t max_q, int64_t max_used,
+                             int64_t HQ, int64_t HK, int64_t D, int64_t page, float scale,
+                             int causal, void* out_fp8, int64_t o_ld, float* scales, int64_t s_ld,
+                             const int* work, int64_t n_work, int64_t tile_rows, int v_bf16,
+                             const int64_t* positions, const void* cos_sin, int cs_is_f32,
+                             const void* q_w, float eps, hipStream_t stream) {
+  QX_CHECK(table && out_fp8 && scales && positions && cos_sin && q_w,
+           "attention_qnorm: null pointer");
+  QX_CHECK(D == 128, "attention_qnorm: head_dim %lld (128)", (long long)D);
+  QX_CHECK(((uintptr_t)cos_sin & 15) == 0 && ((uintptr_t)q_w & 15) == 0,
+           "attention_qnorm: cos_sin / q_w alignment");
+  const qx::QNormArgs qn{positions, cos_sin, static_cast<const uint16_t*>(q_w), eps};
+  return qx::attention_impl(q, q_ld, nullptr, k_pool, v_pool, cu_q, used, table, table_ld,
+                            nullptr, seqs, max_q, max_used, HQ, HK, D, page, scale, causal,
+                            nullptr, out_fp8, o_ld, scales, s_ld, nullptr, 0, work, n_work,
+                            tile_rows, v_bf16, stream, &qn, cs_is_f32 ? 1 : 0);
 }
 
 // The tree path's two calls: bf16 output plus each row's log-sum-exp.

@@ -212,6 +212,48 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
   return g * recip(d) * u;
 }
 
+// qk-norm and neox RoPE (attention.py:833-879) in pieces shared by the
+// qk-norm-rope pass and the attention's Q load, so both give the same bits;
+// no fused multiply-adds: each product and sum rounds on its own. A head's
+// column j-group is a[k] = x[4j + k] and b[k] = x[D/2 + 4j + k], k < 4.
+//
+// sum over k of a[k]^2 + b[k]^2, in k order
+__device__ __forceinline__ float norm_part4(const float (&a)[4], const float (&b)[4]) {
+#pragma clang fp contract(off)
+  float ss = 0.f;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) ss += a[k] * a[k] + b[k] * b[k];
+  return ss;
+}
+
+// 1 / sqrt(mean square + eps) of a head of D columns from its sum of squares
+template <int D>
+__device__ __forceinline__ float norm_rstd(float ss, float eps) {
+#pragma clang fp contract(off)
+  return 1.0f / sqrtf(ss / (float)D + eps);
+}
+
+// xa = a * rstd * wa, xb = b * rstd * wb; oa = xa cos - xb sin,
+// ob = xb cos + xa sin (cos / sin of columns 4j + k)
+__device__ __forceinline__ void norm_rope4(const float (&a)[4], const float (&b)[4],
+                                           const float (&wa)[4], const float (&wb)[4],
+                                           const float (&cosv)[4], const float (&sinv)[4],
+                                           float rstd, float (&oa)[4], float (&ob)[4]) {
+#pragma clang fp contract(off)
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const float xa = a[k] * rstd * wa[k];
+    const float xb = b[k] * rstd * wb[k];
+    oa[k] = xa * cosv[k] - xb * sinv[k];
+    ob[k] = xb * cosv[k] + xa * sinv[k];
+  }
+}
+
+// Four bf16 held in two words, as fp32.
+__device__ __forceinline__ void bf16x4_to_f32(uint2 w, float (&x)[4]) {
+  x[0] = lo_bf16(w.x); x[1] = hi_bf16(w.x); x[2] = lo_bf16(w.y); x[3] = hi_bf16(w.y);
+}
+
 // Per-group FP8 scale: max(amax, 1e-10) / 448 (attention.py:780-781).
 __device__ __forceinline__ float fp8_scale(float amax) {
   return fmaxf(amax, kScaleFloor) / kFp8Max;

@@ -247,25 +247,33 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
   const int row = blockIdx.x;
   const int slot = threadIdx.x / LPH;
   const int j = threadIdx.x % LPH;
-  const int64_t p = pos[row];
   const uint16_t* xrow = qkv + (int64_t)row * qkv_ld;
   const int total = HQ + HK;
   const int64_t kv_row = (int64_t)HK * D;
+  // with no q output the pass writes K and V only (the attention normalizes
+  // and rotates q as it loads it): the first k_threads lanes take the K
+  // heads and the rest copy V alongside (when the K heads leave any)
+  const bool kv_only = POOL && qo == nullptr;
+  const int k_threads = kv_only && HK < HPB ? HK * LPH : 256;
+  const int v_first = k_threads < 256 ? k_threads : 0;
   int64_t drow = 0, drow2 = -1;
   if (POOL) {
     drow = dst[row];
     drow2 = dst2 ? dst2[row] : -1;
-    if (drow >= 0 || drow2 >= 0) {
+    if ((drow >= 0 || drow2 >= 0) && (int)threadIdx.x >= v_first) {
       const uint4* vs = reinterpret_cast<const uint4*>(xrow + total * D);
       uint4* vd = drow >= 0 ? reinterpret_cast<uint4*>(vp + drow * kv_row) : nullptr;
       uint4* vd2 = drow2 >= 0 ? reinterpret_cast<uint4*>(vp2 + drow2 * kv_row) : nullptr;
-      for (int c = threadIdx.x; c < (int)(kv_row >> 3); c += 256) {
+      for (int c = threadIdx.x - v_first; c < (int)(kv_row >> 3); c += 256 - v_first) {
         const uint4 w = V_F16 ? bf16x8_to_f16(vs[c]) : vs[c];
         if (drow >= 0) vd[c] = w;
         if (drow2 >= 0) vd2[c] = w;
       }
     }
   }
+  // whole LPH-lane groups: the group_sum exchanges stay inside live groups
+  if ((int)threadIdx.x >= k_threads) return;
+  const int64_t p = pos[row];
   float cosv[4], sinv[4];
   if (CS_F32) {
     const float* c = reinterpret_cast<const float*>(cs) + p * D;
@@ -275,38 +283,24 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
     sinv[0] = s4.x; sinv[1] = s4.y; sinv[2] = s4.z; sinv[3] = s4.w;
   } else {
     const uint16_t* c = reinterpret_cast<const uint16_t*>(cs) + p * D;
-    uint2 c2 = *reinterpret_cast<const uint2*>(c + j * 4);
-    uint2 s2 = *reinterpret_cast<const uint2*>(c + HALF + j * 4);
-    cosv[0] = lo_bf16(c2.x); cosv[1] = hi_bf16(c2.x); cosv[2] = lo_bf16(c2.y); cosv[3] = hi_bf16(c2.y);
-    sinv[0] = lo_bf16(s2.x); sinv[1] = hi_bf16(s2.x); sinv[2] = lo_bf16(s2.y); sinv[3] = hi_bf16(s2.y);
+    bf16x4_to_f32(*reinterpret_cast<const uint2*>(c + j * 4), cosv);
+    bf16x4_to_f32(*reinterpret_cast<const uint2*>(c + HALF + j * 4), sinv);
   }
-  for (int h0 = 0; h0 < total; h0 += HPB) {
+  const int first = qo ? 0 : HQ;
+  for (int h0 = first; h0 < total; h0 += HPB) {
     const int h = h0 + slot;
     const bool live = h < total;  // uniform across the LPH lanes of a head
     const bool is_q = h < HQ;
     const uint16_t* wt = is_q ? qw : kw;
     const int hin = live ? h : 0;
-    uint2 a2 = *reinterpret_cast<const uint2*>(xrow + hin * D + j * 4);
-    uint2 b2 = *reinterpret_cast<const uint2*>(xrow + hin * D + HALF + j * 4);
-    float a[4] = {lo_bf16(a2.x), hi_bf16(a2.x), lo_bf16(a2.y), hi_bf16(a2.y)};
-    float b[4] = {lo_bf16(b2.x), hi_bf16(b2.x), lo_bf16(b2.y), hi_bf16(b2.y)};
-    float ss = 0.f;
-#pragma unroll
-    for (int k = 0; k < 4; ++k) ss += a[k] * a[k] + b[k] * b[k];
-    ss = group_sum<LPH>(ss);
-    const float rstd = 1.0f / sqrtf(ss / (float)D + eps);
-    uint2 wa2 = *reinterpret_cast<const uint2*>(wt + j * 4);
-    uint2 wb2 = *reinterpret_cast<const uint2*>(wt + HALF + j * 4);
-    float wa[4] = {lo_bf16(wa2.x), hi_bf16(wa2.x), lo_bf16(wa2.y), hi_bf16(wa2.y)};
-    float wb[4] = {lo_bf16(wb2.x), hi_bf16(wb2.x), lo_bf16(wb2.y), hi_bf16(wb2.y)};
-    float oa[4], ob[4];
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      float xa = a[k] * rstd * wa[k];
-      float xb = b[k] * rstd * wb[k];
-      oa[k] = xa * cosv[k] - xb * sinv[k];
-      ob[k] = xb * cosv[k] + xa * sinv[k];
-    }
+    float a[4], b[4], wa[4], wb[4], oa[4], ob[4];
+    bf16x4_to_f32(*reinterpret_cast<const uint2*>(xrow + hin * D + j * 4), a);
+    bf16x4_to_f32(*reinterpret_cast<const uint2*>(xrow + hin * D + HALF + j * 4), b);
+    const float ss = group_sum<LPH>(norm_part4(a, b));
+    const float rstd = norm_rstd<D>(ss, eps);
+    bf16x4_to_f32(*reinterpret_cast<const uint2*>(wt + j * 4), wa);
+    bf16x4_to_f32(*reinterpret_cast<const uint2*>(wt + HALF + j * 4), wb);
+    norm_rope4(a, b, wa, wb, cosv, sinv, rstd, oa, ob);
     if (live && (is_q || !POOL || drow >= 0)) {
       uint16_t* out = is_q    ? qo + (int64_t)row * qo_ld + h * D
                       : POOL ? kp + drow * kv_row + (h - HQ) * D
@@ -558,7 +552,7 @@ int qx_qk_norm_rope_kv(const void* qkv, int64_t qkv_ld, void* q_out, int64_t q_l
                        const int64_t* positions, const void* q_w, const void* k_w, int64_t n,
                        int64_t HQ, int64_t HK, int64_t D, float eps, int v_f16,
                        hipStream_t stream) {
-  QX_CHECK(qkv && q_out && k_pool && v_pool && dst && cos_sin && positions && q_w && k_w,
+  QX_CHECK(qkv && k_pool && v_pool && dst && cos_sin && positions && q_w && k_w,
            "qk_norm_rope_kv: null pointer");
   QX_CHECK(!dst2 || (k_pool2 && v_pool2), "qk_norm_rope_kv: second destination pools");
   QX_CHECK(qkv_ld % 8 == 0 && aligned16(qkv) && aligned16(k_pool) && aligned16(v_pool) &&

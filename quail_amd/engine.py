@@ -380,6 +380,32 @@ class Engine:
         meta["kv_fresh_layer"] = layer
         return q
 
+    def kv_norm_rope(self, qkv, positions, attn, meta):
+        """The K/V half of qk_norm_rope_kv: every row's normed, rotated K and
+        its V go into the arena pages of meta's layer, and q stays as the
+        projection left it; this layer's paged attention then normalizes and
+        rotates q as it loads it (qx_paged_attention_qnorm), with the same
+        arithmetic (bit for bit). Returns the raw q columns of qkv (a view)."""
+        n = qkv.shape[0]
+        hq, hk, d = self.num_q_heads, self.num_kv_heads, self.head_dim
+        if d != GROUP or qkv.shape[1] < (hq + 2 * hk) * d:
+            raise ValueError(f"kv_norm_rope: head_dim {d}, qkv width {qkv.shape[1]}")
+        dst = meta["unified"]["row_dst"]
+        if dst.shape[0] != n:
+            raise ValueError(f"row_dst has {dst.shape[0]} rows, qkv {n}")
+        layer = meta["layer"]
+        k_pool, v_pool = self.arena.layer_kv(layer)
+        self._check_pools(k_pool, v_pool)
+        cache = self._rope_cache()
+        _lib.call("qx_qk_norm_rope_kv", _ptr(qkv), qkv.stride(0), None, 0,
+                  _ptr(k_pool), _ptr(v_pool), _ptr(dst), None, None, None, _ptr(cache),
+                  int(cache.dtype == torch.float32), _ptr(positions), _ptr(attn.q_norm.weight),
+                  _ptr(attn.k_norm.weight), n, hq, hk, d, float(attn.q_norm.variance_epsilon),
+                  int(v_pool.dtype == torch.float16), _stream())
+        meta["kv_fresh_layer"] = layer
+        meta["q_norm_on_load"] = (positions, attn)
+        return qkv[:, :hq * d]
+
     @staticmethod
     def _check_pools(k_pool, v_pool):
         """K pools are bf16; V pools bf16 (the reference KVArena's,
@@ -574,7 +600,8 @@ class Engine:
         if meta["unified"] is None:
             raise ValueError("this engine reads KV from arena pages; pack with pages")
         self.write_kv(k3, v3, meta)
-        out = self._paged(q3, meta["unified"], meta["layer"], softmax_scale, output)
+        out = self._paged(q3, meta["unified"], meta["layer"], softmax_scale, output,
+                          qnorm=meta.pop("q_norm_on_load", None))
         meta["layer"] += 1
         return out
 
@@ -593,13 +620,18 @@ class Engine:
         k3, v3 = self._kv_views(n, k, v)
         self.write_kv(k3, v3, meta)
         qf = q.view(n, hq, d).index_select(0, rows)
-        out = self._paged(qf, fq, meta["layer"], None, None)
+        qnorm = meta.pop("q_norm_on_load", None)
+        if qnorm is not None:
+            qnorm = (qnorm[0].index_select(0, rows), qnorm[1])
+        out = self._paged(qf, fq, meta["layer"], None, None, qnorm=qnorm)
         meta["layer"] += 1
         return out
 
-    def _paged(self, q3, tables, layer, softmax_scale, output):
+    def _paged(self, q3, tables, layer, softmax_scale, output, qnorm=None):
         """One paged causal call over `tables` (cu_q, used, table, max_q,
-        max_used) with the o_proj input quantization fused."""
+        max_used) with the o_proj input quantization fused. qnorm =
+        (positions of q3's rows, attention module): q3 is the raw q of the
+        qkv projection, normalized and rotated as the kernel loads it."""
         n = q3.shape[0]
         hq, hk, d = self.num_q_heads, self.num_kv_heads, self.head_dim
         k_pool, v_pool = self.arena.layer_kv(layer)
@@ -625,7 +657,16 @@ class Engine:
             work = None
         n_work = int(tables.get("n_work", 0)) if work is not None else 0
         rows = int(tables.get("work_rows", 0)) if work is not None else 0
-        if d == GROUP:
+        if qnorm is not None:
+            positions, attn = qnorm
+            if d != GROUP or positions.shape[0] != n:
+                raise ValueError("q-norm on load: head_dim 128 and one position per row")
+            cache = self._rope_cache()
+            _lib.call("qx_paged_attention_qnorm", _ptr(q3), q_ld, *args, _ptr(o_q),
+                      o_q.stride(0), _ptr(o_s), self._scale_ld(o_s), _ptr(work), n_work, rows,
+                      v_bf16, _ptr(positions), _ptr(cache), int(cache.dtype == torch.float32),
+                      _ptr(attn.q_norm.weight), float(attn.q_norm.variance_epsilon), _stream())
+        elif d == GROUP:
             _lib.call("qx_paged_attention", _ptr(q3), q_ld, *args, None, _ptr(o_q),
                       o_q.stride(0), _ptr(o_s), self._scale_ld(o_s), _ptr(work), n_work, rows,
                       v_bf16, _stream())

@@ -55,6 +55,10 @@ class Qwen3Pipeline:
         # qk-norm-rope writes the pack's K and V straight into the arena pages
         # when the engine has it and the pack's scatter source is its own rows
         self.fuse_kv_write = hasattr(self.engine, "qk_norm_rope_kv")
+        # ... and then the attention normalizes and rotates q as it loads it
+        # (that pass writes K and V only), at head_dim 128
+        self.fuse_q_norm = (hasattr(self.engine, "kv_norm_rope")
+                            and self.engine.head_dim == 128)
 
     def _check_bounds(self, chunk):
         """Token ids index the embedding and positions the rotary cache; the
@@ -94,6 +98,8 @@ class Qwen3Pipeline:
         if (chunk is not None and self.fuse_kv_write and chunk.attention_mode == "unified"
                 and not chunk.meta.get("kv_written", False)
                 and (chunk.meta.get("unified") or {}).get("row_dst") is not None):
+            if self.fuse_q_norm:
+                return engine.kv_norm_rope(qkv, positions, attn, chunk.meta), None, None
             return engine.qk_norm_rope_kv(qkv, positions, attn, chunk.meta), None, None
         if (chunk is not None and self.fuse_kv_write and chunk.attention_mode == "tree"
                 and hasattr(engine, "qk_norm_rope_rows")):

@@ -29,7 +29,7 @@ def ref_model(model, device="cpu") -> ref.RefModel:
 
 
 def run_stage(model, workload, readout_kind="margins", num_pages=None, use_tree=True,
-              attention_mode="unified", fuse_kv_write=None, v_dtype=None):
+              attention_mode="unified", fuse_kv_write=None, v_dtype=None, fuse_q_norm=None):
     """Run one stage of the workload through the GPU engine; returns
     (results per document, StageRun). v_dtype: the arena's V page type
     (its default, fp16, when None; bf16 is the reference arena's)."""
@@ -49,6 +49,8 @@ def run_stage(model, workload, readout_kind="margins", num_pages=None, use_tree=
     pipe = Qwen3Pipeline(model, arena)
     if fuse_kv_write is not None:
         pipe.fuse_kv_write = fuse_kv_write
+    if fuse_q_norm is not None:
+        pipe.fuse_q_norm = fuse_q_norm
     labels = workload.label_ids
     if readout_kind == "classify":
         readout = ro.AsyncLabelLogprobs(model.lm_head.weight, labels, normalize=False)
@@ -189,7 +191,9 @@ def exact_contractions(monkeypatch):
     (the dequantized operands' matmul, rounded to bf16; gate_up then the
     engine's own SiLU-quant kernel) and the paged attention (exact softmax
     over the pages the block table names, rounded to bf16, then the
-    engine's own group quant). Everything else stays the engine's."""
+    engine's own group quant). Everything else stays the engine's; q goes
+    through the engine's qk-norm-rope pass (the attention's q-norm on load
+    is an attention kernel's, so the pipeline is kept off it)."""
     from quail_amd.engine import Engine
 
     def gemm(self, q_input, input_scale, linear, out=None):
@@ -207,7 +211,8 @@ def exact_contractions(monkeypatch):
     def gate_up(self, q_input, input_scale, linear):
         return self.activation_quant(gemm(self, q_input, input_scale, linear))
 
-    def paged(self, q3, tables, layer, softmax_scale, output):
+    def paged(self, q3, tables, layer, softmax_scale, output, qnorm=None):
+        assert qnorm is None, "q reaches the exact attention normalized"
         n, hq, d = q3.shape
         group = hq // self.num_kv_heads
         k_pool, v_pool = self.arena.layer_kv(layer)
@@ -238,3 +243,4 @@ def exact_contractions(monkeypatch):
     monkeypatch.setattr(Engine, "gemm", gemm)
     monkeypatch.setattr(Engine, "gate_up_activation_quant", gate_up)
     monkeypatch.setattr(Engine, "_paged", paged)
+    monkeypatch.delattr(Engine, "kv_norm_rope")

@@ -228,7 +228,7 @@ def test_kv_write_in_qk_norm_rope_is_bit_identical(monkeypatch, mode, v_dtype):
                         v_dtype=v_dtype)
     assert not calls
     got, run = run_stage(model, wl, "margins", fuse_kv_write=True, attention_mode=mode,
-                         v_dtype=v_dtype)
+                         v_dtype=v_dtype, fuse_q_norm=False)
     assert len(calls) == cfg.layers * run.stats["chunks"]
     assert len(got) == len(base)
     assert all(np.array_equal(np.asarray(a), np.asarray(b)) for a, b in zip(got, base))

@@ -347,7 +347,7 @@ V_DTYPES = [torch.bfloat16, torch.float16]
 def test_qk_norm_rope_kv_equals_norm_rope_then_scatter(hq, hk, d, cache_dtype, v_dtype):
     """The fused pass writes q, and K / V into pool rows dst[i], bit for bit
     as qk_norm_rope followed by kv_row_scatter(src = 0..n-1); dst < 0 rows
-    write nothing."""
+    write nothing. Without q (q_out NULL) it writes the same pages."""
     n, pool_rows = 93, 320
     g = _gen(7 * hq + d)
     qkv = (torch.randn(n, (hq + 2 * hk) * d, generator=g) * 3).to(torch.bfloat16).to(DEV)
@@ -361,7 +361,7 @@ def test_qk_norm_rope_kv_equals_norm_rope_then_scatter(hq, hk, d, cache_dtype, v
     dst = torch.randperm(pool_rows, generator=g)[:n].to(DEV)
     dst[[0, 17, n - 1]] = -1
     pools = []
-    for _ in range(2):
+    for _ in range(3):
         kp = torch.full((pool_rows, hk, d), 7.0, dtype=torch.bfloat16, device=DEV)
         vp = torch.full((pool_rows, hk, d), 7.0, dtype=v_dtype, device=DEV)
         pools.append((kp, vp))
@@ -371,11 +371,18 @@ def test_qk_norm_rope_kv_equals_norm_rope_then_scatter(hq, hk, d, cache_dtype, v
     fused = _engine(hq, hk, d, arena=_Arena(*pools[1], 16), cache=cache)
     meta = {"layer": 0, "unified": {"row_dst": dst}}
     q = fused.qk_norm_rope_kv(qkv, pos, attn, meta)
+    # K and V only (q_out NULL): the K heads and the V copy on their own lanes
+    _lib.call("qx_qk_norm_rope_kv", _ptr(qkv), qkv.stride(0), None, 0, _ptr(pools[2][0]),
+              _ptr(pools[2][1]), _ptr(dst), None, None, None, _ptr(cache),
+              int(cache_dtype == torch.float32), _ptr(pos), _ptr(attn.q_norm.weight),
+              _ptr(attn.k_norm.weight), n, hq, hk, d, 1e-6, int(v_dtype == torch.float16),
+              _stream())
     torch.cuda.synchronize()
     assert meta["kv_fresh_layer"] == 0
     assert torch.equal(q, q_ref)
-    assert torch.equal(pools[1][0], pools[0][0])
-    assert torch.equal(pools[1][1], pools[0][1])
+    for i in (1, 2):
+        assert torch.equal(pools[i][0], pools[0][0])
+        assert torch.equal(pools[i][1], pools[0][1])
     assert int((pools[1][0].view(pool_rows, -1) != 7.0).all(1).sum()) == n - 3
 
 
@@ -578,6 +585,59 @@ def test_paged_attention_32_row_workgroups_are_bit_identical(v_dtype):
     assert torch.equal(outs[0][2], outs[32][2])
     torch.testing.assert_close(outs[32][2].float().cpu().view_as(want), want.float(), rtol=2e-2,
                                atol=2e-2)
+
+
+@pytest.mark.parametrize("cache_dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("v_dtype", V_DTYPES)
+def test_attention_with_q_norm_on_load_is_bit_identical(cache_dtype, v_dtype):
+    """The K/V-only qk-norm-rope pass plus qx_paged_attention_qnorm on the raw
+    qkv rows (q normalized and rotated as the attention loads it) write the
+    same pages and give the same e4m3 o_proj input and scales, bit for bit,
+    as qk_norm_rope_kv (q written) plus qx_paged_attention; with the 32-row
+    and the 64-row workgroups, on a bf16 and an fp32 rotary cache."""
+    from quail_amd.chunk import _work_list
+
+    hq, hk, d, page = 32, 8, 128, 16
+    _, kp, vp, cu, used, table = _paged_case(57, hq, hk, d, page, 30, 1000)
+    n = int(cu[-1])
+    g = _gen(58)
+    qkv = (torch.randn(n, (hq + 2 * hk) * d, generator=g) * 3).to(torch.bfloat16).to(DEV)
+    # each row's key position in its sequence and the pool row it goes to
+    pos = np.concatenate([np.arange(u - (cu[s_ + 1] - cu[s_]), u)
+                          for s_, u in enumerate(used)]).astype(np.int64)
+    seq = np.repeat(np.arange(len(used)), np.diff(cu))
+    dst = table[seq, pos // page].astype(np.int64) * page + pos % page
+    cache = ref.rope_cache(d, 4096, 1e6).to(cache_dtype).to(DEV)
+    attn = type("A", (), {})()
+    attn.q_norm = type("N", (), {"weight": (1 + 0.1 * torch.randn(d, generator=g)).to(
+        torch.bfloat16).to(DEV), "variance_epsilon": 1e-6})()
+    attn.k_norm = type("N", (), {"weight": (1 + 0.1 * torch.randn(d, generator=g)).to(
+        torch.bfloat16).to(DEV), "variance_epsilon": 1e-6})()
+    host = dict(cu_q=cu, used=used, causal=True)
+    for choose in (False, True):
+        work, n_work, rows = _work_list(host, (hq, hk, d), choose_rows=choose)
+        tables = dict(cu_q=torch.tensor(cu, device=DEV), used=torch.tensor(used, device=DEV),
+                      table=torch.tensor(table, device=DEV), max_q=int(np.diff(cu).max()),
+                      max_used=int(used.max()), causal=True,
+                      work=torch.tensor(work, device=DEV), n_work=n_work, work_rows=rows)
+        outs = []
+        for fused in (False, True):
+            kpool, vpool = kp.clone().to(DEV), vp.to(v_dtype).to(DEV)
+            eng = _engine(hq, hk, d, arena=_Arena(kpool, vpool, page), cache=cache)
+            meta = {"layer": 0, "unified": {"row_dst": torch.tensor(dst, device=DEV)}}
+            p_dev = torch.tensor(pos, device=DEV)
+            if fused:
+                q = eng.kv_norm_rope(qkv, p_dev, attn, meta)
+                qnorm = meta.pop("q_norm_on_load")
+            else:
+                q = eng.qk_norm_rope_kv(qkv, p_dev, attn, meta)
+                qnorm = None
+            o_q, o_s = eng._paged(q.view(n, hq, d), tables, 0, None, None, qnorm=qnorm)
+            torch.cuda.synchronize()
+            outs.append((kpool, vpool, o_q.view(torch.uint8).clone(), o_s.clone()))
+        assert rows == (32 if choose else 0)
+        for a, b in zip(*outs):
+            assert torch.equal(a, b)
 
 
 def test_answer_head_modes():

@@ -64,6 +64,31 @@ def test_packed_answers_equal_documents_run_alone(name, docs):
         assert all(len(r) == len(wl.label_ids) for r in packed)
 
 
+def test_q_norm_on_load_is_bit_identical(monkeypatch):
+    """The attention normalizing and rotating q as it loads it (the
+    qk-norm-rope pass then writes K and V only) gives the same classify
+    logits, bit for bit, as the pass writing q too, and runs on every layer
+    of every pack (the last layer's final-row attention included)."""
+    from quail_amd.engine import Engine
+
+    wl = make_workload("qwen3-8b", seed=6, documents=6)
+    model = build_synthetic(CONFIGS[wl.model], seed=6, device="cuda", layers=LAYERS)
+    calls = []
+    fused = Engine.kv_norm_rope
+
+    def counted(self, *args, **kwargs):
+        calls.append(1)
+        return fused(self, *args, **kwargs)
+
+    monkeypatch.setattr(Engine, "kv_norm_rope", counted)
+    base, _ = run_stage(model, wl, "classify", fuse_q_norm=False)
+    assert not calls
+    got, run = run_stage(model, wl, "classify", fuse_q_norm=True)
+    assert len(calls) == LAYERS * run.stats["chunks"]
+    assert len(got) == len(base)
+    assert all(np.array_equal(np.asarray(a), np.asarray(b)) for a, b in zip(got, base))
+
+
 def test_score_is_sigmoid_of_if_margin():
     wl = make_workload("qwen3-32b", seed=4, documents=8)
     model = build_synthetic(CONFIGS[wl.model], seed=4, device="cuda", layers=LAYERS)
