@@ -121,9 +121,13 @@ class Engine:
         self.is_fp8 = True
         self.use_ue8m0 = False
         # a list to receive (M, N, K, start event, end event, SwiGLU epilogue)
-        # per GEMM launch, recorded on the launch stream; None (the default)
-        # records nothing
+        # per timed GEMM launch, recorded on the launch stream; None (the
+        # default) records nothing. A timed launch costs the stream two event
+        # records (each leaves the GPU idle a few microseconds), so one launch
+        # in gemm_timer_every is timed; gemm_launches counts them all
         self.gemm_timer = None
+        self.gemm_timer_every = 1
+        self.gemm_launches = 0
 
     # ---- weights and quant --------------------------------------------
 
@@ -157,17 +161,25 @@ class Engine:
                              "column-major storage")
         if out is None:
             out = torch.empty((m, n), dtype=torch.bfloat16, device=q_input.device)
-        timer = self.gemm_timer
-        if timer is not None:
+        timed = self._timed_launch()
+        if timed:
             start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             start.record()
         _lib.call("qx_gemm_fp8_blockscaled", _ptr(q_input), _ptr(input_scale), _ptr(w),
                   _ptr(sw), _ptr(out), m, n, k, q_input.stride(0), out.stride(0),
                   self._scale_ld(input_scale), gemm_config(n, k, m), _stream())
-        if timer is not None:
+        if timed:
             end.record()
-            timer.append((m, n, k, start, end, False))
+            self.gemm_timer.append((m, n, k, start, end, False))
         return out
+
+    def _timed_launch(self):
+        """Whether this GEMM launch is timed: gemm_timer is set and the launch
+        is the first of its gemm_timer_every."""
+        if self.gemm_timer is None:
+            return False
+        self.gemm_launches += 1
+        return (self.gemm_launches - 1) % self.gemm_timer_every == 0
 
     def gate_up_activation_quant(self, q_input, input_scale, linear):
         """The gate_up projection and the quantized SiLU-gated product in one
@@ -188,17 +200,17 @@ class Engine:
         half = n // 2
         q = torch.empty((m, half), dtype=self.fp8, device=q_input.device)
         scales = self._col_major_scales(m, half, q_input.device)
-        timer = self.gemm_timer
-        if timer is not None:
+        timed = self._timed_launch()
+        if timed:
             start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             start.record()
         _lib.call("qx_gemm_fp8_swiglu_quant", _ptr(q_input), _ptr(input_scale), _ptr(w),
                   _ptr(sw), _ptr(q), q.stride(0), _ptr(scales), self._scale_ld(scales), m, half,
                   k, q_input.stride(0), self._scale_ld(input_scale), swiglu_config(n, k, m),
                   _stream())
-        if timer is not None:
+        if timed:
             end.record()
-            timer.append((m, n, k, start, end, True))
+            self.gemm_timer.append((m, n, k, start, end, True))
         return q, scales
 
     def quant(self, x, *, output=None):
