@@ -78,35 +78,34 @@ struct QNormArgs {
   float eps;
 };
 
-// The lane's 64 q columns (c*16 + half*8 + k, c, k < 8) of one head through
-// qk-norm and RoPE with the qk-norm-rope pass's arithmetic and summation
-// tree. The pass sums a head's 16 column groups j (columns 4j.. and
-// 64 + 4j..) with a butterfly over j (xor 8, 4, 2, 1); group j = 4c + 2 half
-// + e (c < 4) is this lane's columns c*16 + half*8 + 4e.., so the xor-8 and
-// xor-4 levels pair the lane's own groups (c ^ 2, c ^ 1), xor 2 pairs it
-// with lane ^ 32 and xor 1 its own e ^ 1: the same sums of the same terms,
-// and each addition commutes, so the rows come out bit for bit as the
-// pass writes them.
+// What q-norm on load reads for one lane: the q-norm weight of its 64
+// columns (c*16 + half*8 + k, c, k < 8), then, once the row's position is
+// in, the row's cos / sin of its first-half columns (bf16 for QN = 1, fp32
+// for QN = 2), raw as loaded.
 template <int QN>
-__device__ __forceinline__ void q_norm_rope_frags(v8s (&qf)[8], const QNormArgs& qn, int64_t row,
-                                                  int half) {
-  // the loads first: the position, then that row's cos / sin of the lane's
-  // first-half columns; the q-norm weight of all its columns
-  const int64_t p = qn.pos[row];
+struct QNormIn {
+  static constexpr int kCs = QN == 2 ? 16 : 8;
   uint4 wq[8];
+  uint4 cs[kCs];
+};
+
+template <int QN>
+__device__ __forceinline__ void q_norm_load_weights(QNormIn<QN>& in, const QNormArgs& qn,
+                                                    int half) {
 #pragma unroll
-  for (int c = 0; c < 8; ++c) wq[c] = *reinterpret_cast<const uint4*>(qn.qw + c * 16 + half * 8);
-  float cosv[4][2][4], sinv[4][2][4];
+  for (int c = 0; c < 8; ++c)
+    in.wq[c] = *reinterpret_cast<const uint4*>(qn.qw + c * 16 + half * 8);
+}
+
+template <int QN>
+__device__ __forceinline__ void q_norm_load_row(QNormIn<QN>& in, const QNormArgs& qn, int64_t p,
+                                                int half) {
   if constexpr (QN == 1) {
     const uint16_t* row_cs = reinterpret_cast<const uint16_t*>(qn.cs) + p * 128;
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
-      const uint4 cw = *reinterpret_cast<const uint4*>(row_cs + c * 16 + half * 8);
-      const uint4 sw = *reinterpret_cast<const uint4*>(row_cs + 64 + c * 16 + half * 8);
-      bf16x4_to_f32(make_uint2(cw.x, cw.y), cosv[c][0]);
-      bf16x4_to_f32(make_uint2(cw.z, cw.w), cosv[c][1]);
-      bf16x4_to_f32(make_uint2(sw.x, sw.y), sinv[c][0]);
-      bf16x4_to_f32(make_uint2(sw.z, sw.w), sinv[c][1]);
+      in.cs[2 * c] = *reinterpret_cast<const uint4*>(row_cs + c * 16 + half * 8);
+      in.cs[2 * c + 1] = *reinterpret_cast<const uint4*>(row_cs + 64 + c * 16 + half * 8);
     }
   } else {
     const float* row_cs = reinterpret_cast<const float*>(qn.cs) + p * 128;
@@ -114,12 +113,43 @@ __device__ __forceinline__ void q_norm_rope_frags(v8s (&qf)[8], const QNormArgs&
     for (int c = 0; c < 4; ++c)
 #pragma unroll
       for (int e = 0; e < 2; ++e) {
-        const float4 cv = *reinterpret_cast<const float4*>(row_cs + c * 16 + half * 8 + e * 4);
-        const float4 sv =
-            *reinterpret_cast<const float4*>(row_cs + 64 + c * 16 + half * 8 + e * 4);
-        cosv[c][e][0] = cv.x; cosv[c][e][1] = cv.y; cosv[c][e][2] = cv.z; cosv[c][e][3] = cv.w;
-        sinv[c][e][0] = sv.x; sinv[c][e][1] = sv.y; sinv[c][e][2] = sv.z; sinv[c][e][3] = sv.w;
+        in.cs[4 * c + 2 * e] = *reinterpret_cast<const uint4*>(row_cs + c * 16 + half * 8 + e * 4);
+        in.cs[4 * c + 2 * e + 1] =
+            *reinterpret_cast<const uint4*>(row_cs + 64 + c * 16 + half * 8 + e * 4);
       }
+  }
+}
+
+// The lane's 64 q columns of one head through qk-norm and RoPE with the
+// qk-norm-rope pass's arithmetic and summation tree. The pass sums a head's
+// 16 column groups j (columns 4j.. and 64 + 4j..) with a butterfly over j
+// (xor 8, 4, 2, 1); group j = 4c + 2 half + e (c < 4) is this lane's
+// columns c*16 + half*8 + 4e.., so the xor-8 and xor-4 levels pair the
+// lane's own groups (c ^ 2, c ^ 1), xor 2 pairs it with lane ^ 32 and xor 1
+// its own e ^ 1: the same sums of the same terms, and each addition
+// commutes, so the rows come out bit for bit as the pass writes them.
+template <int QN>
+__device__ __forceinline__ void q_norm_rope_apply(v8s (&qf)[8], const QNormIn<QN>& in,
+                                                  float eps) {
+  float cosv[4][2][4], sinv[4][2][4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    if constexpr (QN == 1) {
+      const uint4 cw = in.cs[2 * c], sw = in.cs[2 * c + 1];
+      bf16x4_to_f32(make_uint2(cw.x, cw.y), cosv[c][0]);
+      bf16x4_to_f32(make_uint2(cw.z, cw.w), cosv[c][1]);
+      bf16x4_to_f32(make_uint2(sw.x, sw.y), sinv[c][0]);
+      bf16x4_to_f32(make_uint2(sw.z, sw.w), sinv[c][1]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const uint4 cv = in.cs[4 * c + 2 * e], sv = in.cs[4 * c + 2 * e + 1];
+        cosv[c][e][0] = __uint_as_float(cv.x); cosv[c][e][1] = __uint_as_float(cv.y);
+        cosv[c][e][2] = __uint_as_float(cv.z); cosv[c][e][3] = __uint_as_float(cv.w);
+        sinv[c][e][0] = __uint_as_float(sv.x); sinv[c][e][1] = __uint_as_float(sv.y);
+        sinv[c][e][2] = __uint_as_float(sv.z); sinv[c][e][3] = __uint_as_float(sv.w);
+      }
+    }
   }
   auto group = [&](const v8s& x, int e, float (&out)[4]) {
     const uint4 w = __builtin_bit_cast(uint4, x);
@@ -138,7 +168,7 @@ __device__ __forceinline__ void q_norm_rope_frags(v8s (&qf)[8], const QNormArgs&
   float w[2];
 #pragma unroll
   for (int e = 0; e < 2; ++e) w[e] = sum_halves((s[0][e] + s[2][e]) + (s[1][e] + s[3][e]));
-  const float rstd = norm_rstd<128>(w[0] + w[1], qn.eps);
+  const float rstd = norm_rstd<128>(w[0] + w[1], eps);
 #pragma unroll
   for (int c = 0; c < 4; ++c) {
     uint4 lo = __builtin_bit_cast(uint4, qf[c]), hi = __builtin_bit_cast(uint4, qf[c + 4]);
@@ -147,8 +177,8 @@ __device__ __forceinline__ void q_norm_rope_frags(v8s (&qf)[8], const QNormArgs&
       float a[4], b[4], wa[4], wb[4], oa[4], ob[4];
       group(qf[c], e, a);
       group(qf[c + 4], e, b);
-      group(__builtin_bit_cast(v8s, wq[c]), e, wa);
-      group(__builtin_bit_cast(v8s, wq[c + 4]), e, wb);
+      group(__builtin_bit_cast(v8s, in.wq[c]), e, wa);
+      group(__builtin_bit_cast(v8s, in.wq[c + 4]), e, wb);
       norm_rope4(a, b, wa, wb, cosv[c][e], sinv[c][e], rstd, oa, ob);
       const uint32_t o0 = pack2_bf16(oa[0], oa[1]), o1 = pack2_bf16(oa[2], oa[3]);
       const uint32_t p0 = pack2_bf16(ob[0], ob[1]), p1 = pack2_bf16(ob[2], ob[3]);
@@ -271,10 +301,16 @@ __global__ __launch_bounds__(HPB * QSUB * 64, 8 / (HPB * QSUB)) void paged_atten
 
   // Q^T fragments (B operand): lane holds query `col`, d = c*16 + half*8 .. +8
   v8s qf[ND16];
+  // q-norm on load: the row's position and the weights go out with Q; the
+  // row's cos / sin (which need the position) after it, with the first K
+  // and V tiles, so that one memory round trip covers both
+  QNormIn<QN == 0 ? 1 : QN> qin;
+  int64_t q_pos = 0;
   {
+    if constexpr (QN != 0) q_pos = qn.pos[qr];
 #pragma unroll
     for (int c = 0; c < ND16; ++c) qf[c] = *reinterpret_cast<const v8s*>(qrow + c * 16 + half * 8);
-    if constexpr (QN != 0) q_norm_rope_frags<QN>(qf, qn, qr, half);
+    if constexpr (QN != 0) q_norm_load_weights(qin, qn, half);
     // consume the Q fragments here, before any KV load is issued: the
     // compiler's own waits for them would otherwise land inside the tile
     // loop, behind the KV loads it does not track, and drain those too
@@ -285,6 +321,7 @@ __global__ __launch_bounds__(HPB * QSUB * 64, 8 / (HPB * QSUB)) void paged_atten
   const uint16_t* kbase = kp + kvh * D;
   const uint16_t* vbase = vp + kvh * D;
   __builtin_amdgcn_s_waitcnt(0);
+  if constexpr (QN != 0) q_norm_load_row(qin, qn, q_pos, half);
   lds_barrier();  // pages_lds visible
 
   // K and V rows of tile t straight into LDS: lane i of a slab writes bytes
@@ -452,11 +489,16 @@ __global__ __launch_bounds__(HPB * QSUB * 64, 8 / (HPB * QSUB)) void paged_atten
   };
 
   v16f sa[2], sb[2];
+  // prologue: K and V of tile 0 and K of tile 1 (with q-norm on load, Q's
+  // norm and RoPE while they and the cos / sin rows are in flight), then S
+  // of tile 0
   if (ntiles > 0) {
-    // prologue: K and V of tile 0 and K of tile 1, then S of tile 0
     issue(0, 0, false);
     issue(0, 0, true);
     issue(1, 1, false);
+  }
+  if constexpr (QN != 0) q_norm_rope_apply(qf, qin, qn.eps);
+  if (ntiles > 0) {
     wait_vmcnt<0>();
     lds_barrier();
     s_tile(0, sa);
