@@ -461,3 +461,58 @@ def test_tiny_label_path_pass_matches_each_label_prefix_run_whole(every_node):
     rel = ((got - want).norm() / want.norm()).item()
     print(f"label-path rows vs each prefix run whole: relative {rel:.4f}")
     assert rel <= 0.06, rel
+
+
+def test_tiny_trie_scores_from_the_pipeline_match_each_prefix_run_whole():
+    """Trie-scored AI.CLASSIFY end to end with this package's label trie
+    (quail_amd.labels: read nodes, paths, the suffix tokens, tree_scores):
+    the label-path pack through the tree pipeline, its read rows' log-softmax
+    over the label tokens, and tree_scores over them, against the same
+    scores from the oracle's final rows of each read node's prompt (document
+    + cue + node tokens) run whole: every label's log probability within
+    0.05 and the same best label."""
+    from oracle import qwen3_ref as ref
+    from quail_amd import labels as qlabels
+    from quail_amd.arena import KVArena
+    from quail_amd.chunk import InputStaging, pack_chunk, upload
+    from quail_amd.qwen3 import Qwen3Pipeline
+    from tests.helpers import ref_model
+
+    cfg = CONFIGS["tiny"]
+    model = build_synthetic(cfg, seed=8, device="cuda", gen_device="cpu", norm_init="random")
+    wl = make_workload("tiny", seed=8)
+    doc = list(wl.prompts[0][:-1])
+    cue = int(wl.prompts[0][-1])
+    labels = ((10,), (20, 21, 22), (20, 25, 26, 27, 28), (30, 31, 32), (30, 31, 33), (30,))
+    arena = KVArena(cfg.layers, 256, 16, cfg.kv_heads, cfg.head_dim)
+    pipe = Qwen3Pipeline(model, arena)
+    heads = (cfg.heads, cfg.kv_heads, cfg.head_dim)
+    arena.activate("doc", len(doc))
+    first = pack_chunk(arena, [dict(key="doc", prefix=doc, f=len(doc), suffixes=[[cue]])],
+                       attention_mode="tree", attention_heads=heads)
+    upload(first, InputStaging())
+    pipe.forward_chunk(first)
+    read = qlabels.read_nodes(labels)
+    paths = qlabels.trie_paths(labels, read)
+    mask = qlabels.path_reads(paths, read)
+    chunk = pack_chunk(arena, [dict(key="doc", prefix=None, f=len(doc),
+                                    suffixes=[qlabels.path_tokens(paths, cue)],
+                                    read_all_rows=True, paths=paths, read_mask=mask)],
+                       attention_mode="tree", attention_heads=heads)
+    upload(chunk, InputStaging())
+    got = pipe.forward_chunk(chunk).float().cpu()
+    nodes = [nd for ns, _, _ in paths for nd in ns]
+    prompts = [doc + [cue] + list(nd) for nd, m in zip(nodes, mask) if m]
+    want = ref.forward_documents(ref_model(model), prompts).float()
+    targets = sorted({t for ids in labels for t in ids})
+    head = model.lm_head.weight.float().cpu()[targets]
+
+    def scores(rows):
+        lp = torch.log_softmax(rows @ head.T, dim=-1).double().numpy()
+        return qlabels.tree_scores(labels, paths, targets, lp, read)
+
+    s_gpu, s_ref = scores(got), scores(want)
+    print("trie scores gpu", np.round(s_gpu, 4), "oracle", np.round(s_ref, 4))
+    assert np.all(np.isfinite(s_ref))
+    assert np.abs(s_gpu - s_ref).max() <= 0.05
+    assert int(np.argmax(s_gpu)) == int(np.argmax(s_ref))
