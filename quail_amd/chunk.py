@@ -272,10 +272,12 @@ def _pack_tree(arena, groups, *, timing=None, attention_heads=None):
     written to the key's pages first (kv_src -> kv_dst), so a later suffix
     or a child can read them.
 
-    Label paths (`paths`, one suffix holding the trie paths back to back,
-    chunk.py:765-786): each path is its own call A segment at positions
-    f + its first node's depth onward, every path row reads the document's
-    pages in call B, and a path's rows read the rows above its first node
+    Label paths (`paths`, one suffix of a paged document holding the trie
+    paths back to back, chunk.py:765-786; the document's rows may be in the
+    same pack, as their own segment, never `whole` or `stacked`): each path
+    is its own call A segment at positions f + its first node's depth
+    onward, every path row reads the document's pages in call B, and a
+    path's rows read the rows above its first node
     (leading rows of earlier paths, its `gathers`) in call C,
     `reads["nodes"]` (chunk.py:894-907). `read_mask` marks the one
     suffix's rows that feed the answer (chunk.py:726-741).
@@ -305,9 +307,13 @@ def _pack_tree(arena, groups, *, timing=None, attention_heads=None):
         row0 = n_tok
         sids, slen = _as_suffixes(g["suffixes"])
         n = len(slen)
+        paths = g.get("paths")
         borrowing = fresh and start > 0
-        stacked = borrowing and n == 1 and g.get("read_key") is not None
-        whole = fresh and paged and not start and n == 1 and bool(g.get("single"))
+        # a group with label paths keeps its prefix rows a segment of their
+        # own (its path rows read them from the pages, as a kept document's)
+        stacked = borrowing and n == 1 and g.get("read_key") is not None and paths is None
+        whole = (fresh and paged and not start and n == 1 and bool(g.get("single"))
+                 and paths is None)
         prefix_len = 0
         if fresh:
             if not paged and n > 1:
@@ -339,7 +345,6 @@ def _pack_tree(arena, groups, *, timing=None, attention_heads=None):
         total = int(slen.sum())
         ends = np.cumsum(slen)
         begins = ends - slen
-        paths = g.get("paths")
         if n:
             id_parts.append(sids)
             read, per_answer, several = _suffix_reads(g, s_row0, slen)
@@ -347,8 +352,8 @@ def _pack_tree(arena, groups, *, timing=None, attention_heads=None):
             rows_per_answer.append(per_answer)
             multi = multi or several
             if paths is not None:
-                if n != 1 or not g.get("read_all_rows") or fresh:
-                    raise ValueError(f"group {key!r}: paths pack one suffix of a resident "
+                if n != 1 or not g.get("read_all_rows") or not paged:
+                    raise ValueError(f"group {key!r}: paths pack one suffix of a paged "
                                      f"document, every row read")
                 lengths = np.asarray([len(nodes) for nodes, _, _ in paths], dtype=np.int64)
                 if int(lengths.sum()) != total:

@@ -9,11 +9,16 @@ pass (stream order keeps later writers behind it); a document's pages are
 freed once its answer is read, or when its last borrower is admitted.
 Documents longer than a pack are prefilled in pieces (admission), and a
 pack that finds the arena full reads the answers in flight, evicts
-retained KV, or runs as two halves.
+retained KV, or runs as two halves. Under tree attention a stage may
+carry label paths (trie-scored AI.CLASSIFY): each document's one suffix
+is then the paths' tokens, every read row goes to the readout, and
+readout.AsyncTrieScores turns them into label scores.
 """
 
 import time
 from collections import deque
+
+import numpy as np
 
 from quail_amd.admission import StageAdmission
 from quail_amd.chunk import ArenaFullError, InputStaging, pack_chunk, upload
@@ -22,7 +27,12 @@ from quail_amd.prefix import PrefixIndex
 
 class StageRun:
     def __init__(self, pipeline, arena, readout, prefixes, suffixes, chunk_budget,
-                 use_tree=True, staging=None, attention_mode="unified"):
+                 use_tree=True, staging=None, attention_mode="unified", label_paths=None):
+        if label_paths is not None and attention_mode != "tree":
+            raise ValueError("label paths run under attention_mode='tree'")
+        # (paths, read_mask) of trie-scored AI.CLASSIFY (label_stages.py:93-99):
+        # every document's one suffix holds the paths' tokens
+        self.label_paths = label_paths
         self.pipeline = pipeline
         self.arena = arena
         self.readout = readout
@@ -117,7 +127,13 @@ class StageRun:
                 self.arena.free_key(key)
         # prefill pieces write KV and read no answer
         answered = [(d, len(g["suffixes"])) for d, g in groups if len(g["suffixes"])]
-        self._inflight.append((self.readout.submit(normed), answered))
+        per_answer = chunk.rows_per_answer
+        if per_answer is not None and len(per_answer) and int(np.max(per_answer)) > 1:
+            # several read rows per answer (label paths, read_all_rows)
+            handle = self.readout.submit(normed, rows_per_answer=[int(r) for r in per_answer])
+        else:
+            handle = self.readout.submit(normed)
+        self._inflight.append((handle, answered))
         if len(self._inflight) > 1:
             self._drain()
 
@@ -130,6 +146,10 @@ class StageRun:
             # pages stacked with its siblings (stage_executor.py:772-774)
             specs = [dict(g, read_key=g.get("borrow_key") if g.get("start") else None,
                           single=len(g["suffixes"]) == 1) for g in specs]
+            if self.label_paths is not None:
+                paths, mask = self.label_paths
+                specs = [dict(g, paths=paths, read_mask=mask, read_all_rows=True)
+                         if len(g["suffixes"]) else g for g in specs]
         chunk = pack_chunk(self.arena, specs, attention_mode=self.attention_mode,
                            attention_heads=(engine.num_q_heads, engine.num_kv_heads,
                                             engine.head_dim))

@@ -236,3 +236,47 @@ class AsyncLabelLogprobs(_HostReadout):
         elif rows_per_answer is not None and any(r != 1 for r in rows_per_answer):
             raise ValueError("this readout holds one row per answer")
         return self._copy(values)
+
+class AsyncTrieScores:
+    """Trie-scored AI.CLASSIFY (the trie_tree rule, label_stages.py:93-99):
+    each document's read path rows through AsyncLabelLogprobs (log
+    probabilities of the label tokens over the full vocabulary with
+    normalize, or raw logits), then quail_amd.labels.tree_scores: one log
+    probability per label, in label order.
+
+    Args:
+        head: The model's output head, (vocabulary, hidden).
+        label_ids: One token id sequence per label.
+        paths, read: From quail_amd.labels (trie_paths, read_nodes); read
+            None reads every path row.
+        targets: The readout's token ids; None takes the labels' tokens.
+    """
+
+    def __init__(self, head, label_ids, paths, read=None, targets=None, normalize=True):
+        from quail_amd import labels
+
+        self.trie = labels.LabelTrie(label_ids)
+        self.paths, self.read = paths, read
+        self.targets = (sorted({t for ids in self.trie.labels for t in ids})
+                        if targets is None else [int(t) for t in targets])
+        self.read_mask = labels.path_reads(paths, read)
+        rows = sum(self.read_mask)
+        self.logprobs = AsyncLabelLogprobs(head, self.targets, rows=max(rows, 2),
+                                           normalize=normalize)
+        self.rows = rows
+
+    def submit(self, normed, rows_per_answer=None):
+        """normed: the pack's read rows, each answer's `rows` in path order."""
+        if rows_per_answer is None:
+            if normed.shape[0] % self.rows:
+                raise ValueError(f"{normed.shape[0]} rows for answers of {self.rows}")
+            rows_per_answer = [self.rows] * (normed.shape[0] // self.rows)
+        if any(r != self.rows for r in rows_per_answer):
+            raise ValueError(f"each answer reads the {self.rows} path rows")
+        return self.logprobs.submit(normed, rows_per_answer=rows_per_answer)
+
+    def result(self, handle):
+        values = self.logprobs.result(handle)
+        return [self.trie.scores(self.paths, self.targets, v[:self.rows], self.read)
+                for v in values]
+

@@ -516,3 +516,61 @@ def test_tiny_trie_scores_from_the_pipeline_match_each_prefix_run_whole():
     assert np.all(np.isfinite(s_ref))
     assert np.abs(s_gpu - s_ref).max() <= 0.05
     assert int(np.argmax(s_gpu)) == int(np.argmax(s_ref))
+
+
+@pytest.mark.parametrize("labels", [((10,), (20, 21, 22), (20, 25, 26, 27, 28), (30, 31, 32),
+                                     (30, 31, 33), (30,)), ((11,), (12,), (13,))])
+def test_trie_scored_stage_through_the_stage_driver(labels):
+    """A trie-scored AI.CLASSIFY stage through StageRun (tree attention,
+    label paths on every document, documents that share a prefix borrowing
+    its pages) and the AsyncTrieScores readout: each document's label log
+    probabilities against tree_scores over the oracle's rows of its read
+    nodes' prompts (document + cue + node tokens) run whole, log-softmax
+    over the full vocabulary: the same best label, and each label within
+    0.05 per term its score sums (its read nodes' log probabilities, and
+    the share its label extensions take, each carrying the tiny model's
+    FP8 noise). One-token labels read a single row per document."""
+    from oracle import qwen3_ref as ref
+    from quail_amd import labels as qlabels
+    from quail_amd.arena import KVArena
+    from quail_amd.executor import StageRun
+    from quail_amd.qwen3 import Qwen3Pipeline
+    from quail_amd.readout import AsyncTrieScores
+    from tests.helpers import ref_model
+
+    cfg = CONFIGS["tiny"]
+    model = build_synthetic(cfg, seed=9, device="cuda", gen_device="cpu", norm_init="random")
+    wl = make_workload("tiny", seed=9)
+    docs = [list(p[:-1]) for p in wl.prompts[:6]]
+    cues = [int(p[-1]) for p in wl.prompts[:6]]
+    read = qlabels.read_nodes(labels)
+    paths = qlabels.trie_paths(labels, read)
+    mask = qlabels.path_reads(paths, read)
+    arena = KVArena(cfg.layers, 256, 16, cfg.kv_heads, cfg.head_dim)
+    pipe = Qwen3Pipeline(model, arena)
+    readout = AsyncTrieScores(model.lm_head.weight, labels, paths, read)
+    run = StageRun(pipe, arena, readout, docs,
+                   [[qlabels.path_tokens(paths, c)] for c in cues], 512,
+                   attention_mode="tree", label_paths=(paths, mask))
+    got = run.run()
+    torch.cuda.synchronize()
+    assert run.stats["borrowed_tokens"] > 0
+    head = model.lm_head.weight.float().cpu()
+    nodes = [nd for ns, _, _ in paths for nd in ns]
+    ends = {tuple(ids) for ids in labels}
+    terms = np.array([sum(ids[:k] in read for k in range(len(ids)))
+                      + any(o != ids and o[:len(ids)] == ids for o in ends)
+                      for ids in map(tuple, labels)])
+    worst = 0.0
+    for d, (doc, cue) in enumerate(zip(docs, cues)):
+        prompts = [doc + [cue] + list(nd) for nd, m in zip(nodes, mask) if m]
+        rows = ref.forward_documents(ref_model(model), prompts).float()
+        lp = torch.log_softmax(rows @ head.T, dim=-1)[:, readout.targets].double().numpy()
+        want = qlabels.tree_scores(labels, paths, readout.targets, lp, read)
+        diff = np.abs(got[d] - want)
+        print(f"document {d}: |diff| per label {np.round(diff, 4)} (terms {terms.tolist()})")
+        worst = max(worst, float((diff / terms).max()))
+        assert np.all(np.isfinite(want))
+        assert int(np.argmax(got[d])) == int(np.argmax(want)), (d, got[d], want)
+    print(f"trie-scored stage, {len(docs)} documents: worst |diff| per term {worst:.4f}")
+    assert worst <= 0.05

@@ -225,6 +225,49 @@ def test_label_paths_read_their_document_ancestors_and_path(labels, every_node):
                    attention_mode="tree")
 
 
+@pytest.mark.parametrize("labels", [LABELS, SPLIT])
+@pytest.mark.parametrize("borrow", [0, 32])
+def test_label_paths_with_their_document_in_the_same_pack(labels, borrow):
+    """A document packed fresh together with its label paths (one group,
+    as the stage driver packs it; reference chunk.py:765-786): its rows are
+    a causal segment of their own written to its pages, reading a lender's
+    first `borrow` tokens from the lender's pages, and each path row reads
+    exactly the document, the cue and its trie node's tokens. A read_key
+    or `single` on the group does not stack or merge it."""
+    arena = plain_arena()
+    pool = PoolModel()
+    doc = list(range(100, 137))
+    prompts = {"doc": doc}
+    if borrow:
+        parent = doc[:borrow] + [5, 6, 7]
+        prompts["parent"] = parent
+        arena.activate("parent", len(parent))
+        first = pack_chunk(arena, [dict(key="parent", prefix=parent, f=len(parent),
+                                        suffixes=[])], attention_mode="tree")
+        check_pack_tree(first, 16, pool, prompts.__getitem__)
+    arena.activate("doc", len(doc), borrow=("parent", borrow) if borrow else None)
+    read = read_nodes(labels)
+    paths = trie_paths(labels, read)
+    cue = 7
+    tokens = path_tokens(paths, cue)
+    mask = path_reads(paths, read)
+    group = dict(key="doc", prefix=doc[borrow:], f=len(doc), start=borrow, suffixes=[tokens],
+                 read_all_rows=True, paths=paths, read_mask=mask, single=True,
+                 read_key="parent" if borrow else None)
+    chunk = pack_chunk(arena, [group], attention_mode="tree")
+    contexts = path_contexts(paths, cue, doc)
+    s_row0 = len(doc) - borrow
+
+    def context(key, r):
+        return None if r < s_row0 else contexts[r - s_row0]
+
+    assert check_pack_tree(chunk, 16, pool, prompts.__getitem__, context) == s_row0 + len(tokens)
+    assert chunk.final_indices.tolist() == [s_row0 + i for i, m in enumerate(mask) if m]
+    assert chunk.rows_per_answer.tolist() == [sum(mask)]
+    with pytest.raises(ValueError, match="paths pack one suffix"):
+        pack_chunk(arena, [dict(group, read_all_rows=False)], attention_mode="tree")
+
+
 @pytest.mark.parametrize("mode", ["unified", "tree"])
 def test_read_rows_and_read_mask_pick_the_answer_rows(mode):
     """read_rows: the last read_rows[j] rows of suffix j answer
