@@ -45,22 +45,18 @@ int qx_device_is_gfx950(void);
  * Replaces Engine.gemm -> DeepGEMM fp8_gemm_nt((A, sA), (W, sW), C)
  * (quail/backends/quail/executor/attention.py:479-490); weight scales are the
  * checkpoint's weight_scale_inv (attention.py:471-477).
- * K and N multiples of 128 (N of 256 for configs 0, 1, 3, 7, 10, 13-16,
- * 18-22). config selects the tile shape, tokens x weights, and the K depth
- * of a pipeline stage: 0: 256x256 (8 waves), 1: 256x256, 2: 128x128,
- * 3: 128x256, 4-6: 256x128 (3, 2, 4 stages of 64 K); 7-9: 256x256, 256x128,
- * 128x128 with fragments prefetched from LDS; 10-12: 256x256 (8 waves),
- * 256x128, 128x128 with two stages of 128 K; 13: 10 with L2 warm-up loads;
- * 14, 15: 128x256 (8 waves, two arrangements) with two stages of 128 K;
- * 16, 17: persistent 256x256 and 256x128 (one workgroup per CU);
- * 18, 19: 256x256 with two wave groups a phase apart (group 0 loads / every
- * wave loads); 20: as 19 over four stages of 64 K; 21: 10 with each
- * block's rescale issued four MFMAs away from the MFMAs on either side of
- * it; 22: 256x256 tiles walked by one persistent workgroup per CU, the
- * next tile's first block loaded during the last block of the current one
- * and the epilogue staged in two passes through one stage buffer. Every
- * config computes
- * each element with the same operations in the same order: the results are
+ * K and N multiples of 128. config selects the tile shape, tokens x weights,
+ * all with two pipeline stages of one 128-K scale block each:
+ * 10: 256x256 tiles, 8 waves, one workgroup per tile (N a multiple of 256);
+ * 11: 256x128 tiles, 4 waves (any N);
+ * 12: 256x320 tiles, 8 waves (N a multiple of 320: whole waves of tiles on
+ *     256 CUs where N = 2560 and M is a multiple of 8192 or just under one);
+ * 22: 256x256 tiles walked by one persistent workgroup per CU, the next
+ *     tile's first block loaded during the last block of the current one
+ *     and the epilogue staged in two passes through one stage buffer (falls
+ *     back to 10 with an odd number of 128-K blocks or too few tiles).
+ * Every config computes each element with the same operations in the same
+ * order: the results are
  * bit-identical.
  */
 int qx_gemm_fp8_blockscaled(const void* A, const float* sA, const void* W, const float* sW,

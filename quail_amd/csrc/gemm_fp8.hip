@@ -131,7 +131,6 @@ struct Cfg128 {
   static_assert(kTN >= 1 && kTM >= 1, "wave tile");
   static_assert(BM % (8 * kWaves) == 0 && BN % (8 * kWaves) == 0, "slabs");
   static_assert(kSaPerWave >= 1 && kSaPerWave <= 64 && BM % kWaves == 0, "scale loads");
-  static_assert(128 % (BN / WAVES_N) == 0 || (BN / WAVES_N) == 128, "weight scale block");
   static_assert(kLds <= 160 * 1024, "LDS");
   static_assert(STAGES >= 2 && (STAGES - 2) * kOpsPerStage < 64, "stages");
 };
@@ -257,6 +256,8 @@ __global__ __launch_bounds__(64 * WAVES_N * WAVES_M) void gemm_fp8_k128_kernel(
     int64_t q_ld, float* __restrict__ Qs, int64_t qs_ld) {
   using Cfg = Cfg128<BM, BN, WAVES_N, WAVES_M, STAGES>;
   constexpr int TN = Cfg::kTN, TM = Cfg::kTM;
+  static_assert(128 % (BN / WAVES_N) == 0 || (BN / WAVES_N) == 128,
+                "a wave's weight rows lie in one scale block");
   // vector loads per stage, not counting the weight-scale load (a scalar
   // load where the compiler sees its uniform address; undercounting only
   // makes a wait stricter)
@@ -410,6 +411,283 @@ int launch128_swiglu(const void* A, const float* sA, const void* W, const float*
                      dim3(tiles_m * tiles_n), dim3(Cfg::kThreads), 0, stream, (const uint8_t*)A,
                      sA, (const uint8_t*)W, sW, nullptr, M, N, K, lda, (int64_t)0, sa_ld, tiles_m,
                      tiles_n, 4, (uint8_t*)Q, q_ld, Qs, qs_ld);
+  QX_LAUNCH_STATUS();
+}
+
+// ---- 256 x 320 tiles: whole waves where N = 2560 -----------------------------
+// Qwen3-4B's o_proj and down projections (N = 2560) make ceil(M/256) x 10
+// tiles of 256 x 256: 2.5 waves of the 256 CUs for a 16k-row pack, 1.25 at
+// M = 8192, the last one half empty. 256 x 320 tiles make ceil(M/256) x 8:
+// exactly 2 waves (1 at M = 8192), each tile 1.25x the work and 10% fewer
+// operand bytes per FLOP. Each wave covers 160 weight rows, which straddle
+// two 128-row scale blocks: its 32-row tiles a < split lie in the first,
+// the rest in the second, and the accumulator rescale keeps one s_prev per
+// block. Every element sees the same operations in the same order as with
+// 256 x 256 tiles (s = sA * sW, acc *= s_prev / s, acc * s_last in the
+// epilogue; a block whose weight scale is 0 skipped), so the results are
+// bit-identical. The bf16 tile (256 x 640 B) does not fit the stage buffers
+// at once and leaves in two passes of 128 rows.
+// Zero rows [r0, r1) of 128 B at rows (a weight block whose scale is 0).
+__device__ __noinline__ void zero_weight_rows(uint8_t* rows, int r0, int r1, int lane) {
+  for (int r = r0; r < r1; r += 8)
+    *reinterpret_cast<v4i*>(rows + (r + (lane >> 3)) * 128 + (lane & 7) * 16) = v4i{0, 0, 0, 0};
+  __builtin_amdgcn_s_waitcnt((15) | (7 << 4) | (0 << 8) | (3 << 14));  // lgkmcnt(0)
+}
+
+// The K loop and epilogue of one 256 x 320 tile for a wave whose first SPLIT
+// 32-row weight tiles lie in its first scale block (SPLIT is fixed per wave
+// for the whole tile, so the selection is resolved at compile time).
+template <int STAGES, int SPLIT>
+__device__ __forceinline__ void n320_tile(
+    uint8_t* smem, const uint8_t* __restrict__ A, const float* __restrict__ sA,
+    const uint8_t* __restrict__ W, const float* __restrict__ sw_row0, uint16_t* __restrict__ C,
+    int M, int N, int K, int64_t lda, int64_t ldc, int64_t sa_ld, int m0, int n0, int lane,
+    int wave) {
+  constexpr int BM = 256, BN = 320, WAVES_N = 2, WAVES_M = 4;
+  using Cfg = Cfg128<BM, BN, WAVES_N, WAVES_M, STAGES>;
+  constexpr int TN = Cfg::kTN, TM = Cfg::kTM;
+  static_assert(TN == 5 && TM == 2 && SPLIT >= 1 && SPLIT <= 4, "160 x 64 wave tiles");
+  constexpr int kOps = Cfg::kOpsPerStage;
+  const int wn = wave % WAVES_N;
+  const int wm = wave / WAVES_N;
+  const int KT = K >> 7;
+  const float* sw_row1 = sw_row0 + KT;
+
+  v16f acc[TN][TM];
+#pragma unroll
+  for (int a = 0; a < TN; ++a)
+#pragma unroll
+    for (int b = 0; b < TM; ++b)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[a][b][e] = 0.0f;
+
+  // 32-bit per-lane offsets of the wave's slab rows within the tile (one
+  // register per slab instead of a 64-bit address; the launcher checks that
+  // 256 * lda and 320 * K fit), added to the block's wave-uniform base
+  uint32_t a_off[Cfg::kASlabs], w_off[Cfg::kWSlabs];
+  {
+    const int r_in = lane >> 3, p = lane & 7;
+#pragma unroll
+    for (int j = 0; j < Cfg::kASlabs; ++j) {
+      const int row = (wave * Cfg::kASlabs + j) * 8 + r_in;
+      const int grow = min(m0 + row, M - 1);  // rows past M repeat the last one
+      a_off[j] = (uint32_t)((grow - m0) * lda + (p ^ swz128(row)) * 16);
+    }
+#pragma unroll
+    for (int j = 0; j < Cfg::kWSlabs; ++j) {
+      const int row = (wave * Cfg::kWSlabs + j) * 8 + r_in;  // n0 + row < N
+      w_off[j] = (uint32_t)((int64_t)row * K + (p ^ swz128(row)) * 16);
+    }
+  }
+  const uint8_t* a_tile = A + (int64_t)m0 * lda;
+  const uint8_t* w_tile = W + (int64_t)n0 * K;
+
+  float sw_ring[STAGES][2];
+  auto issue = [&](int kb, int stage) {
+    uint8_t* buf = smem + stage * Cfg::kStage;
+    const uint8_t* a_blk = a_tile + kb * 128;
+    const uint8_t* w_blk = w_tile + kb * 128;
+#pragma unroll
+    for (int j = 0; j < Cfg::kASlabs; ++j)
+      __builtin_amdgcn_global_load_lds((const void*)(a_blk + a_off[j]),
+                                       (lds_void*)(buf + (wave * Cfg::kASlabs + j) * 1024), 16, 0,
+                                       kOperandLoadPolicy);
+#pragma unroll
+    for (int j = 0; j < Cfg::kWSlabs; ++j)
+      __builtin_amdgcn_global_load_lds(
+          (const void*)(w_blk + w_off[j]),
+          (lds_void*)(buf + Cfg::kABytes + (wave * Cfg::kWSlabs + j) * 1024), 16, 0,
+          kOperandLoadPolicy);
+    {
+      const int t = min(m0 + wave * Cfg::kSaPerWave + lane % Cfg::kSaPerWave, M - 1);
+      __builtin_amdgcn_global_load_lds((const void*)(sA + (int64_t)kb * sa_ld + t),
+                                       (lds_void*)(buf + Cfg::kABytes + Cfg::kWBytes + wave * 256),
+                                       4, 0, 0);
+    }
+    sw_ring[stage][0] = __builtin_nontemporal_load(sw_row0 + kb);
+    sw_ring[stage][1] = __builtin_nontemporal_load(sw_row1 + kb);
+  };
+#pragma unroll
+  for (int st = 0; st < STAGES - 1; ++st)
+    if (st < KT) issue(st, st);
+
+  float s_prev[2][TM];
+#pragma unroll
+  for (int b = 0; b < TM; ++b) s_prev[0][b] = s_prev[1][b] = 0.0f;
+
+  for (int base = 0; base < KT; base += STAGES) {
+#pragma unroll
+    for (int stage = 0; stage < STAGES; ++stage) {
+      const int kb = base + stage;
+      if (kb < KT) {
+        if (kb + STAGES - 2 < KT) {
+          wait_vmcnt<(STAGES - 2) * kOps>();
+        } else {
+          wait_vmcnt<0>();
+        }
+        lds_barrier();
+        if (kb + STAGES - 1 < KT) issue(kb + STAGES - 1, (stage + STAGES - 1) % STAGES);
+        const float sw0 =
+            __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(sw_ring[stage][0])));
+        const float sw1 =
+            __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(sw_ring[stage][1])));
+        const bool live0 = sw0 != 0.0f, live1 = sw1 != 0.0f;  // wave-uniform
+        uint8_t* a_lds = smem + stage * Cfg::kStage;
+        uint8_t* w_lds = a_lds + Cfg::kABytes;
+        if (!(live0 && live1)) {
+          // A block whose weight scale is 0 adds nothing: the wave zeroes
+          // its weight rows of that block in this stage (the other waves
+          // reading them write the same zeros), its tiles' accumulators are
+          // rescaled by exactly 1 and keep their s_prev, and their MFMAs add
+          // +0 to sums that start at +0: bit for bit what skipping does.
+          // Rare (real checkpoints have no all-zero weight blocks).
+          // (out of line: the main loop keeps its registers)
+          zero_weight_rows(w_lds + wn * TN * 32 * 128, live0 ? SPLIT * 32 : 0,
+                           live1 ? SPLIT * 32 : TN * 32, lane);
+        }
+        const float* sa_lds = reinterpret_cast<const float*>(a_lds + Cfg::kABytes + Cfg::kWBytes);
+#pragma unroll
+        for (int b = 0; b < TM; ++b) {
+          const int row = wm * TM * 32 + b * 32 + (lane & 31);
+          const float sa = sa_lds[(row / Cfg::kSaPerWave) * 64 + row % Cfg::kSaPerWave];
+          // the same expressions as the 256 x 256 kernel, per scale block
+          const float s0 = sa * sw0, s1 = sa * sw1;
+          const float q0 = live0 ? s_prev[0][b] / s0 : 1.0f;
+          const float q1 = live1 ? s_prev[1][b] / s1 : 1.0f;
+#pragma unroll
+          for (int a = 0; a < TN; ++a) {
+            const float r = a < SPLIT ? q0 : q1;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[a][b][e] *= r;
+          }
+          s_prev[0][b] = live0 ? s0 : s_prev[0][b];
+          s_prev[1][b] = live1 ? s1 : s_prev[1][b];
+        }
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          // 160 accumulators leave room for one K half's fragments, not two:
+          // the second half's reads wait until the first half's MFMAs issue
+          if (h) __builtin_amdgcn_sched_barrier(0);
+          v8i wf[TN], af[TM];
+#pragma unroll
+          for (int a = 0; a < TN; ++a)
+            wf[a] = read_frag128(w_lds, wn * TN * 32 + a * 32 + (lane & 31), h, lane);
+#pragma unroll
+          for (int b = 0; b < TM; ++b)
+            af[b] = read_frag128(a_lds, wm * TM * 32 + b * 32 + (lane & 31), h, lane);
+#pragma unroll
+          for (int a = 0; a < TN; ++a)
+#pragma unroll
+            for (int b = 0; b < TM; ++b)
+              acc[a][b] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+                  wf[a], af[b], acc[a][b], 0, 0, 0, 0, 0, 0);
+        }
+      }
+    }
+  }
+
+  // epilogue: two passes of 128 tile rows (waves wm = 2p, 2p + 1 stage
+  // theirs), rows padded by 16 bytes, written back 16 bytes per lane,
+  // non-temporal (as the 256 x 256 kernel's)
+  constexpr int kRowBytes = BN * 2 + 16;
+  constexpr int kPassRows = BM / 2;
+  constexpr int kChunks = BN / 8;
+  static_assert(kPassRows * kRowBytes <= Cfg::kLds, "an epilogue pass fits the stage buffers");
+  static_assert((kPassRows * kChunks) % Cfg::kThreads == 0, "epilogue chunks");
+  const bool wide = ((ldc & 7) == 0) && ((reinterpret_cast<uintptr_t>(C) & 15) == 0);
+#pragma unroll
+  for (int pass = 0; pass < 2; ++pass) {
+    __syncthreads();  // the operands (pass 0) or the previous pass's rows are consumed
+    if ((wm >> 1) == pass) {
+#pragma unroll
+      for (int b = 0; b < TM; ++b) {
+        const int row = (wm & 1) * TM * 32 + b * 32 + (lane & 31);
+        uint8_t* lrow = smem + row * kRowBytes;
+#pragma unroll
+        for (int a = 0; a < TN; ++a) {
+          const float s = a < SPLIT ? s_prev[0][b] : s_prev[1][b];
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            const int off = (wn * TN * 32 + a * 32 + (lane >> 5) * 4 + g * 8) * 2;
+            uint2 v;
+            v.x = pack2_bf16(acc[a][b][g * 4 + 0] * s, acc[a][b][g * 4 + 1] * s);
+            v.y = pack2_bf16(acc[a][b][g * 4 + 2] * s, acc[a][b][g * 4 + 3] * s);
+            *reinterpret_cast<uint2*>(lrow + off) = v;
+          }
+        }
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < kPassRows * kChunks / Cfg::kThreads; ++i) {
+      const int idx = i * Cfg::kThreads + threadIdx.x;
+      const int row = idx / kChunks, c = idx % kChunks;
+      const int m = m0 + pass * kPassRows + row;
+      const uint4 v = *reinterpret_cast<const uint4*>(smem + row * kRowBytes + c * 16);
+      if (m < M) {
+        uint16_t* dst = C + (int64_t)m * ldc + n0 + c * 8;
+        if (wide) {
+          const v4i w = {(int)v.x, (int)v.y, (int)v.z, (int)v.w};
+          __builtin_nontemporal_store(w, reinterpret_cast<v4i*>(dst));
+        } else {
+          reinterpret_cast<uint2*>(dst)[0] = make_uint2(v.x, v.y);
+          reinterpret_cast<uint2*>(dst)[1] = make_uint2(v.z, v.w);
+        }
+      }
+    }
+  }
+}
+
+template <int STAGES>
+__global__ __launch_bounds__(512) void gemm_fp8_n320_kernel(
+    const uint8_t* __restrict__ A, const float* __restrict__ sA, const uint8_t* __restrict__ W,
+    const float* __restrict__ sW, uint16_t* __restrict__ C, int M, int N, int K, int64_t lda,
+    int64_t ldc, int64_t sa_ld, int tiles_m, int tiles_n, int group_m) {
+  using Cfg = Cfg128<256, 320, 2, 4, STAGES>;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[Cfg::kLds];
+  const int total = tiles_m * tiles_n;
+  int id = blockIdx.x;
+  {
+    const int per = (total + 7) / 8;
+    const int xcd = id & 7, local = id >> 3;
+    const int full = total - (per - 1) * 8;
+    id = xcd < full ? xcd * per + local : full * per + (xcd - full) * (per - 1) + local;
+  }
+  const int width = group_m * tiles_n;
+  const int group = id / width;
+  const int first_m = group * group_m;
+  const int gsize = min(tiles_m - first_m, group_m);
+  const int tile_m = first_m + (id % width) % gsize;
+  const int tile_n = (id % width) / gsize;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int m0 = tile_m * 256;
+  const int n0 = tile_n * 320;
+  // the wave's weight rows [wrow0, wrow0 + 160): tiles a < split lie in
+  // scale block wrow0 / 128, the others in the next one; wrow0 % 128 is 0
+  // or 32 (even tile_n) and 64 or 96 (odd), so split is 4, 3, 2 or 1
+  const int wrow0 = n0 + (wave % 2) * 160;
+  const int split = (128 - (wrow0 & 127)) >> 5;
+  const float* sw_row0 = sW + (int64_t)(wrow0 >> 7) * (K >> 7);
+#define QX_N320_TILE(S)                                                                          \
+  n320_tile<STAGES, S>(smem, A, sA, W, sw_row0, C, M, N, K, lda, ldc, sa_ld, m0, n0, lane, wave)
+  switch (split) {
+    case 4: QX_N320_TILE(4); break;
+    case 3: QX_N320_TILE(3); break;
+    case 2: QX_N320_TILE(2); break;
+    default: QX_N320_TILE(1); break;
+  }
+#undef QX_N320_TILE
+}
+
+int launch_n320(const void* A, const float* sA, const void* W, const float* sW, void* C, int M,
+                int N, int K, int64_t lda, int64_t ldc, int64_t sa_ld, hipStream_t stream) {
+  using Cfg = Cfg128<256, 320, 2, 4, 2>;
+  const int tiles_m = (M + 255) / 256;
+  const int tiles_n = N / 320;
+  hipLaunchKernelGGL((gemm_fp8_n320_kernel<2>), dim3(tiles_m * tiles_n), dim3(Cfg::kThreads), 0,
+                     stream, (const uint8_t*)A, sA, (const uint8_t*)W, sW, (uint16_t*)C, M, N, K,
+                     lda, ldc, sa_ld, tiles_m, tiles_n, 4);
   QX_LAUNCH_STATUS();
 }
 
@@ -708,7 +986,8 @@ extern "C" {
 // bit, since each output element sums the same products in the same order:
 // 10: 256 x 256 tiles, 8 waves, two 128-K stages, one workgroup per tile
 // (widths that are a multiple of 256); 11: 256 x 128 tiles, 4 waves (any
-// width that is a multiple of 128); 22: config 10's tiles on a persistent
+// width that is a multiple of 128); 12: 256 x 320 tiles, 8 waves (widths
+// that are a multiple of 320: whole waves of tiles where N = 2560); 22: config 10's tiles on a persistent
 // grid with the K pipeline running across tiles (falls back to 10 when there
 // are too few tiles or an odd number of 128-K blocks).
 // gate_up projection + SiLU-gated product + per-128 FP8 quant in one launch:
@@ -763,12 +1042,18 @@ int qx_gemm_fp8_blockscaled(const void* A, const float* sA, const void* W, const
     case 11:
       return qx::launch128<256, 128, 1, 4, 2>(A, sA, W, sW, C, m, n, k, lda, ldc, sa_ld, 8,
                                               stream);
+    case 12:
+      QX_CHECK(n % 320 == 0, "gemm config 12 needs N %% 320 == 0 (N=%d)", n);
+      QX_CHECK(256 * lda < (1LL << 32) && 320LL * k < (1LL << 32),
+               "gemm config 12: a tile's rows must span less than 4 GiB (lda=%lld, K=%d)",
+               (long long)lda, k);
+      return qx::launch_n320(A, sA, W, sW, C, m, n, k, lda, ldc, sa_ld, stream);
     case 22:
       QX_CHECK(n % 256 == 0, "gemm config 22 needs N %% 256 == 0 (N=%d)", n);
       return qx::launch128q<false>(A, sA, W, sW, C, m, n, k, lda, ldc, sa_ld, nullptr, 0,
                                    nullptr, 0, stream);
     default:
-      QX_CHECK(false, "gemm: unknown config %d (10, 11 or 22)", config);
+      QX_CHECK(false, "gemm: unknown config %d (10, 11, 12 or 22)", config);
   }
 }
 

@@ -50,15 +50,38 @@ def _stream():
     return torch.cuda.current_stream().cuda_stream
 
 
+GEMM_WIDE_TILE_CONFIG = 12
+
+
 def gemm_config(n: int, k: int, m: int) -> int:
     forced = os.environ.get(GEMM_CONFIG_ENV)
     if forced is not None:
         return int(forced)
+    if n % 320 == 0 and _wide_tiles_fill_better(n, m):
+        return GEMM_WIDE_TILE_CONFIG
     if n % 256:
         return GEMM_ODD_WIDTH_CONFIG
     if _whole_waves(n, k, m):
         return GEMM_WHOLE_WAVES_CONFIG
     return GEMM_DEFAULT_CONFIG
+
+
+def _wave_cost(tiles: int) -> float:
+    """Time of `tiles` equal tiles on the CUs, in full-wave units: a partial
+    last wave of fraction f costs about 0.5 + 0.5 f of a full one (its tiles
+    run faster with fewer neighbours sharing the loads; measured ~0.75 at f
+    = 0.5 on the N = 2560 shapes)."""
+    full, rest = divmod(tiles, CUS)
+    return full + (0.5 + 0.5 * rest / CUS if rest else 0.0)
+
+
+def _wide_tiles_fill_better(n: int, m: int) -> bool:
+    """256 x 320 tiles (1.25x the work of 256 x 256) take fewer full-wave
+    units: N = 2560 at M = 8192 (256 tiles against 320) or a 16k-row pack
+    (512 against 640)."""
+    tm = -(-m // 256)
+    return 1.25 * _wave_cost(tm * (n // 320)) < (_wave_cost(tm * (n // 256)) if n % 256 == 0
+                                                 else float("inf"))
 
 
 def _whole_waves(n: int, k: int, m: int) -> bool:

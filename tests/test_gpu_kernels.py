@@ -98,12 +98,13 @@ def test_gemm_small_shapes_match_dequantized_matmul(m, n, k):
     _bf16_close(out, want)
 
 
-GEMM_CONFIGS = (10, 11, 22)
+GEMM_CONFIGS = (10, 11, 12, 22)
+GEMM_CONFIGS_256 = (10, 11, 22)   # N a multiple of 256 (config 12 needs 320)
 
 
 @pytest.mark.parametrize("config", GEMM_CONFIGS)
 def test_gemm_tile_configs_agree(config, monkeypatch):
-    q, s, wq, ws = _gemm_case(300, 512, 512, seed=9)
+    q, s, wq, ws = _gemm_case(300, 1280, 512, seed=9)
     monkeypatch.setenv("QUAIL_GEMM_CONFIG", str(config))
     out = _run_gemm(q, s, wq, ws)
     want = ref.gemm(q, s, ref.RefLinear(wq, ws))
@@ -114,7 +115,7 @@ def test_gemm_configs_are_bit_identical(monkeypatch):
     """Every tile configuration computes each element with the same
     operations in the same order (the engine picks configs by shape, and a
     row's result must not depend on it)."""
-    q, s, wq, ws = _gemm_case(700, 1024, 1024, seed=11)
+    q, s, wq, ws = _gemm_case(700, 1280, 1024, seed=11)
     outs = {}
     for config in GEMM_CONFIGS:
         monkeypatch.setenv("QUAIL_GEMM_CONFIG", str(config))
@@ -131,10 +132,10 @@ def test_gemm_persistent_config_with_several_tiles_per_workgroup(monkeypatch):
     configuration bit for bit, and the oracle to the bf16 tolerance."""
     q, s, wq, ws = _gemm_case(5000, 4096, 512, seed=13)
     outs = {}
-    for config in GEMM_CONFIGS:
+    for config in GEMM_CONFIGS_256:
         monkeypatch.setenv("QUAIL_GEMM_CONFIG", str(config))
         outs[config] = _run_gemm(q, s, wq, ws).cpu()
-    for config in GEMM_CONFIGS:
+    for config in GEMM_CONFIGS_256:
         assert torch.equal(outs[config], outs[10]), config
     _bf16_close(outs[22], ref.gemm(q, s, ref.RefLinear(wq, ws)))
 
@@ -143,8 +144,9 @@ def test_gemm_configs_agree_with_zero_weight_blocks(monkeypatch):
     """Weight blocks whose scale is 0 add nothing; configurations skip them
     or run them on zero fragments, and all must agree bit for bit: zero
     blocks at the first and last K block, two in a row, and a whole
-    128-row weight block column."""
-    q, s, wq, ws = _gemm_case(520, 1024, 1024, seed=17)
+    128-row weight block column; with 256 x 320 tiles (config 12) each of
+    them falls in a wave whose 160 weight rows straddle two scale blocks."""
+    q, s, wq, ws = _gemm_case(520, 1280, 1024, seed=17)
     ws = ws.clone()
     ws[0, 0] = 0.0
     ws[1, 7] = 0.0
@@ -208,6 +210,25 @@ def test_gemm_persistent_cross_tile_pipeline_at_pack_shapes(m, n, k, monkeypatch
         monkeypatch.setenv("QUAIL_GEMM_CONFIG", str(config))
         outs[config] = _run_gemm(q, s, wq, ws)
     assert torch.equal(outs[10], outs[22])
+
+
+@pytest.mark.parametrize("m,n,k", [(16294, 2560, 4096), (16294, 2560, 9728), (8192, 2560, 4096),
+                                   (3000, 5120, 768)])
+def test_gemm_wide_tiles_at_pack_shapes(m, n, k, monkeypatch):
+    """Config 12 (256 x 320 tiles, each wave's 160 weight rows straddling two
+    128-row scale blocks) at a 16k-row pack's o_proj and down shapes, the
+    GEMM-alone o_proj shape and a ragged M: bit-identical to config 10, and
+    the engine takes it at the first three."""
+    from quail_amd.engine import gemm_config
+    q, s, wq, ws = _gemm_case(m, n, k, seed=m + n + k)
+    outs = {}
+    for config in (10, 12):
+        monkeypatch.setenv("QUAIL_GEMM_CONFIG", str(config))
+        outs[config] = _run_gemm(q, s, wq, ws)
+    assert torch.equal(outs[10], outs[12])
+    monkeypatch.delenv("QUAIL_GEMM_CONFIG")
+    if m >= 8192:
+        assert gemm_config(n, k, m) == 12
 
 
 @pytest.mark.parametrize("k,n", [(2560, 6144), (4096, 2560), (2560, 19456), (9728, 2560)])

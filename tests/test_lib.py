@@ -96,13 +96,17 @@ def test_attention_tile_rows_choice_and_32_row_work_list():
 def test_gemm_config_choice_by_shape(monkeypatch):
     """Persistent config 22 where 256 x 256 tiles fill whole waves of the 256
     CUs (and K has an even number of 128-blocks), config 10 on a partial
-    last wave, config 11 for widths not a multiple of 256; the environment
-    variable forces one."""
+    last wave, config 12 (256 x 320 tiles) where those take fewer full-wave
+    units than 256 x 256 ones, config 11 for widths not a multiple of 256;
+    the environment variable forces one."""
     from quail_amd.engine import GEMM_CONFIG_ENV, gemm_config
     monkeypatch.delenv(GEMM_CONFIG_ENV, raising=False)
     assert gemm_config(6144, 2560, 16294) == 22     # 64 x 24 tiles: 6 waves
     assert gemm_config(6144, 2560, 16000) == 22     # 1512 tiles: last wave 91% full
-    assert gemm_config(2560, 4096, 16294) == 10     # 640 tiles: 2.5 waves
+    assert gemm_config(2560, 4096, 16294) == 12     # 512 tiles of 256 x 320, not 640
+    assert gemm_config(2560, 9728, 8192) == 12      # 256 tiles, not 320
+    assert gemm_config(2560, 4096, 13056) == 22     # 510 tiles of 256 x 256: 2 waves
+    assert gemm_config(2560, 4096, 2048) == 10      # 80 tiles: 64 wide ones cost more
     assert gemm_config(6144, 2560, 12000) == 10     # 1128 tiles
     assert gemm_config(6144, 2688, 16294) == 10     # 21 K-blocks
     assert gemm_config(6144, 2560, 256) == 10       # fewer tiles than CUs
