@@ -32,9 +32,11 @@ GROUP = 128
 # persistent grid with the K pipeline running across tiles: faster when the
 # 256 x 256 tiles fill whole waves of the 256 CUs (the fill and epilogue of
 # one tile overlap the next), slower on a partial last wave, which one
-# workgroup per tile spreads better. QUAIL_GEMM_CONFIG forces one.
+# workgroup per tile spreads better; 12 = 256 x 320 tiles (widths that are
+# multiples of 320), whole waves where N = 2560 makes 2.5 or 1.25 waves of
+# 256 x 256 tiles. QUAIL_GEMM_CONFIG forces one.
 GEMM_CONFIG_ENV = "QUAIL_GEMM_CONFIG"
-GEMM_CONFIGS = (10, 11, 22)
+GEMM_CONFIGS = (10, 11, 12, 22)
 GEMM_DEFAULT_CONFIG = 10
 SWIGLU_DEFAULT_CONFIG = 10
 GEMM_ODD_WIDTH_CONFIG = 11
