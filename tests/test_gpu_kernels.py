@@ -213,12 +213,13 @@ def test_gemm_persistent_cross_tile_pipeline_at_pack_shapes(m, n, k, monkeypatch
 
 
 @pytest.mark.parametrize("m,n,k", [(16294, 2560, 4096), (16294, 2560, 9728), (8192, 2560, 4096),
-                                   (3000, 5120, 768)])
+                                   (3000, 5120, 768), (77, 640, 384), (600, 2560, 640)])
 def test_gemm_wide_tiles_at_pack_shapes(m, n, k, monkeypatch):
     """Config 12 (256 x 320 tiles, each wave's 160 weight rows straddling two
     128-row scale blocks) at a 16k-row pack's o_proj and down shapes, the
-    GEMM-alone o_proj shape and a ragged M: bit-identical to config 10, and
-    the engine takes it at the first three."""
+    GEMM-alone o_proj shape, a ragged M, one partial token tile and an odd
+    number of 128-K blocks: bit-identical to config 10, and the engine takes
+    it at the first three."""
     from quail_amd.engine import gemm_config
     q, s, wq, ws = _gemm_case(m, n, k, seed=m + n + k)
     outs = {}
