@@ -54,10 +54,18 @@ int qx_device_is_gfx950(void);
  * 22: 256x256 tiles walked by one persistent workgroup per CU, the next
  *     tile's first block loaded during the last block of the current one
  *     and the epilogue staged in two passes through one stage buffer (falls
- *     back to 10 with an odd number of 128-K blocks or too few tiles).
- * Every config computes each element with the same operations in the same
- * order: the results are
- * bit-identical.
+ *     back to 10 with an odd number of 128-K blocks or too few tiles);
+ * 30: the promotion form (DeepGEMM's arithmetic): each 128-K block's
+ *     products summed from zero by one 16x16x128 MFMA per 16x16 output
+ *     tile, then total += (sA * sW) * partial in fp32; 256x256 tiles on a
+ *     persistent grid, the next block's loads issued one per MFMA (N a
+ *     multiple of 256; any number of 128-K blocks).
+ * Configs 10, 11, 12 and 22 rescale the accumulators in place
+ * (acc *= s_prev / s per block, the last s in the epilogue) and compute
+ * each element with the same operations in the same order: their results
+ * are bit-identical. Config 30 sums in another order (within the bf16
+ * tolerance of them and of the dequantized product); a caller that needs a
+ * row's result independent of M picks the family by N alone.
  */
 int qx_gemm_fp8_blockscaled(const void* A, const float* sA, const void* W, const float* sW,
                             void* C, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldc,
@@ -154,10 +162,11 @@ int qx_silu_mul_quant(const void* gate_up, int64_t gu_ld, void* q, int64_t q_ld,
  * (2I x K, rows [gate | up]) and weight_scale_inv as they are; A / sA as
  * for qx_gemm_fp8_blockscaled. Output as qx_silu_mul_quant's: Q (M x I)
  * e4m3 with leading dimension q_ld, Qs column-major (Qs[g * qs_ld + m]).
- * Bit-identical to qx_gemm_fp8_blockscaled (any config) followed by
+ * Bit-identical to qx_gemm_fp8_blockscaled of the same family followed by
  * qx_silu_mul_quant; the bf16 gate_up rows are never written. config: 10
  * (one workgroup per 256x256 tile) or 22 (persistent, as config 22 of
- * qx_gemm_fp8_blockscaled); both give the same bits.
+ * qx_gemm_fp8_blockscaled), the same bits as configs 10-22; 30 (the
+ * promotion form, as config 30 of qx_gemm_fp8_blockscaled).
  */
 int qx_gemm_fp8_swiglu_quant(const void* A, const float* sA, const void* W, const float* sW,
                              void* Q, int64_t q_ld, float* Qs, int64_t qs_ld, int64_t M,

@@ -483,21 +483,28 @@ __device__ __forceinline__ void n320_tile(
   const uint8_t* w_tile = W + (int64_t)n0 * K;
 
   float sw_ring[STAGES][2];
-  auto issue = [&](int kb, int stage) {
+  // the next block's A slabs and scales go out after the barrier, its
+  // weight slabs behind the first K half's MFMAs (the address unit then
+  // takes them while the matrix core runs: 2-4% faster than all at once)
+  auto issue_w = [&](int kb, int stage) {
     uint8_t* buf = smem + stage * Cfg::kStage;
-    const uint8_t* a_blk = a_tile + kb * 128;
     const uint8_t* w_blk = w_tile + kb * 128;
-#pragma unroll
-    for (int j = 0; j < Cfg::kASlabs; ++j)
-      __builtin_amdgcn_global_load_lds((const void*)(a_blk + a_off[j]),
-                                       (lds_void*)(buf + (wave * Cfg::kASlabs + j) * 1024), 16, 0,
-                                       kOperandLoadPolicy);
 #pragma unroll
     for (int j = 0; j < Cfg::kWSlabs; ++j)
       __builtin_amdgcn_global_load_lds(
           (const void*)(w_blk + w_off[j]),
           (lds_void*)(buf + Cfg::kABytes + (wave * Cfg::kWSlabs + j) * 1024), 16, 0,
           kOperandLoadPolicy);
+  };
+  auto issue = [&](int kb, int stage, bool with_w = true) {
+    uint8_t* buf = smem + stage * Cfg::kStage;
+    const uint8_t* a_blk = a_tile + kb * 128;
+#pragma unroll
+    for (int j = 0; j < Cfg::kASlabs; ++j)
+      __builtin_amdgcn_global_load_lds((const void*)(a_blk + a_off[j]),
+                                       (lds_void*)(buf + (wave * Cfg::kASlabs + j) * 1024), 16, 0,
+                                       kOperandLoadPolicy);
+    if (with_w) issue_w(kb, stage);
     {
       const int t = min(m0 + wave * Cfg::kSaPerWave + lane % Cfg::kSaPerWave, M - 1);
       __builtin_amdgcn_global_load_lds((const void*)(sA + (int64_t)kb * sa_ld + t),
@@ -526,7 +533,7 @@ __device__ __forceinline__ void n320_tile(
           wait_vmcnt<0>();
         }
         lds_barrier();
-        if (kb + STAGES - 1 < KT) issue(kb + STAGES - 1, (stage + STAGES - 1) % STAGES);
+        if (kb + STAGES - 1 < KT) issue(kb + STAGES - 1, (stage + STAGES - 1) % STAGES, false);
         const float sw0 =
             __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(sw_ring[stage][0])));
         const float sw1 =
@@ -568,6 +575,8 @@ __device__ __forceinline__ void n320_tile(
           // 160 accumulators leave room for one K half's fragments, not two:
           // the second half's reads wait until the first half's MFMAs issue
           if (h) __builtin_amdgcn_sched_barrier(0);
+          if (h && kb + STAGES - 1 < KT)
+            issue_w(kb + STAGES - 1, (stage + STAGES - 1) % STAGES);
           v8i wf[TN], af[TM];
 #pragma unroll
           for (int a = 0; a < TN; ++a)
@@ -943,6 +952,317 @@ __global__ __launch_bounds__(512) void gemm_fp8_k128q_kernel(
 }
 
 
+// ---- promotion form: one 16x16x128 MFMA per 128-K block ---------------------
+// DeepGEMM's arithmetic (the reference's fp8_gemm_nt): each 128-K block's
+// products are summed from zero into a partial, and the partial is promoted
+// into an fp32 total, total += (sA * sW) * partial. With
+// v_mfma_f32_16x16x128_f8f6f4 one MFMA covers a whole scale block of one
+// 16 x 16 output tile: its C operand is the inline constant 0, its result a
+// 4-register partial that only the promoting FMA reads. The totals are
+// never an MFMA operand, so the promotion runs on the VALU beside the
+// matrix core instead of waiting on it (rescaling the MFMA accumulators in
+// place, configs 10-22, serialises the two). Same tile walk, operand
+// staging and epilogue as config 22; a wave covers 128 weight rows x 64
+// tokens as 8 x 4 tiles of 16 x 16.
+//
+// Fragment of a 16-row tile for the 16x16x128 MFMA: lane l holds row l % 16
+// and the 32 bytes of K at [32 (l / 16), +32), chunks 2 (l / 16) and
+// 2 (l / 16) + 1 of the swizzled 128-byte row. The weight (A) and token (B)
+// operands use the same K order, so each lane pair multiplies matching K.
+// A 16-lane phase reads 16 consecutive rows at one chunk: rows of each
+// parity fall on distinct chunks under ((row >> 1) & 7), all 64 banks.
+__device__ __forceinline__ v8i read_frag16(const uint8_t* lds, int row, int q) {
+  const int sw = swz128(row);
+  const v4i* base = reinterpret_cast<const v4i*>(lds + row * 128);
+  const v4i lo = base[(2 * q) ^ sw];
+  const v4i hi = base[(2 * q + 1) ^ sw];
+  v8i r;
+  r[0] = lo[0]; r[1] = lo[1]; r[2] = lo[2]; r[3] = lo[3];
+  r[4] = hi[0]; r[5] = hi[1]; r[6] = hi[2]; r[7] = hi[3];
+  return r;
+}
+
+template <bool SWIGLU>
+__global__ __launch_bounds__(512) void gemm_fp8_promo_kernel(
+    const uint8_t* __restrict__ A, const float* __restrict__ sA, const uint8_t* __restrict__ W,
+    const float* __restrict__ sW, uint16_t* __restrict__ C, int M, int N, int K, int64_t lda,
+    int64_t ldc, int64_t sa_ld, int tiles_m, int tiles_n, int group_m, uint8_t* __restrict__ Q,
+    int64_t q_ld, float* __restrict__ Qs, int64_t qs_ld) {
+  constexpr int BM = 256, BN = 256, WAVES_N = 2, WAVES_M = 4;
+  using Cfg = Cfg128<BM, BN, WAVES_N, WAVES_M, 2>;
+  constexpr int TN = BN / WAVES_N / 16;  // 8 weight tiles of 16 rows per wave
+  constexpr int TM = BM / WAVES_M / 16;  // 4 token tiles of 16 per wave
+  constexpr int kRowBytes = BN * 2 + 16;   // padded staging row (bank spread)
+  constexpr int kPassRows = WAVES_M * 32;  // two token tiles of every wave per pass
+  constexpr int kPasses = TM / 2;
+  constexpr int kRowsPerWave = kPassRows / Cfg::kWaves;
+  static_assert(kPassRows * kRowBytes <= Cfg::kStage, "an epilogue pass fits one stage");
+  static_assert(kPasses * kPassRows == BM, "passes cover the tile");
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[Cfg::kLds];
+
+  // this workgroup's tiles: a contiguous band of tile ids per XCD (i mod 8),
+  // walked with stride (workgroups per XCD), as in config 22
+  const int total = tiles_m * tiles_n;
+  const int xcd = blockIdx.x & 7;
+  const int per_xcd = gridDim.x >> 3;  // the grid is a multiple of 8
+  const int local = blockIdx.x >> 3;
+  const int per = (total + 7) / 8;
+  const int full = total - (per - 1) * 8;
+  const int band0 = xcd < full ? xcd * per : full * per + (xcd - full) * (per - 1);
+  const int band = xcd < full ? per : per - 1;
+  const int my_tiles = local < band ? (band - local + per_xcd - 1) / per_xcd : 0;
+  const int width = group_m * tiles_n;
+  auto origin = [&](int iter, int& m0_, int& n0_) {
+    const int id = band0 + local + iter * per_xcd;
+    const int first_m = (id / width) * group_m;
+    const int gsize = min(tiles_m - first_m, group_m);
+    m0_ = (first_m + (id % width) % gsize) * BM;
+    n0_ = ((id % width) / gsize) * BN;
+  };
+  const int KT = K >> 7;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wn = wave % WAVES_N;
+  const int wm = wave / WAVES_N;
+  const int r16 = lane & 15, q16 = lane >> 4;
+
+  // Operand loads of one block: slab j of a wave is tile rows
+  // row0 + 8 j, row0 = 32 wave + lane / 8 (A and W alike, 4 slabs each),
+  // and a lane's 16-byte chunk (lane % 8) ^ ((row >> 1) % 8) is c0 for
+  // even j and c0 ^ 4 for odd j. The per-lane part of an address is a
+  // 32-bit offset over a wave-uniform base (the launcher checks that a
+  // tile's rows span less than 4 GiB); token rows past M clamp to M - 1.
+  static_assert(Cfg::kASlabs == 4 && Cfg::kWSlabs == 4, "slab walk");
+  const int row0 = wave * 32 + (lane >> 3);
+  const uint32_t chunk0 = (uint32_t)(((lane & 7) ^ swz128(row0)) * 16);
+  const uint32_t chunk1 = chunk0 ^ 64u;
+  const uint32_t w_lane0 = (uint32_t)row0 * (uint32_t)K + chunk0;
+  const uint32_t w_lane1 = (uint32_t)row0 * (uint32_t)K + chunk1;
+  float sw_next = 0.0f;  // the weight scale of the block in flight
+  // the block to load: its tile, 128-K block and stage
+  struct Blk {
+    const uint8_t* a;  // the tile's first token row at the block's K
+    const uint8_t* w;  // the tile's first weight row at the block's K
+    const float* sa;   // the block's scale of the tile's first token
+    const float* sw;   // the wave's weight scale of the block
+    uint8_t* buf;
+    int m_last;        // the tile's last token row (rows past it clamp)
+  };
+  auto block_of = [&](int m0_, int n0_, int kb, int stage) {
+    Blk b;
+    const int64_t k_off = (int64_t)kb * 128;
+    const int w_row0 = SWIGLU ? (n0_ >> 1) : n0_;
+    b.buf = smem + stage * Cfg::kStage;
+    b.m_last = M - 1 - m0_;
+    b.a = A + (int64_t)m0_ * lda + k_off;
+    b.w = W + (int64_t)w_row0 * K + k_off;
+    b.sa = sA + (int64_t)kb * sa_ld + m0_;
+    b.sw = sW + (int64_t)((SWIGLU ? w_row0 + wn * (N >> 1) : n0_ + wn * (BN / WAVES_N)) >> 7) * KT + kb;
+    return b;
+  };
+  // load op j of a block: A slabs (j < 4), weight slabs (4 <= j < 8), then
+  // the token scales and the weight scale
+  constexpr int kLoadOps = Cfg::kASlabs + Cfg::kWSlabs + 1;
+  const int sa_row = wave * Cfg::kSaPerWave + lane % Cfg::kSaPerWave;
+  auto load_op = [&](const Blk& b, int j) {
+    if (j < 4) {
+      const int row = row0 + 8 * j;
+      const uint32_t crow = (uint32_t)(row < b.m_last ? row : b.m_last);
+      const uint32_t off = crow * (uint32_t)lda + ((j & 1) ? chunk1 : chunk0);
+      __builtin_amdgcn_global_load_lds((const void*)(b.a + off),
+                                       (lds_void*)(b.buf + (wave * 4 + j) * 1024), 16, 0,
+                                       kOperandLoadPolicy);
+    } else if (j < 8) {
+      const int jw = j - 4;
+      // uniform row shift of slab jw (SwiGLU: rows 128.. are up rows)
+      const int shift = 8 * jw + (SWIGLU && wave * 4 + jw >= 16 ? (N >> 1) - 128 : 0);
+      __builtin_amdgcn_global_load_lds(
+          (const void*)(b.w + (int64_t)shift * K + ((jw & 1) ? w_lane1 : w_lane0)),
+          (lds_void*)(b.buf + Cfg::kABytes + (wave * 4 + jw) * 1024), 16, 0,
+          kOperandLoadPolicy);
+    } else {
+      const int t = min(sa_row, b.m_last);
+      __builtin_amdgcn_global_load_lds((const void*)(b.sa + t),
+                                       (lds_void*)(b.buf + Cfg::kABytes + Cfg::kWBytes + wave * 256),
+                                       4, 0, 0);
+      sw_next = __builtin_nontemporal_load(b.sw);
+    }
+  };
+  auto issue = [&](int m0_, int n0_, int kb, int stage) {
+    const Blk b = block_of(m0_, n0_, kb, stage);
+#pragma unroll
+    for (int j = 0; j < kLoadOps; ++j) load_op(b, j);
+  };
+
+  v4f tot[TN][TM];
+  int m0 = 0, n0 = 0;
+  if (my_tiles > 0) {
+    origin(0, m0, n0);
+    issue(m0, n0, 0, 0);
+  }
+  // Blocks alternate between the two stages across tiles: the block after
+  // a tile's last (the next tile's first) is loaded into the other stage
+  // while the last one is consumed, and the epilogue stages the tile
+  // through the last block's stage.
+  int stage = 0;
+  for (int it = 0; it < my_tiles; ++it) {
+    int nm0 = m0, nn0 = n0;
+    const bool has_next = it + 1 < my_tiles;
+    if (has_next) origin(it + 1, nm0, nn0);
+#pragma unroll
+    for (int a = 0; a < TN; ++a)
+#pragma unroll
+      for (int b = 0; b < TM; ++b) tot[a][b] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int kb = 0; kb < KT; ++kb) {
+      wait_vmcnt<0>();  // this block's operands (and earlier stores) are done
+      lds_barrier();
+      const float sw = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(sw_next)));
+      // the next block: this tile's, or after its last the next tile's
+      // first; after the workgroup's last block, the current block again
+      // (into the free stage: loads with no branch around them, drained
+      // before the end)
+      Blk nb;
+      {
+        const bool same = kb + 1 < KT;
+        const bool next_tile = !same && has_next;
+        nb = block_of(next_tile ? nm0 : m0, next_tile ? nn0 : n0,
+                      same ? kb + 1 : (next_tile ? 0 : kb), stage ^ 1);
+      }
+      const uint8_t* a_lds = smem + stage * Cfg::kStage;
+      const uint8_t* w_lds = a_lds + Cfg::kABytes;
+      const float* sa_lds = reinterpret_cast<const float*>(w_lds + Cfg::kWBytes);
+      float s[TM];
+      v8i af[TM];
+#pragma unroll
+      for (int b = 0; b < TM; ++b) {
+        const int row = wm * TM * 16 + b * 16 + r16;
+        s[b] = sa_lds[(row / Cfg::kSaPerWave) * 64 + row % Cfg::kSaPerWave] * sw;
+        af[b] = read_frag16(a_lds, row, q16);
+      }
+      // MFMA t (weight tile a = t / TM, token tile b = t % TM) writes
+      // partial slot t % 3; each scheduling slot issues one MFMA and the
+      // promotion of the partial two MFMAs older, so three partials are
+      // live and the FMAs never wait on the MFMA just issued. The next
+      // weight fragment is read at the start of the current one's MFMAs.
+      constexpr int kLag = 2;
+      v4f part[kLag + 1];
+      auto promote = [&](int t) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          tot[t / TM][t % TM][e] =
+              __builtin_fmaf(s[t % TM], part[t % (kLag + 1)][e], tot[t / TM][t % TM][e]);
+      };
+      v8i wf = read_frag16(w_lds, wn * TN * 16 + r16, q16);
+      v8i wf_next;
+#pragma unroll
+      for (int t = 0; t < TN * TM; ++t) {
+        const int a = t / TM, b = t % TM;
+        if (b == 0 && a + 1 < TN)
+          wf_next = read_frag16(w_lds, wn * TN * 16 + (a + 1) * 16 + r16, q16);
+        part[t % (kLag + 1)] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+            wf, af[b], v4f{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0, 0, 0, 0);
+        if (t >= kLag) promote(t - kLag);
+        // the next block's loads, one per MFMA over the block's first
+        // slots: all of them issued at once after the barrier queue every
+        // wave behind the address unit while the matrix core waits
+        // (measured 7-14% slower), spread one per two or three MFMAs they
+        // land too close to the next barrier (3-8% slower)
+        if (t < kLoadOps) load_op(nb, t);
+        __builtin_amdgcn_sched_barrier(0);
+        if (b == TM - 1 && a + 1 < TN) wf = wf_next;
+      }
+#pragma unroll
+      for (int t = TN * TM - kLag; t < TN * TM; ++t) promote(t);
+      stage ^= 1;
+    }
+
+    // epilogue through the stage of the tile's last block. Lane l holds
+    // token b * 16 + l % 16 of the wave's 64 and weight rows
+    // a * 16 + 4 (l / 16) .. + 3 of its 128. Pass p stages token tiles 2p
+    // and 2p + 1 of every wave: staging row wm * 32 + (b - 2p) * 16 + l % 16.
+    uint8_t* buf = smem + (stage ^ 1) * Cfg::kStage;
+    const bool wide = ((ldc & 7) == 0) && ((reinterpret_cast<uintptr_t>(C) & 15) == 0);
+#pragma unroll
+    for (int pass = 0; pass < kPasses; ++pass) {
+      // pass 0: every wave is done with the last block's operands; later
+      // passes: with the previous pass's rows
+      lgkm_barrier();
+#pragma unroll
+      for (int bb = 0; bb < 2; ++bb) {
+        const int b = pass * 2 + bb;
+        uint8_t* lrow = buf + (wm * 32 + bb * 16 + r16) * kRowBytes;
+#pragma unroll
+        for (int a = 0; a < TN; ++a) {
+          const int off = (wn * TN * 16 + a * 16 + q16 * 4) * 2;
+          uint2 v;
+          v.x = pack2_bf16(tot[a][b][0], tot[a][b][1]);
+          v.y = pack2_bf16(tot[a][b][2], tot[a][b][3]);
+          *reinterpret_cast<uint2*>(lrow + off) = v;
+        }
+      }
+      lgkm_barrier();
+      if constexpr (SWIGLU) {
+        // 16 lanes per row: 8 gate and 8 up values each, one quant group
+        const int j0 = n0 >> 1;
+        const int seg = lane & 15;
+#pragma unroll
+        for (int i = 0; i < kRowsPerWave / 4; ++i) {
+          const int prow = wave * kRowsPerWave + i * 4 + (lane >> 4);
+          const int m = m0 + (prow >> 5) * TM * 16 + pass * 32 + (prow & 31);
+          const uint8_t* lrow = buf + prow * kRowBytes;
+          const uint4 g = *reinterpret_cast<const uint4*>(lrow + seg * 16);
+          const uint4 u = *reinterpret_cast<const uint4*>(lrow + 256 + seg * 16);
+          const uint32_t gw[4] = {g.x, g.y, g.z, g.w}, uw[4] = {u.x, u.y, u.z, u.w};
+          float y[8];
+          float amax = 0.0f;
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            y[2 * k] = silu_mul(lo_bf16(gw[k]), lo_bf16(uw[k]));
+            y[2 * k + 1] = silu_mul(hi_bf16(gw[k]), hi_bf16(uw[k]));
+          }
+#pragma unroll
+          for (int k = 0; k < 8; ++k) amax = fmaxf(amax, fabsf(y[k]));
+          amax = group_max<16>(amax);
+          const float scale = fp8_scale(amax);
+          const float rs = recip(scale);
+          if (m < M) {
+            const v2i o = {(int)pack4_fp8(div_by(y[0], scale, rs), div_by(y[1], scale, rs),
+                                          div_by(y[2], scale, rs), div_by(y[3], scale, rs)),
+                           (int)pack4_fp8(div_by(y[4], scale, rs), div_by(y[5], scale, rs),
+                                          div_by(y[6], scale, rs), div_by(y[7], scale, rs))};
+            __builtin_nontemporal_store(o, reinterpret_cast<v2i*>(Q + (int64_t)m * q_ld + j0 +
+                                                                 seg * 8));
+            if (seg == 0) Qs[(int64_t)(j0 >> 7) * qs_ld + m] = scale;
+          }
+        }
+      } else {
+        constexpr int kChunks = BN / 8;
+        constexpr int kRowsPerOp = 64 / kChunks;
+        const int c = lane % kChunks;
+#pragma unroll
+        for (int i = 0; i < kRowsPerWave / kRowsPerOp; ++i) {
+          const int prow = wave * kRowsPerWave + i * kRowsPerOp + lane / kChunks;
+          const int m = m0 + (prow >> 5) * TM * 16 + pass * 32 + (prow & 31);
+          const uint4 v = *reinterpret_cast<const uint4*>(buf + prow * kRowBytes + c * 16);
+          if (m < M) {
+            uint16_t* dst = C + (int64_t)m * ldc + n0 + c * 8;
+            if (wide) {
+              const v4i w = {(int)v.x, (int)v.y, (int)v.z, (int)v.w};
+              __builtin_nontemporal_store(w, reinterpret_cast<v4i*>(dst));
+            } else {
+              reinterpret_cast<uint2*>(dst)[0] = make_uint2(v.x, v.y);
+              reinterpret_cast<uint2*>(dst)[1] = make_uint2(v.z, v.w);
+            }
+          }
+        }
+      }
+    }
+    m0 = nm0;
+    n0 = nn0;
+  }
+  wait_vmcnt<0>();  // the repeated last block's loads
+}
+
 // Workgroups of the persistent kernel: one per CU, a multiple of 8 (one
 // band per XCD); the CU count is read once per device.
 inline int persistent_grid(int total) {
@@ -973,6 +1293,21 @@ int launch128q(const void* A, const float* sA, const void* W, const float* sW, v
     return launch128<256, 256, 2, 4, 2>(A, sA, W, sW, C, M, N, K, lda, ldc, sa_ld, 4, stream);
   }
   hipLaunchKernelGGL((gemm_fp8_k128q_kernel<SWIGLU>), dim3(grid), dim3(512), 0, stream,
+                     (const uint8_t*)A, sA, (const uint8_t*)W, sW, (uint16_t*)C, M, N, K, lda,
+                     ldc, sa_ld, tiles_m, tiles_n, 4, (uint8_t*)Q, q_ld, Qs, qs_ld);
+  QX_LAUNCH_STATUS();
+}
+// the promotion-form kernel (config 30; the SwiGLU epilogue with Q !=
+// nullptr): one workgroup per CU, at least one per XCD
+template <bool SWIGLU>
+int launch_promo(const void* A, const float* sA, const void* W, const float* sW, void* C, int M,
+                 int N, int K, int64_t lda, int64_t ldc, int64_t sa_ld, void* Q, int64_t q_ld,
+                 float* Qs, int64_t qs_ld, hipStream_t stream) {
+  const int tiles_m = (M + 255) / 256;
+  const int tiles_n = N / 256;
+  int grid = persistent_grid(tiles_m * tiles_n);
+  if (grid < 8) grid = 8;
+  hipLaunchKernelGGL((gemm_fp8_promo_kernel<SWIGLU>), dim3(grid), dim3(512), 0, stream,
                      (const uint8_t*)A, sA, (const uint8_t*)W, sW, (uint16_t*)C, M, N, K, lda,
                      ldc, sa_ld, tiles_m, tiles_n, 4, (uint8_t*)Q, q_ld, Qs, qs_ld);
   QX_LAUNCH_STATUS();
@@ -1008,8 +1343,16 @@ int qx_gemm_fp8_swiglu_quant(const void* A, const float* sA, const void* W, cons
   QX_CHECK(qs_ld >= M && sa_ld >= M, "gemm_swiglu: scale strides");
   QX_CHECK(M < (1LL << 31) && 2 * I < (1LL << 31) && K < (1LL << 31), "gemm_swiglu: dims");
   QX_CHECK(((uintptr_t)A & 15) == 0 && ((uintptr_t)W & 15) == 0, "gemm_swiglu: alignment");
-  QX_CHECK(config == 10 || config == 22, "gemm_swiglu: config %d (10 or 22)", config);
+  QX_CHECK(config == 10 || config == 22 || config == 30,
+           "gemm_swiglu: config %d (10, 22 or 30)", config);
   if (M == 0) return QX_OK;
+  if (config == 30) {
+    QX_CHECK(256 * lda < (1LL << 32) && (I + 128) * K < (1LL << 32),
+             "gemm_swiglu config 30: a tile's rows must span less than 4 GiB (lda=%lld, K=%lld)",
+             (long long)lda, (long long)K);
+    return qx::launch_promo<true>(A, sA, W, sW, nullptr, (int)M, (int)(2 * I), (int)K, lda, 0,
+                                  sa_ld, Q, q_ld, Qs, qs_ld, stream);
+  }
   if (config == 22)
     return qx::launch128q<true>(A, sA, W, sW, nullptr, (int)M, (int)(2 * I), (int)K, lda, 0,
                                 sa_ld, Q, q_ld, Qs, qs_ld, stream);
@@ -1052,8 +1395,15 @@ int qx_gemm_fp8_blockscaled(const void* A, const float* sA, const void* W, const
       QX_CHECK(n % 256 == 0, "gemm config 22 needs N %% 256 == 0 (N=%d)", n);
       return qx::launch128q<false>(A, sA, W, sW, C, m, n, k, lda, ldc, sa_ld, nullptr, 0,
                                    nullptr, 0, stream);
+    case 30:
+      QX_CHECK(n % 256 == 0, "gemm config 30 needs N %% 256 == 0 (N=%d)", n);
+      QX_CHECK(256 * lda < (1LL << 32) && 256LL * k < (1LL << 32),
+               "gemm config 30: a tile's rows must span less than 4 GiB (lda=%lld, K=%d)",
+               (long long)lda, k);
+      return qx::launch_promo<false>(A, sA, W, sW, C, m, n, k, lda, ldc, sa_ld, nullptr, 0,
+                                     nullptr, 0, stream);
     default:
-      QX_CHECK(false, "gemm: unknown config %d (10, 11, 12 or 22)", config);
+      QX_CHECK(false, "gemm: unknown config %d (10, 11, 12, 22 or 30)", config);
   }
 }
 

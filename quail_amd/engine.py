@@ -24,21 +24,29 @@ from quail_amd import _lib
 
 GROUP = 128
 
-# GEMM tile configurations (csrc/gemm_fp8.hip); each computes every output
-# element with the same operations in the same order, so the choice never
-# changes a result bit. 10 = 256 tokens x 256 weights, 8 waves, two 128-K
-# stages (128 KiB LDS), one workgroup per tile; 11 = 256 x 128, 4 waves,
-# takes widths that are not multiples of 256; 22 = config 10's tiles on a
-# persistent grid with the K pipeline running across tiles: faster when the
-# 256 x 256 tiles fill whole waves of the 256 CUs (the fill and epilogue of
-# one tile overlap the next), slower on a partial last wave, which one
-# workgroup per tile spreads better; 12 = 256 x 320 tiles (widths that are
-# multiples of 320), whole waves where N = 2560 makes 2.5 or 1.25 waves of
-# 256 x 256 tiles. QUAIL_GEMM_CONFIG forces one.
+# GEMM tile configurations (csrc/gemm_fp8.hip), in two arithmetic families.
+# Rescale family (10, 11, 12, 22): the MFMA accumulators are rescaled in
+# place by s_prev / s at each 128-K block; each config computes every
+# output element with the same operations in the same order, so the choice
+# among them never changes a bit. 10 = 256 tokens x 256 weights, 8 waves,
+# two 128-K stages, one workgroup per tile; 11 = 256 x 128 (widths not a
+# multiple of 256); 22 = config 10's tiles on a persistent grid; 12 = 256 x
+# 320 tiles (widths that are multiples of 320), whole waves where N = 2560
+# makes 2.5 or 1.25 waves of 256 x 256 tiles. Promotion family (30): each
+# block's products summed from zero by one 16x16x128 MFMA and promoted
+# into an fp32 total, total += (sA * sW) * partial (DeepGEMM's form),
+# persistent 256 x 256 tiles. The family is a function of N alone, so a
+# row's result never depends on how many rows share the launch (a document
+# packed with others equals itself run alone, bit for bit): N a multiple of
+# 320 takes the rescale family (config 12's whole waves there), any other
+# multiple of 256 the promotion kernel, the rest config 11.
+# QUAIL_GEMM_CONFIG forces one.
 GEMM_CONFIG_ENV = "QUAIL_GEMM_CONFIG"
-GEMM_CONFIGS = (10, 11, 12, 22)
+GEMM_CONFIGS = (10, 11, 12, 22, 30)
+RESCALE_CONFIGS = (10, 11, 12, 22)
 GEMM_DEFAULT_CONFIG = 10
-SWIGLU_DEFAULT_CONFIG = 10
+GEMM_PROMOTION_CONFIG = 30
+SWIGLU_DEFAULT_CONFIG = 30
 GEMM_ODD_WIDTH_CONFIG = 11
 GEMM_WHOLE_WAVES_CONFIG = 22
 CUS = 256
@@ -59,13 +67,16 @@ def gemm_config(n: int, k: int, m: int) -> int:
     forced = os.environ.get(GEMM_CONFIG_ENV)
     if forced is not None:
         return int(forced)
-    if n % 320 == 0 and _wide_tiles_fill_better(n, m):
-        return GEMM_WIDE_TILE_CONFIG
-    if n % 256:
-        return GEMM_ODD_WIDTH_CONFIG
-    if _whole_waves(n, k, m):
-        return GEMM_WHOLE_WAVES_CONFIG
-    return GEMM_DEFAULT_CONFIG
+    if n % 320 == 0:
+        # rescale family: 256 x 320 tiles where they take fewer full waves
+        if _wide_tiles_fill_better(n, m):
+            return GEMM_WIDE_TILE_CONFIG
+        if n % 256:
+            return GEMM_ODD_WIDTH_CONFIG
+        return GEMM_WHOLE_WAVES_CONFIG if _whole_waves(n, k, m) else GEMM_DEFAULT_CONFIG
+    if n % 256 == 0:
+        return GEMM_PROMOTION_CONFIG
+    return GEMM_ODD_WIDTH_CONFIG
 
 
 def _wave_cost(tiles: int) -> float:
@@ -99,17 +110,13 @@ SWIGLU_CONFIG_ENV = "QUAIL_SWIGLU_CONFIG"
 
 def swiglu_config(n: int = 0, k: int = 0, m: int = 0) -> int:
     """Tile schedule of the gate_up GEMM with the SiLU-quant epilogue (n =
-    gate_up rows, 256 per tile): 10 (one workgroup per tile) or 22
-    (persistent, the K pipeline running across tiles), chosen as for
-    qx_gemm_fp8_blockscaled (22 where the tiles fill whole waves: the
-    gate_up of a full pack, +1% against 10 in the pass). QUAIL_SWIGLU_CONFIG
+    gate_up rows, 256 per tile): the promotion kernel (30) for every shape;
+    10 and 22 (the rescale family) stay selectable. QUAIL_SWIGLU_CONFIG
     forces it alone, QUAIL_GEMM_CONFIG with every GEMM."""
     for env in (SWIGLU_CONFIG_ENV, GEMM_CONFIG_ENV):
         forced = os.environ.get(env)
-        if forced is not None and int(forced) in (10, 22):
+        if forced is not None and int(forced) in (10, 22, 30):
             return int(forced)
-    if n % 256 == 0 and _whole_waves(n, k, m):
-        return GEMM_WHOLE_WAVES_CONFIG
     return SWIGLU_DEFAULT_CONFIG
 
 

@@ -98,11 +98,13 @@ def test_gemm_small_shapes_match_dequantized_matmul(m, n, k):
     _bf16_close(out, want)
 
 
+# the rescale family: bit-identical to each other
 GEMM_CONFIGS = (10, 11, 12, 22)
 GEMM_CONFIGS_256 = (10, 11, 22)   # N a multiple of 256 (config 12 needs 320)
+PROMOTION_CONFIG = 30             # DeepGEMM's promotion form: its own arithmetic
 
 
-@pytest.mark.parametrize("config", GEMM_CONFIGS)
+@pytest.mark.parametrize("config", GEMM_CONFIGS + (PROMOTION_CONFIG,))
 def test_gemm_tile_configs_agree(config, monkeypatch):
     q, s, wq, ws = _gemm_case(300, 1280, 512, seed=9)
     monkeypatch.setenv("QUAIL_GEMM_CONFIG", str(config))
@@ -137,7 +139,23 @@ def test_gemm_persistent_config_with_several_tiles_per_workgroup(monkeypatch):
         outs[config] = _run_gemm(q, s, wq, ws).cpu()
     for config in GEMM_CONFIGS_256:
         assert torch.equal(outs[config], outs[10]), config
-    _bf16_close(outs[22], ref.gemm(q, s, ref.RefLinear(wq, ws)))
+    want = ref.gemm(q, s, ref.RefLinear(wq, ws))
+    _bf16_close(outs[22], want)
+    monkeypatch.setenv("QUAIL_GEMM_CONFIG", str(PROMOTION_CONFIG))
+    _bf16_close(_run_gemm(q, s, wq, ws), want)
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 256, 128), (257, 768, 384), (4000, 2560, 768),
+                                   (3000, 5120, 1152), (600, 19456, 640)])
+def test_gemm_promotion_kernel_edges(m, n, k, monkeypatch):
+    """Config 30 (each 128-K block summed from zero by one 16x16x128 MFMA,
+    then total += sA * sW * partial) against the oracle: one row, a partial
+    token tile, odd numbers of 128-K blocks (the next tile's first block
+    chained across an odd count), several tiles per workgroup."""
+    q, s, wq, ws = _gemm_case(m, n, k, seed=m + n + k)
+    monkeypatch.setenv("QUAIL_GEMM_CONFIG", str(PROMOTION_CONFIG))
+    out = _run_gemm(q, s, wq, ws)
+    _bf16_close(out, ref.gemm(q, s, ref.RefLinear(wq, ws)))
 
 
 def test_gemm_configs_agree_with_zero_weight_blocks(monkeypatch):
@@ -158,19 +176,27 @@ def test_gemm_configs_agree_with_zero_weight_blocks(monkeypatch):
         outs[config] = _run_gemm(q, s, wq, ws).cpu()
     for config, out in outs.items():
         assert torch.equal(out, outs[10]), config
-    _bf16_close(outs[10], ref.gemm(q, s, ref.RefLinear(wq, ws)))
+    want = ref.gemm(q, s, ref.RefLinear(wq, ws))
+    _bf16_close(outs[10], want)
     assert torch.all(outs[10][:, 5 * 128:6 * 128] == 0)
+    # the promotion form adds 0 * partial for such blocks (finite operands)
+    monkeypatch.setenv("QUAIL_GEMM_CONFIG", str(PROMOTION_CONFIG))
+    out = _run_gemm(q, s, wq, ws).cpu()
+    _bf16_close(out, want)
+    assert torch.all(out[:, 5 * 128:6 * 128] == 0)
 
 
 @pytest.mark.parametrize("m,i,k,zero_blocks", [(700, 768, 512, False), (333, 1536, 256, True),
                                                (2000, 9728, 2560, False)])
-@pytest.mark.parametrize("config", ["10", "22"])
+@pytest.mark.parametrize("config", ["10", "22", "30"])
 def test_gate_up_swiglu_quant_equals_gemm_then_activation_quant(m, i, k, zero_blocks, config,
                                                                  monkeypatch):
     """qx_gemm_fp8_swiglu_quant (gate_up GEMM with the SiLU-quant epilogue)
-    against the two launches it replaces, bit for bit: a partial token tile,
-    the Qwen3-4B gate_up shape (I = 9728, K = 2560) and weight blocks whose
-    scale is 0 (skipped by the GEMM) in both halves."""
+    against the two launches it replaces, bit for bit, within each
+    arithmetic family (10 and 22 against the config-10 GEMM, 30 against the
+    config-30 GEMM): a partial token tile, the Qwen3-4B gate_up shape
+    (I = 9728, K = 2560) and weight blocks whose scale is 0 in both
+    halves."""
     eng = _engine()
     g = _gen(m + i + k)
     a = torch.randn(m, k, generator=g)
@@ -187,7 +213,7 @@ def test_gate_up_swiglu_quant_equals_gemm_then_activation_quant(m, i, k, zero_bl
     scales.copy_(s.T)
     q_in = q.to(DEV)
     sv = scales.permute(1, 0)
-    monkeypatch.setenv("QUAIL_GEMM_CONFIG", "10")
+    monkeypatch.setenv("QUAIL_GEMM_CONFIG", "30" if config == "30" else "10")
     want_q, want_s = eng.activation_quant(eng.gemm(q_in, sv, lin))
     monkeypatch.setenv("QUAIL_GEMM_CONFIG", config)
     got_q, got_s = eng.gate_up_activation_quant(q_in, sv, lin)
@@ -233,12 +259,16 @@ def test_gemm_wide_tiles_at_pack_shapes(m, n, k, monkeypatch):
         assert gemm_config(n, k, m) == 12
 
 
+@pytest.mark.parametrize("config", [None, PROMOTION_CONFIG, 10])
 @pytest.mark.parametrize("k,n", [(2560, 6144), (4096, 2560), (2560, 19456), (9728, 2560)])
-def test_gemm_qwen3_4b_shapes_at_8192_tokens(k, n):
+def test_gemm_qwen3_4b_shapes_at_8192_tokens(k, n, config, monkeypatch):
     """The GEMM-alone config: M=8192 at the four Qwen3-4B projection shapes,
     activations bf16 N(0, 1) quantized per token per 128 columns, weights
     N(0, 0.02) per 128 x 128 block, against the fp32 matmul of the
-    dequantized operands (computed on the GPU in fp32 for time)."""
+    dequantized operands (computed on the GPU in fp32 for time); the
+    engine's choice (None) and each family forced."""
+    if config is not None:
+        monkeypatch.setenv("QUAIL_GEMM_CONFIG", str(config))
     m = 8192
     g = torch.Generator(device=DEV).manual_seed(k + n)
     a = torch.randn(m, k, generator=g, device=DEV).to(torch.bfloat16).float()

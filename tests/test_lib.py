@@ -94,33 +94,47 @@ def test_attention_tile_rows_choice_and_32_row_work_list():
 
 
 def test_gemm_config_choice_by_shape(monkeypatch):
-    """Persistent config 22 where 256 x 256 tiles fill whole waves of the 256
-    CUs (and K has an even number of 128-blocks), config 10 on a partial
-    last wave, config 12 (256 x 320 tiles) where those take fewer full-wave
-    units than 256 x 256 ones, config 11 for widths not a multiple of 256;
-    the environment variable forces one."""
+    """The arithmetic family is a function of N alone: widths that are a
+    multiple of 320 take the rescale family (config 12's 256 x 320 tiles
+    where those take fewer full-wave units than 256 x 256 ones, else the
+    persistent config 22 where 256 x 256 tiles fill whole waves and K has an
+    even number of 128-blocks, else config 10), other multiples of 256 the
+    promotion kernel (30) at every M, the rest config 11; the environment
+    variable forces one."""
     from quail_amd.engine import GEMM_CONFIG_ENV, gemm_config
     monkeypatch.delenv(GEMM_CONFIG_ENV, raising=False)
-    assert gemm_config(6144, 2560, 16294) == 22     # 64 x 24 tiles: 6 waves
-    assert gemm_config(6144, 2560, 16000) == 22     # 1512 tiles: last wave 91% full
+    assert gemm_config(6144, 2560, 16294) == 30     # qkv of a Qwen3-4B pack
+    assert gemm_config(6144, 2688, 16294) == 30     # 21 K-blocks
+    assert gemm_config(6144, 2560, 256) == 30       # fewer tiles than CUs
+    assert gemm_config(4096, 4096, 37) == 30        # Qwen3-8B o_proj, a few final rows
     assert gemm_config(2560, 4096, 16294) == 12     # 512 tiles of 256 x 320, not 640
     assert gemm_config(2560, 9728, 8192) == 12      # 256 tiles, not 320
     assert gemm_config(2560, 4096, 13056) == 22     # 510 tiles of 256 x 256: 2 waves
     assert gemm_config(2560, 4096, 2048) == 10      # 80 tiles: 64 wide ones cost more
-    assert gemm_config(6144, 2560, 12000) == 10     # 1128 tiles
-    assert gemm_config(6144, 2688, 16294) == 10     # 21 K-blocks
-    assert gemm_config(6144, 2560, 256) == 10       # fewer tiles than CUs
+    assert gemm_config(2560, 2688, 12000) == 10     # 21 K-blocks
+    assert gemm_config(10240, 5120, 16294) == 22    # Qwen3-32B qkv: rescale family, 10 waves
     assert gemm_config(2688, 2560, 16294) == 11
+    assert gemm_config(640, 256, 100) == 12         # 320 tiles take fewer waves (odd width)
     monkeypatch.setenv(GEMM_CONFIG_ENV, "11")
     assert gemm_config(6144, 2560, 16294) == 11
+
+
+def test_gemm_family_depends_on_width_only():
+    """Rows never change arithmetic with the number of rows in the launch:
+    for every width, all M choose configs of one family."""
+    from quail_amd.engine import RESCALE_CONFIGS, gemm_config
+    for n in (256, 512, 1280, 2560, 4096, 5120, 6144, 10240, 19456, 2688, 640):
+        fams = {gemm_config(n, 2560, m) in RESCALE_CONFIGS
+                for m in (1, 37, 255, 2048, 8192, 13056, 16294, 16384, 32768)}
+        assert len(fams) == 1, n
 
 
 def test_swiglu_config_choice_by_shape(monkeypatch):
     from quail_amd.engine import GEMM_CONFIG_ENV, SWIGLU_CONFIG_ENV, swiglu_config
     monkeypatch.delenv(GEMM_CONFIG_ENV, raising=False)
     monkeypatch.delenv(SWIGLU_CONFIG_ENV, raising=False)
-    assert swiglu_config(19456, 2560, 16294) == 22   # 64 x 76 tiles: 19 waves
-    assert swiglu_config(19456, 2560, 9000) == 10    # 36 x 76 = 2736 tiles
-    assert swiglu_config(19456, 2688, 16294) == 10   # 21 K-blocks
+    assert swiglu_config(19456, 2560, 16294) == 30
+    assert swiglu_config(19456, 2560, 9000) == 30
+    assert swiglu_config(19456, 2688, 16294) == 30   # 21 K-blocks
     monkeypatch.setenv(SWIGLU_CONFIG_ENV, "10")
     assert swiglu_config(19456, 2560, 16294) == 10
