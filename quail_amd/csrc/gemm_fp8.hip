@@ -966,16 +966,21 @@ __global__ __launch_bounds__(512) void gemm_fp8_k128q_kernel(
 // tokens as 8 x 4 tiles of 16 x 16.
 //
 // Fragment of a 16-row tile for the 16x16x128 MFMA: lane l holds row l % 16
-// and the 32 bytes of K at [32 (l / 16), +32), chunks 2 (l / 16) and
-// 2 (l / 16) + 1 of the swizzled 128-byte row. The weight (A) and token (B)
+// and the 32 bytes of K in 16-byte chunks q and q + 4 of the row, q = l / 16
+// (bytes [16 q, +16) and [64 + 16 q, +16)). The weight (A) and token (B)
 // operands use the same K order, so each lane pair multiplies matching K.
-// A 16-lane phase reads 16 consecutive rows at one chunk: rows of each
-// parity fall on distinct chunks under ((row >> 1) & 7), all 64 banks.
+// In LDS this kernel's rows hold chunk c at position c ^ (row % 8). Measured
+// with a read probe (8 waves per CU, 16 ds_read_b128 per trip): this layout
+// reads at the rate of contiguous 16-byte reads; chunks 2q, 2q + 1 under
+// the ((row >> 1) % 8) swizzle of the 32x32 kernels ran 1.55x slower (bank
+// conflicts: 3.6 cycles per LDS instruction by the SQ counter).
+__device__ __forceinline__ int swz16(int row) { return row & 7; }
+
 __device__ __forceinline__ v8i read_frag16(const uint8_t* lds, int row, int q) {
-  const int sw = swz128(row);
+  const int sw = swz16(row);
   const v4i* base = reinterpret_cast<const v4i*>(lds + row * 128);
-  const v4i lo = base[(2 * q) ^ sw];
-  const v4i hi = base[(2 * q + 1) ^ sw];
+  const v4i lo = base[q ^ sw];
+  const v4i hi = base[(q + 4) ^ sw];
   v8i r;
   r[0] = lo[0]; r[1] = lo[1]; r[2] = lo[2]; r[3] = lo[3];
   r[4] = hi[0]; r[5] = hi[1]; r[6] = hi[2]; r[7] = hi[3];
@@ -1027,17 +1032,16 @@ __global__ __launch_bounds__(512) void gemm_fp8_promo_kernel(
   const int r16 = lane & 15, q16 = lane >> 4;
 
   // Operand loads of one block: slab j of a wave is tile rows
-  // row0 + 8 j, row0 = 32 wave + lane / 8 (A and W alike, 4 slabs each),
-  // and a lane's 16-byte chunk (lane % 8) ^ ((row >> 1) % 8) is c0 for
-  // even j and c0 ^ 4 for odd j. The per-lane part of an address is a
-  // 32-bit offset over a wave-uniform base (the launcher checks that a
-  // tile's rows span less than 4 GiB); token rows past M clamp to M - 1.
+  // row0 + 8 j, row0 = 32 wave + lane / 8 (A and W alike, 4 slabs each);
+  // lane p = lane % 8 of a row writes LDS position p, which holds global
+  // chunk p ^ (row % 8) = p ^ (lane / 8), the same for every slab. The
+  // per-lane part of an address is a 32-bit offset over a wave-uniform base
+  // (the launcher checks that a tile's rows span less than 4 GiB); token
+  // rows past M clamp to M - 1.
   static_assert(Cfg::kASlabs == 4 && Cfg::kWSlabs == 4, "slab walk");
   const int row0 = wave * 32 + (lane >> 3);
-  const uint32_t chunk0 = (uint32_t)(((lane & 7) ^ swz128(row0)) * 16);
-  const uint32_t chunk1 = chunk0 ^ 64u;
-  const uint32_t w_lane0 = (uint32_t)row0 * (uint32_t)K + chunk0;
-  const uint32_t w_lane1 = (uint32_t)row0 * (uint32_t)K + chunk1;
+  const uint32_t chunk = (uint32_t)(((lane & 7) ^ swz16(row0)) * 16);
+  const uint32_t w_lane = (uint32_t)row0 * (uint32_t)K + chunk;
   float sw_next = 0.0f;  // the weight scale of the block in flight
   // the block to load: its tile, 128-K block and stage
   struct Blk {
@@ -1068,7 +1072,7 @@ __global__ __launch_bounds__(512) void gemm_fp8_promo_kernel(
     if (j < 4) {
       const int row = row0 + 8 * j;
       const uint32_t crow = (uint32_t)(row < b.m_last ? row : b.m_last);
-      const uint32_t off = crow * (uint32_t)lda + ((j & 1) ? chunk1 : chunk0);
+      const uint32_t off = crow * (uint32_t)lda + chunk;
       __builtin_amdgcn_global_load_lds((const void*)(b.a + off),
                                        (lds_void*)(b.buf + (wave * 4 + j) * 1024), 16, 0,
                                        kOperandLoadPolicy);
@@ -1077,7 +1081,7 @@ __global__ __launch_bounds__(512) void gemm_fp8_promo_kernel(
       // uniform row shift of slab jw (SwiGLU: rows 128.. are up rows)
       const int shift = 8 * jw + (SWIGLU && wave * 4 + jw >= 16 ? (N >> 1) - 128 : 0);
       __builtin_amdgcn_global_load_lds(
-          (const void*)(b.w + (int64_t)shift * K + ((jw & 1) ? w_lane1 : w_lane0)),
+          (const void*)(b.w + (int64_t)shift * K + w_lane),
           (lds_void*)(b.buf + Cfg::kABytes + (wave * 4 + jw) * 1024), 16, 0,
           kOperandLoadPolicy);
     } else {
