@@ -30,7 +30,16 @@
 extern "C" {
 #endif
 
-/* Library version (1). */
+/*
+ * ABI version of the library: qx_version() returns the QX_ABI_VERSION it
+ * was built with. It is raised whenever an entry point changes its
+ * arguments or their meaning, so that a caller built against another
+ * header fails at load time instead of passing arguments in the wrong
+ * slots. 1: the first release. 2: qx_paged_attention and
+ * qx_paged_attention_work take tile_rows, qx_paged_attention and
+ * qx_attention_lse take v_bf16, qx_qk_norm_rope_kv takes v_f16.
+ */
+#define QX_ABI_VERSION 2
 int qx_version(void);
 
 /* Text of the last argument error on the calling thread. */
@@ -63,9 +72,13 @@ int qx_device_is_gfx950(void);
  * Configs 10, 11, 12 and 22 rescale the accumulators in place
  * (acc *= s_prev / s per block, the last s in the epilogue) and compute
  * each element with the same operations in the same order: their results
- * are bit-identical. Config 30 sums in another order (within the bf16
- * tolerance of them and of the dequantized product); a caller that needs a
- * row's result independent of M picks the family by N alone.
+ * are bit-identical for finite operands. A weight block whose scale is 0
+ * is skipped by 10, 11 and 22 and run on zeroed weight rows by 12, so a
+ * NaN activation code in such a block gives 0 under 10/11/22 and NaN under
+ * 12; config 30 adds 0 * partial, NaN as well, as DeepGEMM's promotion
+ * does. Config 30 sums in another order (within the bf16 tolerance of them
+ * and of the dequantized product); a caller that needs a row's result
+ * independent of M picks the family by N alone.
  */
 int qx_gemm_fp8_blockscaled(const void* A, const float* sA, const void* W, const float* sW,
                             void* C, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldc,
@@ -236,6 +249,17 @@ int qx_kv_scatter(const void* k, int64_t k_ld, const void* v, int64_t v_ld, void
 /* out[i] = table[ids[i]] (bf16 rows). Replaces vLLM embed_tokens (qwen3.py:123). */
 int qx_embed(const void* table, int64_t t_ld, const int64_t* ids, void* out, int64_t o_ld,
              int64_t n, int64_t H, hipStream_t stream);
+
+/*
+ * The most keys (used[s]) one sequence of a paged attention call may have:
+ * 2048 pages of `page` tokens (32,768 at the arena's 16), the page-table
+ * row each workgroup stages in LDS. Host only; -1 (message in
+ * qx_last_error()) for a page size the kernels do not take. No counterpart
+ * in the reference (its paged kernel takes any block-table width); callers
+ * refuse longer documents at admission (StageAdmission) rather than at the
+ * first attention launch.
+ */
+int64_t qx_paged_attention_max_keys(int64_t page);
 
 /*
  * Varlen GQA attention reading bf16 K and a bf16 (v_bf16 = 1, the

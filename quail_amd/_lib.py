@@ -19,6 +19,9 @@ _i64 = ctypes.c_int64
 _i32 = ctypes.c_int
 _f32 = ctypes.c_float
 
+# QX_ABI_VERSION of include/quail_mi355x.h, which these signatures follow
+ABI_VERSION = 2
+
 # name -> argument types (the declarations in include/quail_mi355x.h)
 SIGNATURES = {
     "qx_version": [],
@@ -50,6 +53,7 @@ SIGNATURES = {
                            _i64, _i64, _f32, _i32, _p, _p, _i64, _p, _i64, _p, _i64, _i64, _i32,
                            _p],
     "qx_paged_attention_tile_rows": [_p, _p, _i64, _i64, _i64, _i64, _i32],
+    "qx_paged_attention_max_keys": [_i64],
     "qx_paged_attention_qnorm": [_p, _i64, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64,
                                  _i64, _i64, _i64, _f32, _i32, _p, _i64, _p, _i64, _p, _i64,
                                  _i64, _i32, _p, _p, _i32, _p, _f32, _p],
@@ -85,7 +89,8 @@ SIGNATURES = {
 
 
 # entry points returning a count (>= 0) or -1 instead of a status
-RETURNS_COUNT = {"qx_paged_attention_work", "qx_paged_attention_tile_rows", "qx_vocab_logprobs_workspace",
+RETURNS_COUNT = {"qx_paged_attention_work", "qx_paged_attention_tile_rows",
+                 "qx_paged_attention_max_keys", "qx_vocab_logprobs_workspace",
                  "qx_vocab_logprobs_noalloc_max_bytes"}
 
 
@@ -117,6 +122,10 @@ def load(path: Path = LIB_PATH):
         fn.argtypes = argtypes
         fn.restype = (ctypes.c_char_p if name == "qx_last_error" else
                       ctypes.c_int64 if name in RETURNS_COUNT else ctypes.c_int)
+    built = lib.qx_version()
+    if built != ABI_VERSION:
+        raise QxUnavailable(f"{path} has ABI version {built}; this binding (and "
+                            f"include/quail_mi355x.h) is version {ABI_VERSION}: rebuild it")
     _LIB = lib
     return lib
 
@@ -140,6 +149,12 @@ def count(name: str, *args) -> int:
     if n < 0:
         raise QxError(f"{name}: {lib.qx_last_error().decode(errors='replace')}")
     return int(n)
+
+
+def header_abi_version(header: Path = HEADER) -> int:
+    """QX_ABI_VERSION as include/quail_mi355x.h defines it."""
+    import re
+    return int(re.search(r"#define\s+QX_ABI_VERSION\s+(\d+)", header.read_text()).group(1))
 
 
 def declared_symbols(header: Path = HEADER) -> list:

@@ -32,6 +32,8 @@ from collections import deque
 
 import numpy as np
 
+from quail_amd import _lib
+
 QUEUED, ADMITTED, LENDABLE = 0, 1, 2
 WAIT = "wait"
 
@@ -64,6 +66,9 @@ class StageAdmission:
         self.tree_parent = [None] * n if tree is None else list(tree.parent)
         self.tree_shared = [0] * n if tree is None else [int(s) for s in tree.shared]
         self.suffix_rows = [int(sum(len(s) for s in sufs)) for sufs in self.suffixes]
+        # the attention kernel's page-table row: longer documents are
+        # refused here, not at their first attention launch
+        max_keys = _lib.count("qx_paged_attention_max_keys", arena.page_tokens)
         for d in range(n):
             if self.suffix_rows[d] > self.chunk_budget:
                 raise OversizedDocumentError(
@@ -73,6 +78,11 @@ class StageAdmission:
             if need > arena.num_pages:
                 raise OversizedDocumentError(
                     d, f"{need} KV pages, more than the {arena.num_pages} of the whole arena")
+            keys = len(self.prefixes[d]) + self.suffix_rows[d]
+            if keys > max_keys:
+                raise OversizedDocumentError(
+                    d, f"{keys} tokens, more keys than the paged attention's {max_keys} "
+                       f"per sequence")
         self.state = [QUEUED] * n
         # document -> (parent, tokens read from it); documents that read none are absent
         self.lender = {}

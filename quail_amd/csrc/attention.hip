@@ -844,6 +844,16 @@ int attention_impl(const void* q, int64_t q_ld, const int64_t* q_index, const vo
 extern "C" {
 
 
+// The most keys one sequence of a paged call may see: the page-table row a
+// workgroup stages in LDS holds kMaxPages entries.
+int64_t qx_paged_attention_max_keys(int64_t page) {
+  if (page != qx::kPage) {
+    qx::set_error("attention: page of %lld tokens (the arena uses 16)", (long long)page);
+    return -1;
+  }
+  return (int64_t)qx::kMaxPages * page;
+}
+
 // out_fp8 != NULL: write the e4m3 o_proj input and its scales (D must be
 // 128); otherwise write bf16 to out_bf16. o_ld is in elements of the output.
 // v_bf16: the V pool holds bf16 (the reference arena's pools), else fp16.

@@ -18,7 +18,7 @@ void set_error(const char* fmt, ...) {
 
 extern "C" {
 
-int qx_version(void) { return 1; }
+int qx_version(void) { return QX_LIBRARY_ABI_VERSION; }
 
 const char* qx_last_error(void) { return qx::g_error; }
 

@@ -546,8 +546,10 @@ __device__ __forceinline__ void n320_tile(
           // its weight rows of that block in this stage (the other waves
           // reading them write the same zeros), its tiles' accumulators are
           // rescaled by exactly 1 and keep their s_prev, and their MFMAs add
-          // +0 to sums that start at +0: bit for bit what skipping does.
-          // Rare (real checkpoints have no all-zero weight blocks).
+          // +0 to sums that start at +0: bit for bit what skipping does for
+          // finite activation codes (a NaN code gives 0 * NaN = NaN here, 0
+          // where the block is skipped). Rare (real checkpoints have no
+          // all-zero weight blocks).
           // (out of line: the main loop keeps its registers)
           zero_weight_rows(w_lds + wn * TN * 32 * 128, live0 ? SPLIT * 32 : 0,
                            live1 ? SPLIT * 32 : TN * 32, lane);

@@ -45,13 +45,19 @@ __device__ __forceinline__ float round_bf16(float f) {
   return bf16_to_f32(f32_to_bf16(f));
 }
 
+// x clamped to +-448; NaN stays NaN, as torch.clamp keeps it (fminf and
+// fmaxf alone would turn it into -448)
+__device__ __forceinline__ float clamp_fp8_range(float x) {
+  return x != x ? x : fminf(fmaxf(x, -kFp8Max), kFp8Max);
+}
+
 // Four fp32 values -> four packed e4m3fn bytes (little-endian order), with
 // the clamp to +-448 applied first.
 __device__ __forceinline__ uint32_t pack4_fp8(float a, float b, float c, float d) {
-  a = fminf(fmaxf(a, -kFp8Max), kFp8Max);
-  b = fminf(fmaxf(b, -kFp8Max), kFp8Max);
-  c = fminf(fmaxf(c, -kFp8Max), kFp8Max);
-  d = fminf(fmaxf(d, -kFp8Max), kFp8Max);
+  a = clamp_fp8_range(a);
+  b = clamp_fp8_range(b);
+  c = clamp_fp8_range(c);
+  d = clamp_fp8_range(d);
   int v = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
   v = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, v, true);
   return static_cast<uint32_t>(v);
@@ -69,11 +75,17 @@ __device__ __forceinline__ uint32_t pack2_bf16(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, v);
 }
 
+// fp32 clamped to fp16's finite range; NaN stays NaN (fminf / fmaxf return
+// the operand that is not NaN, so NaN is passed around the clamp)
+__device__ __forceinline__ float clamp_f16_range(float x) {
+  return x != x ? x : fminf(fmaxf(x, -65504.0f), 65504.0f);
+}
+
 // Two fp32 -> packed fp16, round to nearest even, saturated at +-65504 (a
-// value past fp16's range becomes its largest finite value, not inf).
+// value past fp16's range, infinities included, becomes its largest finite
+// value; NaN stays NaN, as it does in the reference's bf16 pools).
 __device__ __forceinline__ uint32_t pack2_f16_sat(float lo, float hi) {
-  const f16x2 v = {(_Float16)fminf(fmaxf(lo, -65504.0f), 65504.0f),
-                   (_Float16)fminf(fmaxf(hi, -65504.0f), 65504.0f)};
+  const f16x2 v = {(_Float16)clamp_f16_range(lo), (_Float16)clamp_f16_range(hi)};
   return __builtin_bit_cast(uint32_t, v);
 }
 

@@ -7,6 +7,10 @@
 #define QX_EINVAL (-1)
 #endif
 
+// The ABI version qx_version() reports; equal to QX_ABI_VERSION of
+// include/quail_mi355x.h (a CPU test compares the two).
+#define QX_LIBRARY_ABI_VERSION 2
+
 namespace qx {
 void set_error(const char* fmt, ...);
 }

@@ -519,6 +519,22 @@ def test_kv_scatter_is_bit_exact_and_skips_negative_rows(v_dtype):
         want = big.float().clamp(-65504, 65504).half()
         assert torch.equal(vp[3].reshape(1, -1), want)
         assert bool(torch.isfinite(vp[3]).all())
+    # NaN stays NaN in either pool type; +-inf saturates to +-65504 in fp16
+    # pools and stays inf in bf16 ones
+    odd = torch.ones((1, hk * d), dtype=torch.bfloat16, device=DEV)
+    odd[0, 0::3] = float("nan")
+    odd[0, 1::3] = float("inf")
+    odd[0, 2::6] = float("-inf")
+    eng.kv_row_scatter(odd, odd, torch.zeros(1, dtype=torch.long, device=DEV),
+                       torch.full((1,), 4, dtype=torch.long, device=DEV), 0)
+    got = vp[4].reshape(-1).float().cpu()
+    src = odd.reshape(-1).float().cpu()
+    nan = torch.isnan(src)
+    assert torch.equal(torch.isnan(got), nan)
+    if v_dtype == torch.bfloat16:
+        assert torch.equal(got[~nan], src[~nan])
+    else:
+        assert torch.equal(got[~nan], src[~nan].clamp(-65504, 65504))
 
 
 def _paged_case(seed, hq, hk, d, page, seqs, pool_pages):

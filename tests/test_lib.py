@@ -16,7 +16,7 @@ def test_library_exports_every_declared_symbol():
     missing = [name for name in declared if not hasattr(lib, name)]
     assert not missing
     assert set(declared) == set(_lib.SIGNATURES)
-    assert lib.qx_version() == 1
+    assert lib.qx_version() == _lib.ABI_VERSION == _lib.header_abi_version()
 
 
 def test_argument_errors_return_minus_one_with_a_message():

@@ -23,6 +23,7 @@ import pytest
 import torch
 
 from oracle import qwen3_ref as ref
+from quail_amd import _lib
 from quail_amd.admission import OversizedDocumentError, StageAdmission
 from quail_amd.arena import KVArena
 from quail_amd.executor import StageRun
@@ -211,6 +212,24 @@ def test_oversized_documents_are_refused_up_front():
     with pytest.raises(OversizedDocumentError, match="question rows"):
         StageAdmission([docs[0][:10]], [[docs[0][10:200]]], KVArena(
             CFG.layers, 64, PAGE, CFG.kv_heads, CFG.head_dim, device="cpu"), 100)
+
+
+def test_documents_past_the_attention_key_limit_are_refused_up_front():
+    """The paged attention stages at most 2048 page ids (32,768 keys at
+    16-token pages) per sequence: a longer document passes the arena and
+    chunked-prefill checks but is refused at admission; one at the limit
+    is admitted."""
+    limit = _lib.count("qx_paged_attention_max_keys", PAGE)
+    assert limit == 2048 * PAGE
+    arena = KVArena(1, 4096, PAGE, CFG.kv_heads, CFG.head_dim, device="cpu")
+    rng = np.random.default_rng(0)
+    long_doc = rng.integers(0, CFG.vocab, limit + 1)
+    with pytest.raises(OversizedDocumentError, match="32768 per sequence"):
+        StageAdmission([long_doc[:-1]], [[long_doc[-1:]]], arena, 16384)
+    ok = long_doc[:limit]
+    StageAdmission([ok[:-1]], [[ok[-1:]]], arena, 16384)
+    with pytest.raises(_lib.QxError, match="page of 32 tokens"):
+        _lib.count("qx_paged_attention_max_keys", 32)
 
 
 def test_children_wait_for_a_parent_mid_prefill():
