@@ -52,6 +52,7 @@ class KVArena:
         # probability instead of 8)
         self.v = [p.view(self.v_dtype).view(rows, heads, dim) for p in parts[1::2]]
         self._holds = {}
+        self._reading = {}
         self._deferred = set()
 
     # ---- sizes -------------------------------------------------------------
@@ -118,34 +119,56 @@ class KVArena:
         return self.accounting.alloc(key, tokens, capacity_tokens,
                                      borrowed=self._borrow_plan(borrow))
 
-    def _evict_for_pages(self, need: int) -> None:
+    def _evict_until(self, satisfied) -> tuple:
+        """Free retained keys in the accounting's victim order until
+        satisfied() holds (arena.py:478-492); a key a queued borrower will
+        read (held) or that an admission is reading is never a victim.
+        Returns the evicted keys."""
         acct = self.accounting
-        while need > acct.free_pages:
-            victim = acct.pop_retained_victim(keep=frozenset(self._holds))
-            if victim is None:
-                return
-            key, pages, tokens = victim
-            self.evicted_keys += 1
-            self.evicted_prefix_tokens += tokens
-            self.evicted_pages += acct.free_key(key)
-
-    def evict_retained(self, pages_needed: int) -> tuple:
-        """Free retained keys nothing holds, oldest-priority first, until
-        pages_needed pages have come free (arena.py:468-492). Returns the
-        evicted keys."""
-        acct = self.accounting
-        start = acct.free_pages
+        keep = frozenset(self._holds) | frozenset(self._reading)
         keys = []
-        while acct.free_pages - start < pages_needed:
-            victim = acct.pop_retained_victim(keep=frozenset(self._holds))
+        while not satisfied():
+            victim = acct.pop_retained_victim(keep=keep)
             if victim is None:
                 break
-            key, pages, tokens = victim
+            key, _, tokens = victim
             self.evicted_keys += 1
             self.evicted_prefix_tokens += tokens
-            self.evicted_pages += acct.free_key(key)
+            self.evicted_pages += self.free_key(key)
             keys.append(key)
         return tuple(keys)
+
+    def _evict_for_pages(self, need: int) -> None:
+        self._evict_until(lambda: self.accounting.free_pages >= need)
+
+    def evict_retained(self, pages_needed: int) -> tuple:
+        """Free retained keys until pages_needed pages have come free
+        (arena.py:468-476). Returns the evicted keys."""
+        start = self.accounting.free_pages
+        return self._evict_until(lambda: self.accounting.free_pages - start >= pages_needed)
+
+    def reserve(self, key, tokens: int, *, capacity_tokens: int, borrow=None,
+                extension=False, share_points=()) -> bool:
+        """Pages for an admitted document (arena.py:584-642): retained KV is
+        evicted until its capacity fits, never the document's own pages or
+        the parent it borrows from; then it is activated (pinned). False
+        leaves it as it was (evictions may have happened)."""
+        acct = self.accounting
+        if acct.is_resident(key):
+            held = len(acct.table_pages(key))
+        else:
+            held = len(self._borrow_plan(borrow))
+        need = max(0, acct.pages_needed(capacity_tokens) - held)
+        protected = (key,) if borrow is None else (key, borrow[0])
+        self.read_state(protected)
+        try:
+            self._evict_until(lambda: acct.free_pages >= need)
+            if acct.free_pages < need:
+                return False
+            return self.activate(key, tokens, capacity_tokens=capacity_tokens,
+                                 borrow=borrow) is not None
+        finally:
+            self.done_reading(protected)
 
     def activate(self, key, tokens: int, capacity_tokens=None, base_tokens=None, borrow=None):
         """Make a prefix active (pinned), evicting retained KV when needed."""
@@ -173,8 +196,10 @@ class KVArena:
         return None if pages is None else (key, pages)
 
     def free_key(self, key) -> int:
-        """Free a key's pages; a key with queued borrowers waits for them."""
-        if self._holds.get(key):
+        """Free a key's pages, or once its holds and reads are over (a key
+        queued borrowers will read, or that an admission reads, waits for
+        them). Returns the pages that went free now."""
+        if key in self._holds or key in self._reading:
             self._deferred.add(key)
             return 0
         return self.accounting.free_key(key)
@@ -182,22 +207,67 @@ class KVArena:
     def pin(self, key) -> None:
         self.accounting.pin(key)
 
-    def retain(self, key, priority=None) -> None:
+    def retain(self, key, tokens=None, priority=None) -> None:
+        """Keep a key's first `tokens` (all of them by default) for a later
+        operator; it becomes evictable."""
+        if tokens is not None:
+            self.accounting.rewind(key, tokens)
         self.accounting.retain(key, priority)
 
+    # ---- holds and reads: keys that admitted or queued readers need -------------
+
     def hold(self, key, borrowers: int) -> None:
+        """Keep a key for `borrowers` documents that will read its pages."""
         if borrowers:
             self._holds[key] = self._holds.get(key, 0) + borrowers
 
     def release(self, key) -> None:
-        if key not in self._holds:
+        """One borrower of the key was admitted, or will not come."""
+        count = self._holds.get(key)
+        if count is None:
             return
-        self._holds[key] -= 1
-        if not self._holds[key]:
-            del self._holds[key]
-            if key in self._deferred:
+        if count > 1:
+            self._holds[key] = count - 1
+        else:
+            self._drop_hold(key)
+
+    def _drop_hold(self, key) -> None:
+        del self._holds[key]
+        if key in self._deferred and key not in self._reading:
+            self._deferred.discard(key)
+            self.free_key(key)
+
+    def drop_holds(self, keys=None) -> bool:
+        """Release every hold on the keys (all by default): freed keys go
+        free, retained ones become evictable. True when any hold went."""
+        keys = list(self._holds) if keys is None else [k for k in keys if k in self._holds]
+        for key in keys:
+            self._drop_hold(key)
+        return bool(keys)
+
+    def read_state(self, keys) -> None:
+        """Keep each key's pages until done_reading for the same keys."""
+        for key in keys:
+            self._reading[key] = self._reading.get(key, 0) + 1
+
+    def done_reading(self, keys) -> None:
+        for key in keys:
+            left = self._reading[key] - 1
+            if left:
+                self._reading[key] = left
+                continue
+            del self._reading[key]
+            if key in self._deferred and key not in self._holds:
                 self._deferred.discard(key)
                 self.free_key(key)
+
+    def origin(self, tokens: int) -> int:
+        """The first row a key's pages must hold for a borrower of `tokens`
+        rows: 0 (every layer keeps every row; no sliding window)."""
+        return 0
+
+    def keep_window(self, key, shared: int) -> None:
+        """No sliding window: every row a borrower reads stays."""
 
     # ---- tensors read by attention ---------------------------------------------
 

@@ -649,6 +649,22 @@ class Engine:
         meta["layer"] += 1
         return out
 
+    def write_kv_only(self, q, k, v, chunk):
+        """A layer whose attention output no row reads (the last layer of a
+        pass of prefill pieces): only its K and V rows go to the pages."""
+        n = q.shape[0]
+        k3, v3 = self._kv_views(n, k, v)
+        meta = chunk.meta
+        if chunk.attention_mode == "tree":
+            layer = meta["layer"]
+            written = meta.pop("kv_fresh_layer", None) == layer
+            if meta.get("kv_src") is not None and meta["kv_src"].numel() and not written:
+                self.kv_row_scatter(k3, v3, meta["kv_src"], meta["kv_dst"], layer)
+        else:
+            self.write_kv(k3, v3, meta)
+        meta.pop("q_norm_on_load", None)
+        meta["layer"] += 1
+
     def attention_final(self, q, k, v, chunk, rows):
         """The last layer's attention: write the pack's KV (every row: later
         packs may borrow it), then attend only for `rows` (the pass's final

@@ -142,6 +142,12 @@ class Qwen3Pipeline:
             else:
                 q, k, v, residual = self.before_attention(hidden, residual, chunk.positions,
                                                           layer, chunk)
+            if index == last and not final.shape[0]:
+                # a pass of prefill pieces reads no row: later passes need
+                # only the last layer's KV from it
+                engine.write_kv_only(q, k, v, chunk)
+                return torch.empty((0, self.embed.weight.shape[1]), dtype=torch.bfloat16,
+                                   device=q.device)
             if index == last and chunk.meta.get("final_query") is not None:
                 # past the last layer's KV only the final rows matter: their
                 # attention, o_proj and MLP run alone, bit-identical to what

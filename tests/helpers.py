@@ -244,3 +244,31 @@ def exact_contractions(monkeypatch):
     monkeypatch.setattr(Engine, "gate_up_activation_quant", gate_up)
     monkeypatch.setattr(Engine, "_paged", paged)
     monkeypatch.delattr(Engine, "kv_norm_rope")
+
+
+def admit(prefixes, suffixes, arena, budget, tree=None, unified=True):
+    """StageAdmission whose admissions reserve their arena pages as the stage
+    driver's do (one question in the document's own pages on the unified
+    path, several in temporary pages)."""
+    from quail_amd.admission import StageAdmission
+
+    single = all(len(s) == 1 for s in suffixes)
+    extra = max(len(s[0]) for s in suffixes) if unified and single else 0
+    holder = {}
+
+    def reserve(d, reads, rows):
+        adm = holder["adm"]
+        parent, shared = (None, 0) if reads is None else reads
+        f = len(prefixes[d])
+        return arena.reserve(adm.keys[d], f, capacity_tokens=f + extra,
+                             borrow=(adm.keys[parent], shared) if shared else None)
+
+    adm = StageAdmission(prefixes, suffixes, arena, budget, tree=tree, extra_tokens=extra,
+                         temporary_pages=unified, reserve=reserve)
+    holder["adm"] = adm
+    return adm
+
+
+def pack_specs(adm, groups, prefills=()):
+    """The pack_chunk groups of one pass's question groups and prefill pieces."""
+    return [adm.group_spec(*g) for g in groups] + [adm.piece_spec(*p) for p in prefills]

@@ -249,10 +249,10 @@ def test_tiny_paged_oracle_agrees_on_the_same_pack():
     per-document oracle (pins pack metadata numerically), and the GPU's
     final rows match it."""
     from quail_amd.arena import KVArena
-    from quail_amd.admission import StageAdmission
     from quail_amd.chunk import InputStaging, pack_chunk, upload
     from quail_amd.prefix import PrefixIndex
     from quail_amd.qwen3 import Qwen3Pipeline
+    from tests.helpers import admit, pack_specs
 
     cfg = CONFIGS["tiny"]
     wl = make_workload("tiny", seed=2)
@@ -260,10 +260,10 @@ def test_tiny_paged_oracle_agrees_on_the_same_pack():
     arena = KVArena(cfg.layers, 256, 16, cfg.kv_heads, cfg.head_dim)
     prefixes, suffixes = wl.groups_input()
     tree = PrefixIndex(wl.prompts).tree(16)
-    adm = StageAdmission(prefixes, suffixes, arena, wl.chunk_budget, tree=tree)
-    groups = adm.next_chunk()
-    assert adm.done()
-    chunk = pack_chunk(arena, [g for _, g in groups])
+    adm = admit(prefixes, suffixes, arena, wl.chunk_budget, tree=tree)
+    groups = adm.next_chunk(arena.free_pages)
+    assert not adm.pending and not adm.take_prefills()
+    chunk = pack_chunk(arena, pack_specs(adm, groups))
     host_unified = dict(chunk.meta["unified"])
     final = chunk.final_indices.copy()
     upload(chunk, InputStaging())
@@ -274,7 +274,7 @@ def test_tiny_paged_oracle_agrees_on_the_same_pack():
              for _ in range(cfg.layers)]
     paged = ref.forward_chunk(m, chunk.host_ids, chunk.host_positions, final, host_unified,
                               pools, 16)
-    order = [d for d, _ in groups]
+    order = [d for d, *_ in groups]
     dense = ref.forward_documents(m, [wl.prompts[d] for d in order])
     torch.testing.assert_close(paged.float(), dense.float(), rtol=0.02, atol=0.02)
     rel = ((normed - dense.float()).norm() / dense.float().norm()).item()

@@ -106,10 +106,10 @@ def test_last_layer_on_final_rows_only_is_bit_identical():
     only (chunk.meta["final_query"]); without that metadata the pipeline
     runs it for every row. The final rows must not change."""
     from quail_amd.arena import KVArena
-    from quail_amd.admission import StageAdmission
     from quail_amd.chunk import InputStaging, pack_chunk, upload
     from quail_amd.prefix import PrefixIndex
     from quail_amd.qwen3 import Qwen3Pipeline
+    from tests.helpers import admit, pack_specs
 
     wl = make_workload("qwen3-8b", seed=5, documents=5)
     cfg = CONFIGS[wl.model]
@@ -119,10 +119,10 @@ def test_last_layer_on_final_rows_only_is_bit_identical():
         arena = KVArena(LAYERS, 3 * wl.chunk_budget // 16 + 64, 16, cfg.kv_heads, cfg.head_dim)
         prefixes, suffixes = wl.groups_input()
         tree = PrefixIndex(wl.prompts).tree(16)
-        adm = StageAdmission(prefixes, suffixes, arena, wl.chunk_budget, tree=tree)
-        groups = adm.next_chunk()
-        assert adm.done()
-        chunk = pack_chunk(arena, [g for _, g in groups])
+        adm = admit(prefixes, suffixes, arena, wl.chunk_budget, tree=tree)
+        groups = adm.next_chunk(arena.free_pages)
+        assert not adm.pending and not adm.take_prefills()
+        chunk = pack_chunk(arena, pack_specs(adm, groups))
         upload(chunk, InputStaging())
         if not pruned:
             chunk.meta["final_query"] = None

@@ -261,11 +261,11 @@ def test_qwen3_4b_tree_attention_equals_the_unified_attention():
     bit-identical)."""
     import dataclasses
 
-    from quail_amd.admission import StageAdmission
     from quail_amd.arena import KVArena
     from quail_amd.chunk import InputStaging, pack_chunk, upload
     from quail_amd.prefix import PrefixIndex
     from quail_amd.qwen3 import Qwen3Pipeline
+    from tests.helpers import admit, pack_specs
 
     cfg = dataclasses.replace(CONFIGS["qwen3-4b"], layers=1)
     wl = make_workload("qwen3-4b", seed=0)
@@ -279,10 +279,10 @@ def test_qwen3_4b_tree_attention_equals_the_unified_attention():
         arena = KVArena(1, 2048, 16, cfg.kv_heads, cfg.head_dim)
         pipe = Qwen3Pipeline(model, arena)
         engine = pipe.engine
-        adm = StageAdmission(prefixes, suffixes, arena, 3000, tree=tree)
+        adm = admit(prefixes, suffixes, arena, 3000, tree=tree, unified=mode == "unified")
         outs, stacked = [], 0
         for _ in range(2):
-            specs = [g for _, g in adm.next_chunk()]
+            specs = pack_specs(adm, adm.next_chunk(arena.free_pages))
             if mode == "tree":
                 specs = [dict(g, read_key=g["borrow_key"] if g["start"] else None, single=True)
                          for g in specs]

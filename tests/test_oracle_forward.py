@@ -7,13 +7,12 @@ import numpy as np
 import torch
 
 from oracle import qwen3_ref as ref
-from quail_amd.admission import StageAdmission
 from quail_amd.arena import KVArena
 from quail_amd.chunk import pack_chunk
 from quail_amd.model import CONFIGS, build_synthetic
 from quail_amd.prefix import PrefixIndex
 from quail_amd.workload import make_workload
-from tests.helpers import ref_model
+from tests.helpers import admit, pack_specs, ref_model
 
 
 def test_paged_pack_forward_equals_whole_documents():
@@ -26,20 +25,21 @@ def test_paged_pack_forward_equals_whole_documents():
     tree = PrefixIndex(wl.prompts).tree(16)
     # a small budget forces several packs; children borrow pages written by
     # an earlier pack
-    adm = StageAdmission(prefixes, suffixes, arena, chunk_budget=400, tree=tree)
+    adm = admit(prefixes, suffixes, arena, 400, tree=tree)
     pools = [(torch.zeros(96 * 16, cfg.kv_heads, cfg.head_dim, dtype=torch.bfloat16),
               torch.zeros(96 * 16, cfg.kv_heads, cfg.head_dim, dtype=torch.bfloat16))
              for _ in range(cfg.layers)]
     got = {}
     packs = 0
     while not adm.done():
-        groups = adm.next_chunk()
-        assert groups
-        chunk = pack_chunk(arena, [g for _, g in groups])
+        groups = adm.next_chunk(arena.free_pages)
+        assert groups and not adm.take_prefills()
+        chunk = pack_chunk(arena, pack_specs(adm, groups))
         normed = ref.forward_chunk(m, chunk.host_ids, chunk.host_positions,
                                    chunk.final_indices, chunk.meta["unified"], pools, 16)
-        for i, (d, _) in enumerate(groups):
+        for i, (d, first, end, _) in enumerate(groups):
             got[d] = normed[i]
+            adm.report(d, first, end, [True])
         packs += 1
     assert packs >= 2
     assert adm.borrowed_tokens > 0

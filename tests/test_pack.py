@@ -6,10 +6,10 @@ import numpy as np
 import pytest
 
 from oracle.packing_ref import PoolModel, check_pack
-from quail_amd.admission import StageAdmission
 from quail_amd.arena import KVArena
 from quail_amd.chunk import pack_chunk
 from quail_amd.prefix import PrefixIndex
+from tests.helpers import admit, pack_specs
 
 
 def plain_arena(pages=64, page=16, layers=1):
@@ -92,33 +92,36 @@ def test_packs_read_exactly_their_documents(seed):
     prefixes = [d[:-1] for d in docs]
     suffixes = [[d[-1:]] for d in docs]
     tree = PrefixIndex(docs).tree(16)
-    adm = StageAdmission(prefixes, suffixes, arena, chunk_budget=256, tree=tree)
+    adm = admit(prefixes, suffixes, arena, 256, tree=tree)
     pool = PoolModel()
     prompts = {adm.keys[i]: d for i, d in enumerate(docs)}
     checked = 0
     packs = 0
     live = []
-    while not adm.done():
-        groups = adm.next_chunk()
-        if not groups:
-            assert live, "nothing admitted and nothing to free"
-            # free the oldest pack's documents (the loop reads answers one pack late)
-            for d in live.pop(0):
-                pages = arena.owned_pages(adm.keys[d])
+
+    def settle():
+        # the loop reads answers one pack late; a finished document's pages go free
+        for d, first, end, _ in live.pop(0):
+            if adm.report(d, first, end, [0] * (end - first)):
                 arena.free_key(adm.keys[d])
+
+    while not adm.done():
+        groups = adm.next_chunk(arena.free_pages)
+        prefills = adm.take_prefills()
+        if not groups and not prefills:
+            assert live, "nothing admitted and nothing to free"
+            settle()
             continue
-        chunk = pack_chunk(arena, [g for _, g in groups])
+        chunk = pack_chunk(arena, pack_specs(adm, groups, prefills))
         checked += check_pack(chunk, 16, pool, prompts.__getitem__)
         for temp in chunk.temporary_keys:
             arena.free_key(temp)
-        live.append([d for d, _ in groups])
+        live.append(groups)
         packs += 1
         if len(live) > 1:
-            for d in live.pop(0):
-                arena.free_key(adm.keys[d])
-    for docs_left in live:
-        for d in docs_left:
-            arena.free_key(adm.keys[d])
+            settle()
+    while live:
+        settle()
     total = sum(len(d) for d in docs)
     assert checked == total - adm.borrowed_tokens
     assert packs >= 2
@@ -131,14 +134,13 @@ def test_borrowers_read_parent_pages_written_in_the_same_pack():
     docs = [prefix + [100 + i] * (3 + i) for i in range(5)]
     arena = plain_arena()
     tree = PrefixIndex(docs).tree(16)
-    adm = StageAdmission([d[:-1] for d in docs], [[d[-1:]] for d in docs], arena,
-                         chunk_budget=1024, tree=tree)
-    groups = adm.next_chunk()
-    assert len(groups) == 5 and adm.done()
-    starts = [g["start"] for _, g in groups]
-    assert starts == [0, 32, 32, 32, 32]
-    root = groups[0][1]["key"]
-    chunk = pack_chunk(arena, [g for _, g in groups])
+    adm = admit([d[:-1] for d in docs], [[d[-1:]] for d in docs], arena, 1024, tree=tree)
+    groups = adm.next_chunk(arena.free_pages)
+    assert len(groups) == 5 and not adm.pending
+    specs = pack_specs(adm, groups)
+    assert [g["start"] for g in specs] == [0, 32, 32, 32, 32]
+    root = specs[0]["key"]
+    chunk = pack_chunk(arena, specs)
     u = chunk.meta["unified"]
     root_pages = arena.owned_pages(root)[:2]
     for s in range(1, 5):

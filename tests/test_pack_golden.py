@@ -17,11 +17,11 @@ from pathlib import Path
 import numpy as np
 import pytest
 
-from quail_amd.admission import StageAdmission
 from quail_amd.arena import KVArena
 from quail_amd.chunk import pack_chunk
 from quail_amd.prefix import PrefixIndex
 from quail_amd.workload import make_workload
+from tests.helpers import admit, pack_specs
 
 GOLDEN = Path(__file__).resolve().parent / "golden" / "pack_vectors.npz"
 PAGE = 16
@@ -40,12 +40,13 @@ def _packs(name):
     prompts = [np.asarray(p, dtype=np.int64) for p in wl.prompts]
     tree = PrefixIndex([p.tolist() for p in prompts]).tree(PAGE)
     arena = KVArena(1, BIG_ARENA, PAGE, 1, 2, device="cpu")
-    adm = StageAdmission([p[:-1] for p in prompts], [[p[-1:]] for p in prompts], arena,
-                         wl.chunk_budget, tree=tree)
+    adm = admit([p[:-1] for p in prompts], [[p[-1:]] for p in prompts], arena,
+                wl.chunk_budget, tree=tree)
     for _ in range(PACKS[name]):
-        groups = adm.next_chunk()
-        docs = [d for d, _ in groups]
-        chunk = pack_chunk(arena, [g for _, g in groups])
+        groups = adm.next_chunk(arena.free_pages)
+        assert not adm.take_prefills()
+        docs = [d for d, *_ in groups]
+        chunk = pack_chunk(arena, pack_specs(adm, groups))
         yield adm, arena, docs, chunk
 
 

@@ -8,10 +8,10 @@ import numpy as np
 import pytest
 
 from oracle.packing_ref import PoolModel, check_pack_tree
-from quail_amd.admission import StageAdmission
 from quail_amd.arena import KVArena
 from quail_amd.chunk import pack_chunk
 from quail_amd.prefix import PrefixIndex
+from tests.helpers import admit, pack_specs
 from tests.test_pack import _corpus
 
 
@@ -98,32 +98,36 @@ def test_tree_packs_read_exactly_their_documents(seed):
     docs = _corpus(seed, 40)
     arena = plain_arena(pages=48)
     tree = PrefixIndex(docs).tree(16)
-    adm = StageAdmission([d[:-1] for d in docs], [[d[-1:]] for d in docs], arena,
-                         chunk_budget=256, tree=tree)
+    adm = admit([d[:-1] for d in docs], [[d[-1:]] for d in docs], arena, 256, tree=tree,
+                unified=False)
     pool = PoolModel()
     prompts = {adm.keys[i]: d for i, d in enumerate(docs)}
     checked = packs = stacked = 0
     live = []
+
+    def settle():
+        for d, first, end, _ in live.pop(0):
+            if adm.report(d, first, end, [0] * (end - first)):
+                arena.free_key(adm.keys[d])
+
     while not adm.done():
-        groups = adm.next_chunk()
+        groups = adm.next_chunk(arena.free_pages)
+        assert not adm.take_prefills()
         if not groups:
             assert live
-            for d in live.pop(0):
-                arena.free_key(adm.keys[d])
+            settle()
             continue
         specs = [dict(g, read_key=g["borrow_key"] if g["start"] else None, single=True)
-                 for _, g in groups]
+                 for g in pack_specs(adm, groups)]
         stacked += sum(1 for g in specs if g["read_key"] is not None)
         chunk = pack_chunk(arena, specs, attention_mode="tree")
         checked += check_pack_tree(chunk, 16, pool, prompts.__getitem__)
-        live.append([d for d, _ in groups])
+        live.append(groups)
         packs += 1
         if len(live) > 1:
-            for d in live.pop(0):
-                arena.free_key(adm.keys[d])
-    for left in live:
-        for d in left:
-            arena.free_key(adm.keys[d])
+            settle()
+    while live:
+        settle()
     assert checked == sum(len(d) for d in docs) - adm.borrowed_tokens
     assert packs >= 2 and stacked > 0
     assert arena.free_pages == arena.num_pages
@@ -134,11 +138,11 @@ def test_siblings_share_one_stacked_read_of_their_parent():
     docs = [prefix + [100 + i] * (3 + i) for i in range(5)]
     arena = plain_arena()
     tree = PrefixIndex(docs).tree(16)
-    adm = StageAdmission([d[:-1] for d in docs], [[d[-1:]] for d in docs], arena,
-                         chunk_budget=1024, tree=tree)
-    groups = adm.next_chunk()
+    adm = admit([d[:-1] for d in docs], [[d[-1:]] for d in docs], arena, 1024, tree=tree,
+                unified=False)
+    groups = adm.next_chunk(arena.free_pages)
     specs = [dict(g, read_key=g["borrow_key"] if g["start"] else None, single=True)
-             for _, g in groups]
+             for g in pack_specs(adm, groups)]
     chunk = pack_chunk(arena, specs, attention_mode="tree")
     reads = chunk.meta["reads"]
     # the root is one segment with no reads; its four children read the

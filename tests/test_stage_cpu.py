@@ -29,7 +29,7 @@ from quail_amd.arena import KVArena
 from quail_amd.executor import StageRun
 from quail_amd.model import CONFIGS, build_synthetic
 from quail_amd.prefix import PrefixIndex
-from tests.helpers import ref_model
+from tests.helpers import admit, ref_model
 
 CFG = CONFIGS["tiny"]
 PAGE = 16
@@ -126,24 +126,31 @@ def test_document_longer_than_a_pack_is_prefilled_in_pieces():
 
 def test_admission_pieces_cover_each_prefix_once_in_order():
     """The pieces of a long document tile its prefix: consecutive, no gap,
-    none past the pack budget, and the question comes with or after the last."""
+    none past the pack budget, each filling the room the pack has left;
+    its question runs in the pack after its last piece (admission.py:
+    611-648, 760-768)."""
     docs = _docs(2, [300, 10])
     arena = KVArena(CFG.layers, 64, PAGE, CFG.kv_heads, CFG.head_dim, device="cpu")
-    adm = StageAdmission([d[:-1] for d in docs], [[d[-1:]] for d in docs], arena, 100)
-    seen = {0: [], 1: []}
+    adm = admit([d[:-1] for d in docs], [[d[-1:]] for d in docs], arena, 100)
+    pieces, questions, packs = [], {}, 0
     while not adm.done():
-        groups = adm.next_chunk()
-        assert groups
-        rows = 0
-        for d, g in groups:
-            n = 0 if g["prefix"] is None else len(g["prefix"])
-            seen[d].append((g["start"], g["start"] + n, len(g["suffixes"])))
-            rows += n + sum(len(s) for s in g["suffixes"])
+        groups = adm.next_chunk(arena.free_pages)
+        prefills = adm.take_prefills()
+        assert groups or prefills
+        rows = sum(end - start for _, start, end in prefills)
+        for d, first, end, carried in groups:
+            rows += (adm.flen[d] if carried else 0) + end - first
+            questions[d] = (packs, carried)
+            adm.report(d, first, end, [True] * (end - first))
         assert rows <= 100
-    spans = seen[0]
+        pieces += [(packs, d, start, end) for d, start, end in prefills]
+        packs += 1
+    spans = [(start, end) for _, d, start, end in pieces if d == 0]
     assert spans[0][0] == 0 and all(a[1] == b[0] for a, b in zip(spans, spans[1:]))
-    assert spans[-1][1] == len(docs[0]) - 1 and spans[-1][2] == 1
-    assert all(s[2] == 0 for s in spans[:-1])
+    assert spans[-1][1] == len(docs[0]) - 1 and len(spans) >= 3
+    last_piece = max(i for i, d, _, _ in pieces if d == 0)
+    assert questions[0] == (last_piece + 1, False)
+    assert questions[1][1]                  # the short one packs whole, with its question
 
 
 def test_tiny_arena_answers_every_document():
@@ -165,10 +172,10 @@ def _two_questions(docs):
     return [d[:-4] for d in docs], [[d[-4:-2], d[-2:]] for d in docs]
 
 
-def test_full_arena_evicts_retained_kv_then_retries():
+def test_full_arena_evicts_retained_kv():
     """Retained KV of an earlier operator fills the arena; documents with two
-    questions each need temporary question pages at pack time, which only
-    evicting the retained keys provides."""
+    questions each need their pages and temporary question pages, which only
+    evicting the retained keys provides (arena.py:584-642)."""
     model = _model(4)
     docs = _docs(4, [30, 45, 50], shared=16)
     arena = KVArena(CFG.layers, 24, PAGE, CFG.kv_heads, CFG.head_dim, device="cpu")
@@ -178,8 +185,8 @@ def test_full_arena_evicts_retained_kv_then_retries():
         arena.retain(key)
     prefixes, suffixes = _two_questions(docs)
     got, run, _ = _run(model, arena, prefixes, suffixes, budget=512)
-    assert run.stats["evict_retries"] >= 1
-    assert arena.evicted_keys >= 1
+    assert run.stats["evictions"] >= 1
+    assert arena.evicted_keys == run.stats["evictions"]
     want_a = _whole(model, [np.concatenate([p, s[0]]) for p, s in zip(prefixes, suffixes)])
     # each question follows the prefix directly (its positions restart at f)
     want_b = _whole(model, [np.concatenate([p, s[1]]) for p, s in zip(prefixes, suffixes)])
@@ -188,15 +195,34 @@ def test_full_arena_evicts_retained_kv_then_retries():
     assert arena.free_pages == arena.num_pages - arena.retained_pages
 
 
+class OptimisticRun(StageRun):
+    """Admission told `extra` more free pages than the arena has, as when
+    another operator takes pages between admission and packing: a pack's
+    temporary question pages then do not fit (ArenaFullError)."""
+
+    extra = 0
+
+    def _free_pages(self):
+        return self.arena.free_pages + self.extra
+
+
 def test_full_arena_splits_the_part():
-    """Nothing retained and nothing in flight: a pack of four two-question
-    documents whose question pages exceed the free arena runs as halves."""
+    """A pack of four two-question documents whose question pages exceed
+    the free arena, nothing retained to evict: the part runs as two halves
+    (stage_executor.py:1036-1062); every answer equals the document run
+    whole and no page leaks."""
     model = _model(5)
     docs = _docs(5, [20, 25, 30, 35], shared=0)
     prefixes, suffixes = _two_questions(docs)
-    need = sum(-(-(len(p) + 4) // PAGE) for p in prefixes)
-    arena = KVArena(CFG.layers, need + 4, PAGE, CFG.kv_heads, CFG.head_dim, device="cpu")
-    got, run, pipe = _run(model, arena, prefixes, suffixes, budget=512)
+    need = sum(-(-len(p) // PAGE) for p in prefixes)
+    # five pages past the documents' own: the four documents' question pages
+    # (2 + 2 + 2 + 4) do not fit at once, each half does
+    arena = KVArena(CFG.layers, need + 5, PAGE, CFG.kv_heads, CFG.head_dim, device="cpu")
+    pipe = OraclePipeline(model, arena)
+    run = OptimisticRun(pipe, arena, MarginReadout(pipe.m), prefixes, suffixes, 512,
+                        staging=HostStaging())
+    run.extra = 8
+    got = run.run()
     assert run.stats["splits"] >= 1
     for j in range(2):
         want = _whole(model, [np.concatenate([p, s[j]]) for p, s in zip(prefixes, suffixes)])
@@ -209,7 +235,7 @@ def test_oversized_documents_are_refused_up_front():
     docs = _docs(6, [200])
     with pytest.raises(OversizedDocumentError, match="whole arena"):
         StageAdmission([docs[0][:-1]], [[docs[0][-1:]]], arena, 1024)
-    with pytest.raises(OversizedDocumentError, match="question rows"):
+    with pytest.raises(OversizedDocumentError, match="question exceeds"):
         StageAdmission([docs[0][:10]], [[docs[0][10:200]]], KVArena(
             CFG.layers, 64, PAGE, CFG.kv_heads, CFG.head_dim, device="cpu"), 100)
 
@@ -242,16 +268,17 @@ def test_children_wait_for_a_parent_mid_prefill():
     tree = PrefixIndex(docs).tree(PAGE)
     assert tree.order[0] == 0 and tree.parent[1] == 0
     arena = KVArena(CFG.layers, 64, PAGE, CFG.kv_heads, CFG.head_dim, device="cpu")
-    adm = StageAdmission([d[:-1] for d in docs], [[d[-1:]] for d in docs], arena, 100,
-                         tree=tree)
+    adm = admit([d[:-1] for d in docs], [[d[-1:]] for d in docs], arena, 100, tree=tree)
     parent = tree.order[0]
     child_doc = 1 - parent
     packs = []
     while not adm.done():
-        packs.append(adm.next_chunk())
-    first_child = next(i for i, p in enumerate(packs) if any(d == child_doc for d, _ in p))
-    last_parent_piece = max(i for i, p in enumerate(packs) for d, g in p
-                            if d == parent and g["prefix"] is not None)
-    assert first_child >= last_parent_piece
-    g = next(g for d, g in packs[first_child] if d == child_doc)
-    assert g["start"] == tree.shared[child_doc] > 0
+        groups = adm.next_chunk(arena.free_pages)
+        packs.append((groups, adm.take_prefills()))
+        for d, first, end, _ in groups:
+            adm.report(d, first, end, [True] * (end - first))
+    first_child = next(i for i, (g, _) in enumerate(packs) if any(x[0] == child_doc for x in g))
+    last_parent_piece = max(i for i, (_, p) in enumerate(packs) for d, _, _ in p if d == parent)
+    assert first_child > last_parent_piece
+    assert adm.shared(child_doc) == tree.shared[child_doc] > 0
+    assert adm.parent(child_doc) == parent
