@@ -59,8 +59,9 @@ class StageRun:
         self.stats = dict(chunks=0, fresh_tokens=0, borrowed_tokens=0, pack_s=0.0,
                           admission_s=0.0, prefill_pieces=0, splits=0, evict_retries=0,
                           evictions=0, drop_holds=0)
-        # per pass: (groups, prefill pieces), in launch order
+        # per pass: (groups, prefill pieces) and its rows, in launch order
         self.passes = []
+        self.pass_rows = []
 
     # ---- admission callbacks ----------------------------------------------------------
 
@@ -221,6 +222,7 @@ class StageRun:
                  + [adm.piece_spec(*p) for p in prefills])
         chunk = self._pack(specs)
         self.passes.append((list(groups), list(prefills)))
+        self.pass_rows.append(int(chunk.tokens))
         self.stats["chunks"] += 1
         self.stats["fresh_tokens"] += chunk.tokens
         try:
