@@ -11,22 +11,26 @@
 //   C  : M x N bf16, row-major, leading dimension ldc (elements)
 //
 // Design (MI355X / CDNA4):
-//   * v_mfma_f32_32x32x64_f8f6f4 does the products; the MFMA "A" operand is
-//     the weight tile and "B" the token tile, so a 32x32 output tile holds
-//     one token per lane column: the token scale is one value per lane per
-//     tile and the weight scale one value per wave;
-//   * the scales change every 128 of K. Instead of promoting each 128-K
-//     partial from a temporary, the accumulator is kept in units of the
-//     current block's scale s = sA * sW: entering block kb it is multiplied
-//     by s_(kb-1) / s_kb and the MFMAs accumulate the raw FP8 products into
-//     it; the epilogue multiplies by the last block's scale. That is
-//     sum_kb s_kb P_kb as the reference defines it, with no temporaries and
+//   * the MFMA "A" operand is the weight tile and "B" the token tile, so an
+//     output tile holds one token per lane column: the token scale is one
+//     value per lane per tile and the weight scale one value per wave;
+//   * the scales change every 128 of K. Two arithmetic families compute
+//     sum_kb s_kb P_kb (s = sA * sW, P_kb the block's FP8 products):
+//       - rescale (configs 10, 11, 12, 22; v_mfma_scale_f32_32x32x64_f8f6f4
+//         with unit scales): the accumulator is kept in units of the
+//         current block's scale; entering block kb it is multiplied by
+//         s_(kb-1) / s_kb and the MFMAs accumulate the raw products into it;
+//         the epilogue multiplies by the last block's scale. No temporaries;
+//       - promotion (config 30; v_mfma_scale_f32_16x16x128_f8f6f4 with unit
+//         scales): each block's products are summed from zero by one MFMA
+//         per 16 x 16 tile and promoted into an fp32 total on the VALU,
+//         total += s_kb * P_kb;
 //   * operand tiles go HBM -> LDS with global_load_lds_dwordx4 (no VGPR
 //     staging), one 128-K scale block per pipeline stage (two stages), so
 //     the next block's loads are in flight while one is consumed. A stage
-//     row is 128 B (8 chunks of 16 B), chunk-swizzled by ((row >> 1) & 7)
-//     so the rows one ds_read_b128 phase touches cover all 64 LDS banks;
-//     rows of one ds_read_b128 phase cover all 64 LDS banks;
+//     row is 128 B (8 chunks of 16 B), chunk-swizzled so that the rows one
+//     ds_read_b128 phase touches cover all 64 LDS banks: by ((row >> 1) & 7)
+//     for the 32x32 fragments, by (row & 7) for the 16x16 ones;
 //   * workgroups are remapped so each XCD (8 per MI355X, each with its own
 //     L2) runs a contiguous band of tiles that share operands.
 #include <type_traits>
@@ -1041,10 +1045,10 @@ __global__ __launch_bounds__(512) void gemm_fp8_promo_kernel(
   // (the launcher checks that a tile's rows span less than 4 GiB); token
   // rows past M clamp to M - 1.
   static_assert(Cfg::kASlabs == 4 && Cfg::kWSlabs == 4, "slab walk");
+  static_assert(Cfg::kSaPerWave < 64, "a scale slot past the token scales");
   const int row0 = wave * 32 + (lane >> 3);
   const uint32_t chunk = (uint32_t)(((lane & 7) ^ swz16(row0)) * 16);
   const uint32_t w_lane = (uint32_t)row0 * (uint32_t)K + chunk;
-  float sw_next = 0.0f;  // the weight scale of the block in flight
   // the block to load: its tile, 128-K block and stage
   struct Blk {
     const uint8_t* a;  // the tile's first token row at the block's K
@@ -1067,7 +1071,10 @@ __global__ __launch_bounds__(512) void gemm_fp8_promo_kernel(
     return b;
   };
   // load op j of a block: A slabs (j < 4), weight slabs (4 <= j < 8), then
-  // the token scales and the weight scale
+  // the token scales and the weight scale, in one direct load: lane i < 32
+  // of a wave brings token scale i of its 32 rows, the lanes past them the
+  // wave's weight scale (a scalar load here would stall every LDS wait of
+  // the block behind it: the scalar and LDS counters are one)
   constexpr int kLoadOps = Cfg::kASlabs + Cfg::kWSlabs + 1;
   const int sa_row = wave * Cfg::kSaPerWave + lane % Cfg::kSaPerWave;
   auto load_op = [&](const Blk& b, int j) {
@@ -1088,10 +1095,11 @@ __global__ __launch_bounds__(512) void gemm_fp8_promo_kernel(
           kOperandLoadPolicy);
     } else {
       const int t = min(sa_row, b.m_last);
-      __builtin_amdgcn_global_load_lds((const void*)(b.sa + t),
+      // lanes past the wave's token scales carry its weight scale
+      const float* src = lane < Cfg::kSaPerWave ? b.sa + t : b.sw;
+      __builtin_amdgcn_global_load_lds((const void*)src,
                                        (lds_void*)(b.buf + Cfg::kABytes + Cfg::kWBytes + wave * 256),
                                        4, 0, 0);
-      sw_next = __builtin_nontemporal_load(b.sw);
     }
   };
   auto issue = [&](int m0_, int n0_, int kb, int stage) {
@@ -1122,7 +1130,6 @@ __global__ __launch_bounds__(512) void gemm_fp8_promo_kernel(
     for (int kb = 0; kb < KT; ++kb) {
       wait_vmcnt<0>();  // this block's operands (and earlier stores) are done
       lds_barrier();
-      const float sw = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(sw_next)));
       // the next block: this tile's, or after its last the next tile's
       // first; after the workgroup's last block, the current block again
       // (into the free stage: loads with no branch around them, drained
@@ -1137,19 +1144,31 @@ __global__ __launch_bounds__(512) void gemm_fp8_promo_kernel(
       const uint8_t* a_lds = smem + stage * Cfg::kStage;
       const uint8_t* w_lds = a_lds + Cfg::kABytes;
       const float* sa_lds = reinterpret_cast<const float*>(w_lds + Cfg::kWBytes);
-      float s[TM];
-      v8i af[TM];
+      // the block's scales (the wave's weight scale came with its token
+      // scales, in the slot past them), then the fragments in the order the
+      // first MFMAs use them: weight tile 0, the token tiles, weight tile 1
+      // (reading the weight fragments two tiles ahead hides the LDS latency
+      // that one ahead left exposed: 3-5% faster)
+      const float sw = sa_lds[wave * 64 + Cfg::kSaPerWave];
+      float sr[TM];
 #pragma unroll
       for (int b = 0; b < TM; ++b) {
         const int row = wm * TM * 16 + b * 16 + r16;
-        s[b] = sa_lds[(row / Cfg::kSaPerWave) * 64 + row % Cfg::kSaPerWave] * sw;
-        af[b] = read_frag16(a_lds, row, q16);
+        sr[b] = sa_lds[(row / Cfg::kSaPerWave) * 64 + row % Cfg::kSaPerWave];
       }
+      v8i wf = read_frag16(w_lds, wn * TN * 16 + r16, q16);
+      v8i af[TM];
+#pragma unroll
+      for (int b = 0; b < TM; ++b) af[b] = read_frag16(a_lds, wm * TM * 16 + b * 16 + r16, q16);
+      v8i wf_next = read_frag16(w_lds, wn * TN * 16 + 16 + r16, q16);
+      float s[TM];
+#pragma unroll
+      for (int b = 0; b < TM; ++b) s[b] = sr[b] * sw;
       // MFMA t (weight tile a = t / TM, token tile b = t % TM) writes
       // partial slot t % 3; each scheduling slot issues one MFMA and the
       // promotion of the partial two MFMAs older, so three partials are
-      // live and the FMAs never wait on the MFMA just issued. The next
-      // weight fragment is read at the start of the current one's MFMAs.
+      // live and the FMAs never wait on the MFMA just issued. Weight
+      // fragment a + 2 is read at the start of fragment a's MFMAs.
       constexpr int kLag = 2;
       v4f part[kLag + 1];
       auto promote = [&](int t) {
@@ -1158,13 +1177,12 @@ __global__ __launch_bounds__(512) void gemm_fp8_promo_kernel(
           tot[t / TM][t % TM][e] =
               __builtin_fmaf(s[t % TM], part[t % (kLag + 1)][e], tot[t / TM][t % TM][e]);
       };
-      v8i wf = read_frag16(w_lds, wn * TN * 16 + r16, q16);
-      v8i wf_next;
+      v8i wf_next2;
 #pragma unroll
       for (int t = 0; t < TN * TM; ++t) {
         const int a = t / TM, b = t % TM;
-        if (b == 0 && a + 1 < TN)
-          wf_next = read_frag16(w_lds, wn * TN * 16 + (a + 1) * 16 + r16, q16);
+        if (b == 0 && a + 2 < TN)
+          wf_next2 = read_frag16(w_lds, wn * TN * 16 + (a + 2) * 16 + r16, q16);
         part[t % (kLag + 1)] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
             wf, af[b], v4f{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0, 0, 0, 0);
         if (t >= kLag) promote(t - kLag);
@@ -1175,7 +1193,10 @@ __global__ __launch_bounds__(512) void gemm_fp8_promo_kernel(
         // land too close to the next barrier (3-8% slower)
         if (t < kLoadOps) load_op(nb, t);
         __builtin_amdgcn_sched_barrier(0);
-        if (b == TM - 1 && a + 1 < TN) wf = wf_next;
+        if (b == TM - 1 && a + 1 < TN) {
+          wf = wf_next;
+          wf_next = wf_next2;
+        }
       }
 #pragma unroll
       for (int t = TN * TM - kLag; t < TN * TM; ++t) promote(t);
