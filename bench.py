@@ -65,6 +65,9 @@ def parse():
     p.add_argument("--workload", default=WORKLOAD)
     p.add_argument("--seed", type=int, default=0)
     p.add_argument("--attention", choices=("unified", "tree"), default="unified")
+    p.add_argument("--v-dtype", choices=("fp16", "bf16"), default="fp16",
+                   help="type of the arena's V pages: fp16 (this engine's arena) or bf16 "
+                        "(the reference KVArena's layout)")
     p.add_argument("--cpu-seconds", type=float, default=15.0,
                    help="target wall time of the CPU baseline sample (0 skips it)")
     p.add_argument("--copy-mib", type=int, default=0,
@@ -94,6 +97,30 @@ def describe(wl, cfg, attention) -> str:
             f"{wl.describe_lengths()}, {wl.prefix_tokens}-token shared prefix in the paged "
             f"arena, {wl.chunk_budget}-row packs")
     return text + ("" if attention == "unified" else ", tree attention path")
+
+
+def issued_work(cfg, fresh, finals, final_pairs, pairs):
+    """(GEMM FLOP, attention FLOP, streaming HBM bytes) the engine issues for
+    a stage: every layer but the last on every fresh row; the last layer's
+    qkv projection, q/k norm and RoPE and KV write on every row (later packs
+    read that KV), its attention, o_proj, MLP and norms on the final rows
+    only (the rows an answer is read from). pairs: (query, key) pairs of all
+    rows in one layer; final_pairs: those of the final rows."""
+    h, i_, hq, hk, d = cfg.hidden, cfg.intermediate, cfg.heads, cfg.kv_heads, cfg.head_dim
+    shapes = dict(zip(("qkv", "o", "gate_up", "down"), cfg.linear_shapes()))
+    per_row = {k: 2.0 * kk * n for k, (kk, n) in shapes.items()}
+    layer = sum(per_row.values())
+    f_gemm = (cfg.layers - 1) * layer * fresh + per_row["qkv"] * fresh + (
+        per_row["o"] + per_row["gate_up"] + per_row["down"]) * finals
+    per_pair = 4.0 * hq * d
+    f_attn = per_pair * ((cfg.layers - 1) * pairs + final_pairs)
+    norm = 7 * h + h // 32                       # one add_rms_norm_quant
+    qk = 4 * (hq + hk) * d                       # qk_norm_rope
+    kv = 8 * hk * d                              # KV scatter
+    tail = 3 * hq * d + norm + 5 * i_            # attention quant, post norm, silu_mul_quant
+    b_stream = (cfg.layers - 1) * (2 * norm + qk + kv + 3 * hq * d + 5 * i_) * fresh + (
+        norm + qk + kv) * fresh + tail * finals
+    return f_gemm, f_attn, b_stream
 
 
 def cpu_threads() -> int:
@@ -275,18 +302,30 @@ def summarize(directory: str, copy_mib: int) -> None:
             summarize_mfma(dispatch)
             continue
         for counter, kernels in per.items():
-            print(f"\n{counter} (KiB per dispatch)")
-            print(f"{'calls':>7} {'mean KiB':>14}  kernel")
-            for k, v in sorted(kernels.items(), key=lambda kv: -sum(kv[1])):
-                print(f"{len(v):7d} {sum(v) / len(v):14.1f}  {k}")
             copy = [v for k, v in kernels.items() if "embed_kernel" in k]
+            factor = None
+            if copy and copy_mib:
+                # the calibration copy is the largest embed dispatch
+                factor = copy_mib * 2**20 / (max(copy[0]) * 1024)
+            # mean dispatch duration of each kernel (every dispatch runs alone
+            # under --pmc), for the calibrated GB/s
+            ns = defaultdict(list)
+            for (kernel, _), d in dispatch.items():
+                ns[kernel].append(d["_ns"])
+            print(f"\n{counter} (KiB per dispatch; calibrated: x the copy's factor)")
+            print(f"{'calls':>7} {'mean KiB':>14} {'calib. MB':>10} {'avg us':>9} {'GB/s':>8}  "
+                  f"kernel")
+            for k, v in sorted(kernels.items(), key=lambda kv: -sum(kv[1])):
+                kib = sum(v) / len(v)
+                us = sum(ns[k]) / len(ns[k]) / 1e3 if ns[k] else 0.0
+                cal = kib * 1024 * factor if factor else float("nan")
+                rate = cal / (us * 1e-6) / 1e9 if us and factor else float("nan")
+                print(f"{len(v):7d} {kib:14.1f} {cal / 1e6:10.2f} {us:9.2f} {rate:8.1f}  {k}")
             gemm = [x for k, v in kernels.items() if "gemm_fp8" in k for x in v]
-            if copy and copy_mib and gemm:
-                known = copy_mib * 2**20
-                factor = known / (copy[0][-1] * 1024)
+            if factor and gemm:
                 mean = sum(gemm) / len(gemm) * 1024 * factor
                 print(f"copy calibration: {copy_mib} MiB moved, counter reads "
-                      f"{copy[0][-1] * 1024 / 2**20:.1f} MiB, factor {factor:.4f}")
+                      f"{max(copy[0]) * 1024 / 2**20:.1f} MiB, factor {factor:.4f}")
                 print(f"{counter}_bytes_per_gemm_launch = {mean:.0f}")
 
 
@@ -427,7 +466,9 @@ def main():
     if wl.function != "classify":
         retain_answer_head(model, wl.label_ids[:2])
     num_pages = 3 * wl.chunk_budget // wl.page_tokens + 64
-    arena = KVArena(cfg.layers, num_pages, wl.page_tokens, cfg.kv_heads, cfg.head_dim)
+    v_dtype = torch.bfloat16 if args.v_dtype == "bf16" else torch.float16
+    arena = KVArena(cfg.layers, num_pages, wl.page_tokens, cfg.kv_heads, cfg.head_dim,
+                    v_dtype=v_dtype)
     pipe = Qwen3Pipeline(model, arena)
     # the stage's AI function: AI.IF bits, AI.SCORE values, or the
     # AI.CLASSIFY label logits at each document's last row
@@ -524,7 +565,14 @@ def main():
     b_layer = 14 * h + h // 16 + 4 * (hq + hk) * d + 8 * hk * d + 3 * hq * d + 5 * i_
     b_stream = b_layer * cfg.layers * fresh
     t_roof = f_gemm / PEAK_FP8 + f_attn / PEAK_BF16 + b_stream / PEAK_HBM
-    e2e_frac = t_roof / (elapsed / args.steps)
+    e2e_model = t_roof / (elapsed / args.steps)
+    # the same over the work the engine issues (the last layer past its KV
+    # on final rows only): one final row per question asked
+    finals = sum(len(s) for s in suffixes)
+    final_pairs = sum(len(p) + len(q) for p, sufs in zip(prefixes, suffixes) for q in sufs)
+    i_gemm, i_attn, i_stream = issued_work(cfg, fresh, finals, final_pairs, pairs)
+    t_issued = i_gemm / PEAK_FP8 + i_attn / PEAK_BF16 + i_stream / PEAK_HBM
+    e2e_frac = t_issued / (elapsed / args.steps)
 
     log(f"timed {args.steps} steps: {elapsed:.3f} s")
     alone = None
@@ -555,10 +603,13 @@ def main():
             "workload": describe(wl, cfg, args.attention),
             "documents": docs, "fresh_tokens": fresh, "packs": stats[0]["chunks"],
             "borrowed_tokens": stats[0]["borrowed_tokens"], "attention_pairs": pairs,
-            "parallelism": "none (1 GPU)",
+            "parallelism": "none (1 GPU)", "v_pages": args.v_dtype,
         },
         "prefill_tok_s": round(tok_s, 1),
         "e2e_roofline_frac": round(e2e_frac, 4),
+        "e2e_roofline_basis": "issued work: the last layer's attention, o_proj and MLP on "
+                              "final rows only, as the engine runs it",
+        "e2e_roofline_frac_model_work": round(e2e_model, 4),
         "roofline": {
             "bound": "mfma",
             "kernel": f"FP8 block-scaled GEMM, all four {model_name(cfg)} projections: "
