@@ -328,7 +328,35 @@ __global__ __launch_bounds__(HPB * QSUB * 64, 8 / (HPB * QSUB)) void paged_atten
   // [16i, 16i+16): key i / KCH of the slab, physical chunk i % KCH, which
   // holds logical chunk (i % KCH) ^ swizzle(key); keys past the last (in
   // the last tile) re-read the last key (in bounds, never used)
+  // A wave's KPW keys of a tile lie in one page (KPW divides the page and
+  // the wave's first key is a multiple of KPW): for a tile wholly below
+  // kv_end each lane's address is the page's first row (wave-uniform) plus
+  // a byte offset that is the same for every tile
+  constexpr int KPW = kBK / NW;
+  static_assert(KPW * NW == kBK && kPage % KPW == 0 && SLABS * KEYS_PER_SLAB == KPW, "page slabs");
+  uint32_t koff[SLABS], voff[SLABS];
+#pragma unroll
+  for (int j = 0; j < SLABS; ++j) {
+    const int key = (wave * SLABS + j) * KEYS_PER_SLAB + lane / KCH;  // key within the tile
+    const uint32_t in_page = (uint32_t)((wave * KPW) % kPage + j * KEYS_PER_SLAB + lane / KCH);
+    const int p = lane % KCH;
+    koff[j] = in_page * (uint32_t)(kv_row * 2) + (uint32_t)((p ^ kswz<D>(key)) * 16);
+    voff[j] = in_page * (uint32_t)(kv_row * 2) + (uint32_t)((p ^ vswz<D>(key)) * 16);
+  }
   auto issue = [&](int t, int buf, bool v) {
+    if (t * kBK + kBK <= kv_end) {
+      const int page_slot = t * (kBK / kPage) + (wave * KPW) / kPage;
+      const int64_t row0 =
+          CONTIG ? (int64_t)kv0 + t * kBK + ((wave * KPW) / kPage) * kPage
+                 : (int64_t)__builtin_amdgcn_readfirstlane(pages_lds[page_slot]) * kPage;
+      const uint8_t* src = reinterpret_cast<const uint8_t*>((v ? vbase : kbase) + row0 * kv_row);
+#pragma unroll
+      for (int j = 0; j < SLABS; ++j) {
+        const int slab = wave * SLABS + j;
+        lds_dma16(src + (v ? voff[j] : koff[j]), (v ? v_buf(buf) : k_buf(buf)) + slab * 1024);
+      }
+      return;
+    }
 #pragma unroll
     for (int j = 0; j < SLABS; ++j) {
       const int slab = wave * SLABS + j;
@@ -402,13 +430,14 @@ __global__ __launch_bounds__(HPB * QSUB * 64, 8 / (HPB * QSUB)) void paged_atten
     // a tile every row of this wave sees whole needs no mask (wave-uniform)
     const int t0 = t * kBK;
     if (t0 + kBK <= wave_lim_min && wave_rows_full) return;
+    // key (ks, i) of this lane is t0 + half * 4 + ks * 32 + (i / 4) * 8 + i % 4:
+    // visible when that constant offset is below `room` (none for a padding row)
+    const int room = r_ok ? lim - t0 - half * 4 : -1;
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int kidx = t0 + ks * 32 + (i >> 2) * 8 + half * 4 + (i & 3);
-        sacc[ks][i] = (kidx < lim && r_ok) ? sacc[ks][i] : -INFINITY;
-      }
+      for (int i = 0; i < 16; ++i)
+        sacc[ks][i] = ks * 32 + (i >> 2) * 8 + (i & 3) < room ? sacc[ks][i] : -INFINITY;
   };
   auto softmax_pv = [&](const int buf, v16f (&sacc)[2]) {
     // the running max is kept on raw scores (scale_log2 > 0), and the scale
