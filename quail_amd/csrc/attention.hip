@@ -357,20 +357,31 @@ __global__ __launch_bounds__(HPB * QSUB * 64, 8 / (HPB * QSUB)) void paged_atten
       }
       return;
     }
+    // the item's last tile: the same page-based addresses for the keys below
+    // kv_end; the rest re-read the last key's row (its page read once too)
+    const int kv_last = kv_end - 1;
+    const int wave_key0 = t * kBK + wave * KPW;
+    const int page_key0 = (min(wave_key0, kv_last) / kPage) * kPage;
+    int64_t row0, row_last;
+    if (CONTIG) {
+      row0 = (int64_t)kv0 + page_key0;
+      row_last = (int64_t)kv0 + kv_last;
+    } else {
+      row0 = (int64_t)__builtin_amdgcn_readfirstlane(pages_lds[page_key0 / kPage]) * kPage;
+      row_last = (int64_t)__builtin_amdgcn_readfirstlane(pages_lds[kv_last / kPage]) * kPage +
+                 kv_last % kPage;
+    }
+    const uint8_t* base = reinterpret_cast<const uint8_t*>(v ? vbase : kbase);
+    const uint8_t* src = base + row0 * kv_row * 2;
+    const uint8_t* src_last = base + row_last * kv_row * 2;
 #pragma unroll
     for (int j = 0; j < SLABS; ++j) {
       const int slab = wave * SLABS + j;
-      const int key = slab * KEYS_PER_SLAB + lane / KCH;
+      const int key = slab * KEYS_PER_SLAB + lane / KCH;  // within the tile
       const int p = lane % KCH;
-      int kidx = t * kBK + key;
-      kidx = kidx < kv_end ? kidx : kv_end - 1;
-      const int64_t prow = CONTIG ? (int64_t)kv0 + kidx
-                                  : (int64_t)pages_lds[kidx / kPage] * kPage + (kidx % kPage);
-      if (v) {
-        lds_dma16(vbase + prow * kv_row + (p ^ vswz<D>(key)) * 8, v_buf(buf) + slab * 1024);
-      } else {
-        lds_dma16(kbase + prow * kv_row + (p ^ kswz<D>(key)) * 8, k_buf(buf) + slab * 1024);
-      }
+      const uint32_t chunk = (uint32_t)((p ^ (v ? vswz<D>(key) : kswz<D>(key))) * 16);
+      const uint8_t* at = t * kBK + key < kv_end ? src + (v ? voff[j] : koff[j]) : src_last + chunk;
+      lds_dma16(at, (v ? v_buf(buf) : k_buf(buf)) + slab * 1024);
     }
   };
 
