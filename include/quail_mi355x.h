@@ -68,17 +68,21 @@ int qx_device_is_gfx950(void);
  *     products summed from zero by one 16x16x128 MFMA per 16x16 output
  *     tile, then total += (sA * sW) * partial in fp32; 256x256 tiles on a
  *     persistent grid, the next block's loads issued one per MFMA (N a
- *     multiple of 256; any number of 128-K blocks).
+ *     multiple of 256; any number of 128-K blocks);
+ * 31: config 30's arithmetic on 256x320 tiles (N a multiple of 320): each
+ *     wave's 160 weight rows lie in two 128-row scale blocks and each of
+ *     its 16-row tiles is promoted with its block's scale; bit-identical
+ *     to config 30 where N is a multiple of both.
  * Configs 10, 11, 12 and 22 rescale the accumulators in place
  * (acc *= s_prev / s per block, the last s in the epilogue) and compute
  * each element with the same operations in the same order: their results
  * are bit-identical for finite operands. A weight block whose scale is 0
  * is skipped by 10, 11 and 22 and run on zeroed weight rows by 12, so a
  * NaN activation code in such a block gives 0 under 10/11/22 and NaN under
- * 12; config 30 adds 0 * partial, NaN as well, as DeepGEMM's promotion
- * does. Config 30 sums in another order (within the bf16 tolerance of them
- * and of the dequantized product); a caller that needs a row's result
- * independent of M picks the family by N alone.
+ * 12; configs 30 and 31 add 0 * partial, NaN as well, as DeepGEMM's
+ * promotion does. Configs 30 and 31 sum in another order (within the bf16
+ * tolerance of the others and of the dequantized product); a caller that
+ * needs a row's result independent of M picks the family by N alone.
  */
 int qx_gemm_fp8_blockscaled(const void* A, const float* sA, const void* W, const float* sW,
                             void* C, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldc,

@@ -993,19 +993,28 @@ __device__ __forceinline__ v8i read_frag16(const uint8_t* lds, int row, int q) {
   return r;
 }
 
-template <bool SWIGLU>
+// BN = 320 (config 31, plain output only): each wave's 160 weight rows
+// straddle two 128-row scale blocks, the first `split` of its 16-row tiles
+// in the first (8, 6, 4 or 2, by the tile column's parity and the wave's
+// half); the block's second weight scale rides in the same direct load, and
+// a tile's promotion takes the scale of its block. The 656-byte staging rows
+// of a 320-column tile leave in four passes of one token tile per wave.
+template <bool SWIGLU, int BN>
 __global__ __launch_bounds__(512) void gemm_fp8_promo_kernel(
     const uint8_t* __restrict__ A, const float* __restrict__ sA, const uint8_t* __restrict__ W,
     const float* __restrict__ sW, uint16_t* __restrict__ C, int M, int N, int K, int64_t lda,
     int64_t ldc, int64_t sa_ld, int tiles_m, int tiles_n, int group_m, uint8_t* __restrict__ Q,
     int64_t q_ld, float* __restrict__ Qs, int64_t qs_ld) {
-  constexpr int BM = 256, BN = 256, WAVES_N = 2, WAVES_M = 4;
+  static_assert(BN == 256 || (BN == 320 && !SWIGLU), "256-wide tiles, or 320-wide plain");
+  constexpr int BM = 256, WAVES_N = 2, WAVES_M = 4;
   using Cfg = Cfg128<BM, BN, WAVES_N, WAVES_M, 2>;
-  constexpr int TN = BN / WAVES_N / 16;  // 8 weight tiles of 16 rows per wave
+  constexpr int TN = BN / WAVES_N / 16;  // 8 (10) weight tiles of 16 rows per wave
   constexpr int TM = BM / WAVES_M / 16;  // 4 token tiles of 16 per wave
   constexpr int kRowBytes = BN * 2 + 16;   // padded staging row (bank spread)
-  constexpr int kPassRows = WAVES_M * 32;  // two token tiles of every wave per pass
-  constexpr int kPasses = TM / 2;
+  constexpr int kTPP = BN == 256 ? 2 : 1;  // token tiles of every wave per epilogue pass
+  constexpr int kPassRows = WAVES_M * 16 * kTPP;
+  constexpr int kPasses = TM / kTPP;
+  constexpr int kWS = Cfg::kWSlabs;        // weight slabs per wave per block: 4 (5)
   constexpr int kRowsPerWave = kPassRows / Cfg::kWaves;
   static_assert(kPassRows * kRowBytes <= Cfg::kStage, "an epilogue pass fits one stage");
   static_assert(kPasses * kPassRows == BM, "passes cover the tile");
@@ -1044,17 +1053,19 @@ __global__ __launch_bounds__(512) void gemm_fp8_promo_kernel(
   // per-lane part of an address is a 32-bit offset over a wave-uniform base
   // (the launcher checks that a tile's rows span less than 4 GiB); token
   // rows past M clamp to M - 1.
-  static_assert(Cfg::kASlabs == 4 && Cfg::kWSlabs == 4, "slab walk");
-  static_assert(Cfg::kSaPerWave < 64, "a scale slot past the token scales");
+  static_assert(Cfg::kASlabs == 4 && (kWS == 4 || kWS == 5), "slab walk");
+  static_assert(Cfg::kSaPerWave + 2 <= 64, "scale slots past the token scales");
   const int row0 = wave * 32 + (lane >> 3);
   const uint32_t chunk = (uint32_t)(((lane & 7) ^ swz16(row0)) * 16);
-  const uint32_t w_lane = (uint32_t)row0 * (uint32_t)K + chunk;
+  // a wave's weight slabs are rows w_row0 + 8 jw (row % 8 = lane / 8 as for A)
+  const int w_row0 = wave * kWS * 8 + (lane >> 3);
+  const uint32_t w_lane = (uint32_t)w_row0 * (uint32_t)K + chunk;
   // the block to load: its tile, 128-K block and stage
   struct Blk {
     const uint8_t* a;  // the tile's first token row at the block's K
     const uint8_t* w;  // the tile's first weight row at the block's K
     const float* sa;   // the block's scale of the tile's first token
-    const float* sw;   // the wave's weight scale of the block
+    const float* sw;   // the wave's (first) weight scale of the block
     uint8_t* buf;
     int m_last;        // the tile's last token row (rows past it clamp)
   };
@@ -1070,11 +1081,12 @@ __global__ __launch_bounds__(512) void gemm_fp8_promo_kernel(
     b.sw = sW + (int64_t)((SWIGLU ? w_row0 + wn * (N >> 1) : n0_ + wn * (BN / WAVES_N)) >> 7) * KT + kb;
     return b;
   };
-  // load op j of a block: A slabs (j < 4), weight slabs (4 <= j < 8), then
-  // the token scales and the weight scale, in one direct load: lane i < 32
-  // of a wave brings token scale i of its 32 rows, the lanes past them the
-  // wave's weight scale (a scalar load here would stall every LDS wait of
-  // the block behind it: the scalar and LDS counters are one)
+  // load op j of a block: A slabs (j < 4), weight slabs (4 <= j < 4 + kWS),
+  // then the token scales and the weight scales, in one direct load: lane
+  // i < 32 of a wave brings token scale i of its 32 rows, the lanes past
+  // them the wave's weight scale (odd lanes, with 320-wide tiles, that of
+  // its second block; a scalar load here would stall every LDS wait of the
+  // block behind it: the scalar and LDS counters are one)
   constexpr int kLoadOps = Cfg::kASlabs + Cfg::kWSlabs + 1;
   const int sa_row = wave * Cfg::kSaPerWave + lane % Cfg::kSaPerWave;
   auto load_op = [&](const Blk& b, int j) {
@@ -1085,18 +1097,19 @@ __global__ __launch_bounds__(512) void gemm_fp8_promo_kernel(
       __builtin_amdgcn_global_load_lds((const void*)(b.a + off),
                                        (lds_void*)(b.buf + (wave * 4 + j) * 1024), 16, 0,
                                        kOperandLoadPolicy);
-    } else if (j < 8) {
+    } else if (j < 4 + kWS) {
       const int jw = j - 4;
       // uniform row shift of slab jw (SwiGLU: rows 128.. are up rows)
       const int shift = 8 * jw + (SWIGLU && wave * 4 + jw >= 16 ? (N >> 1) - 128 : 0);
       __builtin_amdgcn_global_load_lds(
           (const void*)(b.w + (int64_t)shift * K + w_lane),
-          (lds_void*)(b.buf + Cfg::kABytes + (wave * 4 + jw) * 1024), 16, 0,
+          (lds_void*)(b.buf + Cfg::kABytes + (wave * kWS + jw) * 1024), 16, 0,
           kOperandLoadPolicy);
     } else {
       const int t = min(sa_row, b.m_last);
-      // lanes past the wave's token scales carry its weight scale
-      const float* src = lane < Cfg::kSaPerWave ? b.sa + t : b.sw;
+      // lanes past the wave's token scales carry its weight scale(s)
+      const float* src = lane < Cfg::kSaPerWave ? b.sa + t
+                                                : (BN == 320 && (lane & 1) ? b.sw + KT : b.sw);
       __builtin_amdgcn_global_load_lds((const void*)src,
                                        (lds_void*)(b.buf + Cfg::kABytes + Cfg::kWBytes + wave * 256),
                                        4, 0, 0);
@@ -1123,6 +1136,8 @@ __global__ __launch_bounds__(512) void gemm_fp8_promo_kernel(
     int nm0 = m0, nn0 = n0;
     const bool has_next = it + 1 < my_tiles;
     if (has_next) origin(it + 1, nm0, nn0);
+    // the wave's weight tiles in its first scale block (all of them, 256 wide)
+    const int split = BN == 320 ? (128 - ((n0 + wn * (BN / WAVES_N)) & 127)) / 16 : TN;
 #pragma unroll
     for (int a = 0; a < TN; ++a)
 #pragma unroll
@@ -1150,6 +1165,7 @@ __global__ __launch_bounds__(512) void gemm_fp8_promo_kernel(
       // (reading the weight fragments two tiles ahead hides the LDS latency
       // that one ahead left exposed: 3-5% faster)
       const float sw = sa_lds[wave * 64 + Cfg::kSaPerWave];
+      const float sw1 = BN == 320 ? sa_lds[wave * 64 + Cfg::kSaPerWave + 1] : 0.0f;
       float sr[TM];
 #pragma unroll
       for (int b = 0; b < TM; ++b) {
@@ -1160,10 +1176,18 @@ __global__ __launch_bounds__(512) void gemm_fp8_promo_kernel(
       v8i af[TM];
 #pragma unroll
       for (int b = 0; b < TM; ++b) af[b] = read_frag16(a_lds, wm * TM * 16 + b * 16 + r16, q16);
-      v8i wf_next = read_frag16(w_lds, wn * TN * 16 + 16 + r16, q16);
-      float s[TM];
+      // weight fragments kAhead tiles ahead (one ahead in the 320-wide
+      // kernel, whose 160 totals leave no registers for a third fragment:
+      // measured 6-8% faster than two ahead there, or than a one-MFMA lag)
+      constexpr int kAhead = BN == 256 ? 2 : 1;
+      v8i wf_next;
+      if constexpr (kAhead == 2) wf_next = read_frag16(w_lds, wn * TN * 16 + 16 + r16, q16);
+      float s[TM], s1[TM];
 #pragma unroll
-      for (int b = 0; b < TM; ++b) s[b] = sr[b] * sw;
+      for (int b = 0; b < TM; ++b) {
+        s[b] = sr[b] * sw;
+        s1[b] = BN == 320 ? sr[b] * sw1 : 0.0f;
+      }
       // MFMA t (weight tile a = t / TM, token tile b = t % TM) writes
       // partial slot t % 3; each scheduling slot issues one MFMA and the
       // promotion of the partial two MFMAs older, so three partials are
@@ -1172,17 +1196,24 @@ __global__ __launch_bounds__(512) void gemm_fp8_promo_kernel(
       constexpr int kLag = 2;
       v4f part[kLag + 1];
       auto promote = [&](int t) {
+        // the scale of the tile's weight block (wave-uniform choice)
+        const float sc = BN == 320 && t / TM >= split ? s1[t % TM] : s[t % TM];
 #pragma unroll
         for (int e = 0; e < 4; ++e)
           tot[t / TM][t % TM][e] =
-              __builtin_fmaf(s[t % TM], part[t % (kLag + 1)][e], tot[t / TM][t % TM][e]);
+              __builtin_fmaf(sc, part[t % (kLag + 1)][e], tot[t / TM][t % TM][e]);
       };
       v8i wf_next2;
 #pragma unroll
       for (int t = 0; t < TN * TM; ++t) {
         const int a = t / TM, b = t % TM;
-        if (b == 0 && a + 2 < TN)
-          wf_next2 = read_frag16(w_lds, wn * TN * 16 + (a + 2) * 16 + r16, q16);
+        if constexpr (kAhead == 2) {
+          if (b == 0 && a + 2 < TN)
+            wf_next2 = read_frag16(w_lds, wn * TN * 16 + (a + 2) * 16 + r16, q16);
+        } else {
+          if (b == 0 && a + 1 < TN)
+            wf_next = read_frag16(w_lds, wn * TN * 16 + (a + 1) * 16 + r16, q16);
+        }
         part[t % (kLag + 1)] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
             wf, af[b], v4f{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0, 0, 0, 0);
         if (t >= kLag) promote(t - kLag);
@@ -1195,7 +1226,7 @@ __global__ __launch_bounds__(512) void gemm_fp8_promo_kernel(
         __builtin_amdgcn_sched_barrier(0);
         if (b == TM - 1 && a + 1 < TN) {
           wf = wf_next;
-          wf_next = wf_next2;
+          if constexpr (kAhead == 2) wf_next = wf_next2;
         }
       }
 #pragma unroll
@@ -1205,8 +1236,9 @@ __global__ __launch_bounds__(512) void gemm_fp8_promo_kernel(
 
     // epilogue through the stage of the tile's last block. Lane l holds
     // token b * 16 + l % 16 of the wave's 64 and weight rows
-    // a * 16 + 4 (l / 16) .. + 3 of its 128. Pass p stages token tiles 2p
-    // and 2p + 1 of every wave: staging row wm * 32 + (b - 2p) * 16 + l % 16.
+    // a * 16 + 4 (l / 16) .. + 3 of its 128 (160). Pass p stages token tiles
+    // kTPP p .. kTPP p + kTPP - 1 of every wave: staging row
+    // wm * 16 kTPP + (b - kTPP p) * 16 + l % 16.
     uint8_t* buf = smem + (stage ^ 1) * Cfg::kStage;
     const bool wide = ((ldc & 7) == 0) && ((reinterpret_cast<uintptr_t>(C) & 15) == 0);
 #pragma unroll
@@ -1215,9 +1247,9 @@ __global__ __launch_bounds__(512) void gemm_fp8_promo_kernel(
       // passes: with the previous pass's rows
       lgkm_barrier();
 #pragma unroll
-      for (int bb = 0; bb < 2; ++bb) {
-        const int b = pass * 2 + bb;
-        uint8_t* lrow = buf + (wm * 32 + bb * 16 + r16) * kRowBytes;
+      for (int bb = 0; bb < kTPP; ++bb) {
+        const int b = pass * kTPP + bb;
+        uint8_t* lrow = buf + (wm * 16 * kTPP + bb * 16 + r16) * kRowBytes;
 #pragma unroll
         for (int a = 0; a < TN; ++a) {
           const int off = (wn * TN * 16 + a * 16 + q16 * 4) * 2;
@@ -1235,7 +1267,7 @@ __global__ __launch_bounds__(512) void gemm_fp8_promo_kernel(
 #pragma unroll
         for (int i = 0; i < kRowsPerWave / 4; ++i) {
           const int prow = wave * kRowsPerWave + i * 4 + (lane >> 4);
-          const int m = m0 + (prow >> 5) * TM * 16 + pass * 32 + (prow & 31);
+          const int m = m0 + (prow >> 5) * TM * 16 + pass * 32 + (prow & 31);  // kTPP = 2
           const uint8_t* lrow = buf + prow * kRowBytes;
           const uint4 g = *reinterpret_cast<const uint4*>(lrow + seg * 16);
           const uint4 u = *reinterpret_cast<const uint4*>(lrow + 256 + seg * 16);
@@ -1263,13 +1295,16 @@ __global__ __launch_bounds__(512) void gemm_fp8_promo_kernel(
           }
         }
       } else {
+        // 16-byte chunks of the wave's staged rows, 64 per store instruction
         constexpr int kChunks = BN / 8;
-        constexpr int kRowsPerOp = 64 / kChunks;
-        const int c = lane % kChunks;
+        static_assert(kRowsPerWave * kChunks % 64 == 0, "whole store instructions");
+        constexpr int kRowsG = 16 * kTPP;  // staging rows per wave group
 #pragma unroll
-        for (int i = 0; i < kRowsPerWave / kRowsPerOp; ++i) {
-          const int prow = wave * kRowsPerWave + i * kRowsPerOp + lane / kChunks;
-          const int m = m0 + (prow >> 5) * TM * 16 + pass * 32 + (prow & 31);
+        for (int i = 0; i < kRowsPerWave * kChunks / 64; ++i) {
+          const int idx = i * 64 + lane;
+          const int prow = wave * kRowsPerWave + idx / kChunks;
+          const int c = idx % kChunks;
+          const int m = m0 + (prow / kRowsG) * TM * 16 + pass * kRowsG + prow % kRowsG;
           const uint4 v = *reinterpret_cast<const uint4*>(buf + prow * kRowBytes + c * 16);
           if (m < M) {
             uint16_t* dst = C + (int64_t)m * ldc + n0 + c * 8;
@@ -1324,17 +1359,18 @@ int launch128q(const void* A, const float* sA, const void* W, const float* sW, v
                      ldc, sa_ld, tiles_m, tiles_n, 4, (uint8_t*)Q, q_ld, Qs, qs_ld);
   QX_LAUNCH_STATUS();
 }
-// the promotion-form kernel (config 30; the SwiGLU epilogue with Q !=
-// nullptr): one workgroup per CU, at least one per XCD
-template <bool SWIGLU>
+// the promotion-form kernel (config 30, 256 x 256 tiles; the SwiGLU
+// epilogue with Q != nullptr; config 31, 256 x 320 tiles): one workgroup per
+// CU, at least one per XCD
+template <bool SWIGLU, int BN>
 int launch_promo(const void* A, const float* sA, const void* W, const float* sW, void* C, int M,
                  int N, int K, int64_t lda, int64_t ldc, int64_t sa_ld, void* Q, int64_t q_ld,
                  float* Qs, int64_t qs_ld, hipStream_t stream) {
   const int tiles_m = (M + 255) / 256;
-  const int tiles_n = N / 256;
+  const int tiles_n = N / BN;
   int grid = persistent_grid(tiles_m * tiles_n);
   if (grid < 8) grid = 8;
-  hipLaunchKernelGGL((gemm_fp8_promo_kernel<SWIGLU>), dim3(grid), dim3(512), 0, stream,
+  hipLaunchKernelGGL((gemm_fp8_promo_kernel<SWIGLU, BN>), dim3(grid), dim3(512), 0, stream,
                      (const uint8_t*)A, sA, (const uint8_t*)W, sW, (uint16_t*)C, M, N, K, lda,
                      ldc, sa_ld, tiles_m, tiles_n, 4, (uint8_t*)Q, q_ld, Qs, qs_ld);
   QX_LAUNCH_STATUS();
@@ -1344,14 +1380,16 @@ int launch_promo(const void* A, const float* sA, const void* W, const float* sW,
 
 extern "C" {
 
-// Tile configurations (tokens x weights); both give the same result, bit for
-// bit, since each output element sums the same products in the same order:
-// 10: 256 x 256 tiles, 8 waves, two 128-K stages, one workgroup per tile
-// (widths that are a multiple of 256); 11: 256 x 128 tiles, 4 waves (any
-// width that is a multiple of 128); 12: 256 x 320 tiles, 8 waves (widths
-// that are a multiple of 320: whole waves of tiles where N = 2560); 22: config 10's tiles on a persistent
-// grid with the K pipeline running across tiles (falls back to 10 when there
-// are too few tiles or an odd number of 128-K blocks).
+// Tile configurations (tokens x weights). The rescale family, bit-identical
+// to each other since each output element sums the same products in the
+// same order: 10: 256 x 256 tiles, 8 waves, two 128-K stages, one workgroup
+// per tile (widths that are a multiple of 256); 11: 256 x 128 tiles, 4
+// waves (any width that is a multiple of 128); 12: 256 x 320 tiles, 8 waves
+// (widths that are a multiple of 320); 22: config 10's tiles on a
+// persistent grid with the K pipeline running across tiles (falls back to
+// 10 when there are too few tiles or an odd number of 128-K blocks). The
+// promotion family, bit-identical to each other: 30 (256 x 256 tiles) and
+// 31 (256 x 320 tiles), both persistent.
 // gate_up projection + SiLU-gated product + per-128 FP8 quant in one launch:
 // W / sW are the gate_up weight (2I x K, rows [gate | up]) and its scales;
 // I = intermediate width.
@@ -1377,7 +1415,7 @@ int qx_gemm_fp8_swiglu_quant(const void* A, const float* sA, const void* W, cons
     QX_CHECK(256 * lda < (1LL << 32) && (I + 128) * K < (1LL << 32),
              "gemm_swiglu config 30: a tile's rows must span less than 4 GiB (lda=%lld, K=%lld)",
              (long long)lda, (long long)K);
-    return qx::launch_promo<true>(A, sA, W, sW, nullptr, (int)M, (int)(2 * I), (int)K, lda, 0,
+    return qx::launch_promo<true, 256>(A, sA, W, sW, nullptr, (int)M, (int)(2 * I), (int)K, lda, 0,
                                   sa_ld, Q, q_ld, Qs, qs_ld, stream);
   }
   if (config == 22)
@@ -1427,10 +1465,17 @@ int qx_gemm_fp8_blockscaled(const void* A, const float* sA, const void* W, const
       QX_CHECK(256 * lda < (1LL << 32) && 256LL * k < (1LL << 32),
                "gemm config 30: a tile's rows must span less than 4 GiB (lda=%lld, K=%d)",
                (long long)lda, k);
-      return qx::launch_promo<false>(A, sA, W, sW, C, m, n, k, lda, ldc, sa_ld, nullptr, 0,
-                                     nullptr, 0, stream);
+      return qx::launch_promo<false, 256>(A, sA, W, sW, C, m, n, k, lda, ldc, sa_ld, nullptr, 0,
+                                          nullptr, 0, stream);
+    case 31:
+      QX_CHECK(n % 320 == 0, "gemm config 31 needs N %% 320 == 0 (N=%d)", n);
+      QX_CHECK(256 * lda < (1LL << 32) && 320LL * k < (1LL << 32),
+               "gemm config 31: a tile's rows must span less than 4 GiB (lda=%lld, K=%d)",
+               (long long)lda, k);
+      return qx::launch_promo<false, 320>(A, sA, W, sW, C, m, n, k, lda, ldc, sa_ld, nullptr, 0,
+                                          nullptr, 0, stream);
     default:
-      QX_CHECK(false, "gemm: unknown config %d (10, 11, 12, 22 or 30)", config);
+      QX_CHECK(false, "gemm: unknown config %d (10, 11, 12, 22, 30 or 31)", config);
   }
 }
 

@@ -25,30 +25,29 @@ from quail_amd import _lib
 GROUP = 128
 
 # GEMM tile configurations (csrc/gemm_fp8.hip), in two arithmetic families.
-# Rescale family (10, 11, 12, 22): the MFMA accumulators are rescaled in
-# place by s_prev / s at each 128-K block; each config computes every
-# output element with the same operations in the same order, so the choice
-# among them never changes a bit. 10 = 256 tokens x 256 weights, 8 waves,
-# two 128-K stages, one workgroup per tile; 11 = 256 x 128 (widths not a
-# multiple of 256); 22 = config 10's tiles on a persistent grid; 12 = 256 x
-# 320 tiles (widths that are multiples of 320), whole waves where N = 2560
-# makes 2.5 or 1.25 waves of 256 x 256 tiles. Promotion family (30): each
-# block's products summed from zero by one 16x16x128 MFMA and promoted
-# into an fp32 total, total += (sA * sW) * partial (DeepGEMM's form),
-# persistent 256 x 256 tiles. The family is a function of N alone, so a
-# row's result never depends on how many rows share the launch (a document
-# packed with others equals itself run alone, bit for bit): N a multiple of
-# 320 takes the rescale family (config 12's whole waves there), any other
-# multiple of 256 the promotion kernel, the rest config 11.
-# QUAIL_GEMM_CONFIG forces one.
+# Promotion family (30, 31): each 128-K block's products summed from zero by
+# one 16x16x128 MFMA and promoted into an fp32 total, total += (sA * sW) *
+# partial (DeepGEMM's form), persistent grids; 30 = 256 tokens x 256
+# weights, 31 = 256 x 320 (widths that are multiples of 320: whole waves
+# where N = 2560 makes 2.5 or 1.25 waves of 256 x 256 tiles). Rescale family
+# (10, 11, 12, 22): the MFMA accumulators rescaled in place by s_prev / s at
+# each block; 10 = 256 x 256, one workgroup per tile; 11 = 256 x 128 (widths
+# not a multiple of 256); 22 = config 10's tiles on a persistent grid; 12 =
+# 256 x 320. Within a family every config computes each output element with
+# the same operations in the same order, so the choice among them never
+# changes a bit. The family is a function of N alone, so a row's result
+# never depends on how many rows share the launch (a document packed with
+# others equals itself run alone, bit for bit): N a multiple of 256 or 320
+# takes the promotion family, the rest config 11. QUAIL_GEMM_CONFIG forces
+# one.
 GEMM_CONFIG_ENV = "QUAIL_GEMM_CONFIG"
-GEMM_CONFIGS = (10, 11, 12, 22, 30)
+GEMM_CONFIGS = (10, 11, 12, 22, 30, 31)
 RESCALE_CONFIGS = (10, 11, 12, 22)
-GEMM_DEFAULT_CONFIG = 10
+PROMOTION_CONFIGS = (30, 31)
 GEMM_PROMOTION_CONFIG = 30
+GEMM_PROMOTION_WIDE_CONFIG = 31
 SWIGLU_DEFAULT_CONFIG = 30
 GEMM_ODD_WIDTH_CONFIG = 11
-GEMM_WHOLE_WAVES_CONFIG = 22
 CUS = 256
 
 
@@ -60,21 +59,17 @@ def _stream():
     return torch.cuda.current_stream().cuda_stream
 
 
-GEMM_WIDE_TILE_CONFIG = 12
-
-
 def gemm_config(n: int, k: int, m: int) -> int:
+    """The tile configuration of an (m x k) by (n x k) GEMM: the promotion
+    family for widths that are a multiple of 256 or 320 (256 x 320 tiles
+    where they take fewer full-wave units, or where 256 x 256 ones cannot
+    tile N), config 11 for the rest."""
     forced = os.environ.get(GEMM_CONFIG_ENV)
     if forced is not None:
         return int(forced)
-    if n % 320 == 0:
-        # rescale family: 256 x 320 tiles where they take fewer full waves
-        if _wide_tiles_fill_better(n, m):
-            return GEMM_WIDE_TILE_CONFIG
-        if n % 256:
-            return GEMM_ODD_WIDTH_CONFIG
-        return GEMM_WHOLE_WAVES_CONFIG if _whole_waves(n, k, m) else GEMM_DEFAULT_CONFIG
-    if n % 256 == 0:
+    if n % 256 == 0 or n % 320 == 0:
+        if n % 320 == 0 and (n % 256 or _wide_tiles_fill_better(n, m)):
+            return GEMM_PROMOTION_WIDE_CONFIG
         return GEMM_PROMOTION_CONFIG
     return GEMM_ODD_WIDTH_CONFIG
 
@@ -95,14 +90,6 @@ def _wide_tiles_fill_better(n: int, m: int) -> bool:
     tm = -(-m // 256)
     return 1.25 * _wave_cost(tm * (n // 320)) < (_wave_cost(tm * (n // 256)) if n % 256 == 0
                                                  else float("inf"))
-
-
-def _whole_waves(n: int, k: int, m: int) -> bool:
-    """256 x 256 tiles fill whole waves of the CUs (the last at least 7/8
-    full) and K has an even number of 128-blocks (config 22's pipeline)."""
-    tiles = -(-m // 256) * (n // 256)
-    return (tiles >= CUS and tiles % CUS in (0,) + tuple(range(CUS - CUS // 8, CUS))
-            and (k // 128) % 2 == 0)
 
 
 SWIGLU_CONFIG_ENV = "QUAIL_SWIGLU_CONFIG"

@@ -102,9 +102,10 @@ def test_gemm_small_shapes_match_dequantized_matmul(m, n, k):
 GEMM_CONFIGS = (10, 11, 12, 22)
 GEMM_CONFIGS_256 = (10, 11, 22)   # N a multiple of 256 (config 12 needs 320)
 PROMOTION_CONFIG = 30             # DeepGEMM's promotion form: its own arithmetic
+PROMOTION_WIDE_CONFIG = 31        # the same arithmetic on 256 x 320 tiles
 
 
-@pytest.mark.parametrize("config", GEMM_CONFIGS + (PROMOTION_CONFIG,))
+@pytest.mark.parametrize("config", GEMM_CONFIGS + (PROMOTION_CONFIG, PROMOTION_WIDE_CONFIG))
 def test_gemm_tile_configs_agree(config, monkeypatch):
     q, s, wq, ws = _gemm_case(300, 1280, 512, seed=9)
     monkeypatch.setenv("QUAIL_GEMM_CONFIG", str(config))
@@ -158,6 +159,38 @@ def test_gemm_promotion_kernel_edges(m, n, k, monkeypatch):
     _bf16_close(out, ref.gemm(q, s, ref.RefLinear(wq, ws)))
 
 
+@pytest.mark.parametrize("m,n,k", [(1, 1280, 128), (257, 1280, 384), (4000, 2560, 768),
+                                   (16294, 2560, 4096), (8192, 2560, 9728), (3000, 5120, 1152),
+                                   (600, 10240, 640)])
+def test_gemm_wide_promotion_tiles_equal_config_30(m, n, k, monkeypatch):
+    """Config 31 (256 x 320 tiles; each wave's 160 weight rows in two
+    128-row scale blocks, its tiles promoted with their block's scale) is
+    config 30's arithmetic: bit-identical on widths that are multiples of
+    both 256 and 320 (one row, a partial token tile, odd numbers of 128-K
+    blocks, the Qwen3-4B o_proj and down shapes of a pack and of the GEMM-
+    alone record, several tiles per workgroup), and the oracle's result to
+    the bf16 tolerance."""
+    q, s, wq, ws = _gemm_case(m, n, k, seed=m + n + k)
+    outs = {}
+    for config in (PROMOTION_CONFIG, PROMOTION_WIDE_CONFIG):
+        monkeypatch.setenv("QUAIL_GEMM_CONFIG", str(config))
+        outs[config] = _run_gemm(q, s, wq, ws)
+    assert torch.equal(outs[PROMOTION_CONFIG], outs[PROMOTION_WIDE_CONFIG])
+    if m <= 4000:
+        _bf16_close(outs[PROMOTION_WIDE_CONFIG], ref.gemm(q, s, ref.RefLinear(wq, ws)))
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 640, 256), (300, 640, 512), (700, 1920, 1152)])
+def test_gemm_wide_promotion_tiles_at_widths_only_320_divides(m, n, k, monkeypatch):
+    """Widths that are multiples of 320 but not of 256 take config 31 (the
+    engine's choice) and agree with the oracle to the bf16 tolerance."""
+    from quail_amd.engine import gemm_config
+    monkeypatch.delenv("QUAIL_GEMM_CONFIG", raising=False)
+    assert gemm_config(n, k, m) == PROMOTION_WIDE_CONFIG
+    q, s, wq, ws = _gemm_case(m, n, k, seed=m + n + k)
+    _bf16_close(_run_gemm(q, s, wq, ws), ref.gemm(q, s, ref.RefLinear(wq, ws)))
+
+
 def test_gemm_configs_agree_with_zero_weight_blocks(monkeypatch):
     """Weight blocks whose scale is 0 add nothing; configurations skip them
     or run them on zero fragments, and all must agree bit for bit: zero
@@ -179,11 +212,14 @@ def test_gemm_configs_agree_with_zero_weight_blocks(monkeypatch):
     want = ref.gemm(q, s, ref.RefLinear(wq, ws))
     _bf16_close(outs[10], want)
     assert torch.all(outs[10][:, 5 * 128:6 * 128] == 0)
-    # the promotion form adds 0 * partial for such blocks (finite operands)
+    # the promotion form adds 0 * partial for such blocks (finite operands);
+    # its 256 x 320 tiles give the same bits
     monkeypatch.setenv("QUAIL_GEMM_CONFIG", str(PROMOTION_CONFIG))
     out = _run_gemm(q, s, wq, ws).cpu()
     _bf16_close(out, want)
     assert torch.all(out[:, 5 * 128:6 * 128] == 0)
+    monkeypatch.setenv("QUAIL_GEMM_CONFIG", str(PROMOTION_WIDE_CONFIG))
+    assert torch.equal(_run_gemm(q, s, wq, ws).cpu(), out)
 
 
 @pytest.mark.parametrize("m,i,k,zero_blocks", [(700, 768, 512, False), (333, 1536, 256, True),
@@ -245,7 +281,8 @@ def test_gemm_wide_tiles_at_pack_shapes(m, n, k, monkeypatch):
     128-row scale blocks) at a 16k-row pack's o_proj and down shapes, the
     GEMM-alone o_proj shape, a ragged M, one partial token tile and an odd
     number of 128-K blocks: bit-identical to config 10 (config 11 where N is
-    not a multiple of 256), and the engine takes it at the first three."""
+    not a multiple of 256). (The engine takes config 31, the promotion
+    form's 256 x 320 tiles, at the first three.)"""
     from quail_amd.engine import gemm_config
     q, s, wq, ws = _gemm_case(m, n, k, seed=m + n + k)
     base = 10 if n % 256 == 0 else 11
@@ -256,7 +293,7 @@ def test_gemm_wide_tiles_at_pack_shapes(m, n, k, monkeypatch):
     assert torch.equal(outs[base], outs[12])
     monkeypatch.delenv("QUAIL_GEMM_CONFIG")
     if m >= 8192:
-        assert gemm_config(n, k, m) == 12
+        assert gemm_config(n, k, m) == PROMOTION_WIDE_CONFIG
 
 
 @pytest.mark.parametrize("config", [None, PROMOTION_CONFIG, 10])

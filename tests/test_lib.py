@@ -95,26 +95,25 @@ def test_attention_tile_rows_choice_and_32_row_work_list():
 
 def test_gemm_config_choice_by_shape(monkeypatch):
     """The arithmetic family is a function of N alone: widths that are a
-    multiple of 320 take the rescale family (config 12's 256 x 320 tiles
-    where those take fewer full-wave units than 256 x 256 ones, else the
-    persistent config 22 where 256 x 256 tiles fill whole waves and K has an
-    even number of 128-blocks, else config 10), other multiples of 256 the
-    promotion kernel (30) at every M, the rest config 11; the environment
-    variable forces one."""
+    multiple of 256 or 320 take the promotion family (config 31's 256 x 320
+    tiles where those take fewer full-wave units than 256 x 256 ones, or
+    where N is not a multiple of 256; config 30 otherwise), the rest config
+    11; the environment variable forces one."""
     from quail_amd.engine import GEMM_CONFIG_ENV, gemm_config
     monkeypatch.delenv(GEMM_CONFIG_ENV, raising=False)
     assert gemm_config(6144, 2560, 16294) == 30     # qkv of a Qwen3-4B pack
     assert gemm_config(6144, 2688, 16294) == 30     # 21 K-blocks
     assert gemm_config(6144, 2560, 256) == 30       # fewer tiles than CUs
     assert gemm_config(4096, 4096, 37) == 30        # Qwen3-8B o_proj, a few final rows
-    assert gemm_config(2560, 4096, 16294) == 12     # 512 tiles of 256 x 320, not 640
-    assert gemm_config(2560, 9728, 8192) == 12      # 256 tiles, not 320
-    assert gemm_config(2560, 4096, 13056) == 22     # 510 tiles of 256 x 256: 2 waves
-    assert gemm_config(2560, 4096, 2048) == 10      # 80 tiles: 64 wide ones cost more
-    assert gemm_config(2560, 2688, 12000) == 10     # 21 K-blocks
-    assert gemm_config(10240, 5120, 16294) == 22    # Qwen3-32B qkv: rescale family, 10 waves
+    assert gemm_config(2560, 4096, 16294) == 31     # 512 tiles of 256 x 320, not 640
+    assert gemm_config(2560, 9728, 8192) == 31      # 256 tiles, not 320
+    assert gemm_config(2560, 4096, 13056) == 30     # 510 tiles of 256 x 256: 2 waves
+    assert gemm_config(2560, 4096, 2048) == 30      # 80 tiles: 64 wide ones cost more
+    assert gemm_config(2560, 2688, 12000) == 30     # 470 tiles against 376 wide ones
+    assert gemm_config(10240, 5120, 16294) == 30    # Qwen3-32B qkv: 10 waves either way
+    assert gemm_config(5120, 8192, 16294) == 30     # Qwen3-32B o_proj: 5 waves either way
     assert gemm_config(2688, 2560, 16294) == 11
-    assert gemm_config(640, 256, 100) == 12         # 320 tiles take fewer waves (odd width)
+    assert gemm_config(640, 256, 100) == 31         # a multiple of 320 but not of 256
     monkeypatch.setenv(GEMM_CONFIG_ENV, "11")
     assert gemm_config(6144, 2560, 16294) == 11
 
