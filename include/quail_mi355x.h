@@ -256,7 +256,8 @@ int qx_embed(const void* table, int64_t t_ld, const int64_t* ids, void* out, int
 
 /*
  * The most keys (used[s]) one sequence of a paged attention call may have:
- * 2048 pages of `page` tokens (32,768 at the arena's 16), the page-table
+ * 2560 pages of `page` tokens (40,960 at the arena's 16: Qwen3's whole
+ * context), the page-table
  * row each workgroup stages in LDS. Host only; -1 (message in
  * qx_last_error()) for a page size the kernels do not take. No counterpart
  * in the reference (its paged kernel takes any block-table width); callers

@@ -49,7 +49,9 @@ typedef __attribute__((address_space(3))) void lds_void;
 
 constexpr int kBK = 64;          // keys per KV tile
 constexpr int kPage = 16;        // tokens per arena page
-constexpr int kMaxPages = 2048;  // page-table entries staged in LDS per sequence
+// page-table entries staged in LDS per sequence: 40,960 keys at 16-row
+// pages, Qwen3's whole context (two workgroups' 74.5 KiB still fit a CU)
+constexpr int kMaxPages = 2560;
 // a row's reference max moves when a tile raises its max by more than this
 // many powers of two (probabilities then stay below 2^8)
 constexpr float kLazyLog2 = 8.0f;

@@ -622,15 +622,18 @@ def test_paged_attention_matches_exact_fp32(hq, hk, d, v_dtype):
 
 
 @pytest.mark.parametrize("v_dtype", V_DTYPES)
-def test_paged_attention_long_sequences_match_exact_fp32(v_dtype):
-    """Sequences past 4096 keys (more than 64 key tiles: the kernel re-reads
-    its page ids every 64 tiles), with ragged last pages and query tiles, in
-    a shuffled pool: against exact fp32 attention."""
+@pytest.mark.parametrize("q_lens,used", [((33, 64, 100, 7), (4200, 4500, 5003, 8190)),
+                                         ((16, 40), (32768 + 113, 40960))])
+def test_paged_attention_long_sequences_match_exact_fp32(v_dtype, q_lens, used):
+    """Sequences past 4096 keys (more than 64 key tiles), up to Qwen3's whole
+    40,960-token context (2560 pages, the most the kernel stages), with
+    ragged last pages and query tiles, in a shuffled pool: against exact
+    fp32 attention."""
     hq, hk, d, page = 32, 8, 128, 16
     rng = np.random.default_rng(41)
     g = _gen(41)
-    q_lens = np.array([33, 64, 100, 7], dtype=np.int64)
-    used = np.array([4200, 4500, 5003, 8190], dtype=np.int64)
+    q_lens = np.array(q_lens, dtype=np.int64)
+    used = np.array(used, dtype=np.int64)
     cu = np.concatenate([[0], np.cumsum(q_lens)]).astype(np.int32)
     need = -(-used // page)
     pool_pages = int(need.sum()) + 5

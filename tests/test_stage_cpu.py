@@ -241,16 +241,16 @@ def test_oversized_documents_are_refused_up_front():
 
 
 def test_documents_past_the_attention_key_limit_are_refused_up_front():
-    """The paged attention stages at most 2048 page ids (32,768 keys at
-    16-token pages) per sequence: a longer document passes the arena and
-    chunked-prefill checks but is refused at admission; one at the limit
-    is admitted."""
+    """The paged attention stages at most 2560 page ids (40,960 keys at
+    16-token pages, Qwen3's whole context) per sequence: a longer document
+    passes the arena and chunked-prefill checks but is refused at
+    admission; one at the limit is admitted."""
     limit = _lib.count("qx_paged_attention_max_keys", PAGE)
-    assert limit == 2048 * PAGE
+    assert limit == 2560 * PAGE == 40960
     arena = KVArena(1, 4096, PAGE, CFG.kv_heads, CFG.head_dim, device="cpu")
     rng = np.random.default_rng(0)
     long_doc = rng.integers(0, CFG.vocab, limit + 1)
-    with pytest.raises(OversizedDocumentError, match="32768 per sequence"):
+    with pytest.raises(OversizedDocumentError, match="40960 per sequence"):
         StageAdmission([long_doc[:-1]], [[long_doc[-1:]]], arena, 16384)
     ok = long_doc[:limit]
     StageAdmission([ok[:-1]], [[ok[-1:]]], arena, 16384)
