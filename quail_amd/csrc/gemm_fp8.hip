@@ -21,9 +21,10 @@
 //         current block's scale; entering block kb it is multiplied by
 //         s_(kb-1) / s_kb and the MFMAs accumulate the raw products into it;
 //         the epilogue multiplies by the last block's scale. No temporaries;
-//       - promotion (config 30; v_mfma_scale_f32_16x16x128_f8f6f4 with unit
-//         scales): each block's products are summed from zero by one MFMA
-//         per 16 x 16 tile and promoted into an fp32 total on the VALU,
+//       - promotion (configs 30 and 31, 256 x 256 and 256 x 320 tiles;
+//         v_mfma_scale_f32_16x16x128_f8f6f4 with unit scales): each
+//         block's products are summed from zero by one MFMA per 16 x 16
+//         tile and promoted into an fp32 total on the VALU,
 //         total += s_kb * P_kb;
 //   * operand tiles go HBM -> LDS with global_load_lds_dwordx4 (no VGPR
 //     staging), one 128-K scale block per pipeline stage (two stages), so
@@ -1299,9 +1300,14 @@ __global__ __launch_bounds__(512) void gemm_fp8_promo_kernel(
         constexpr int kChunks = BN / 8;
         static_assert(kRowsPerWave * kChunks % 64 == 0, "whole store instructions");
         constexpr int kRowsG = 16 * kTPP;  // staging rows per wave group
+        // 320 wide: the lane's rows and chunks are formed here for each
+        // tile; kept from the kernel's start they outlived the block loop in
+        // spilled registers (100 B per lane, 13 MB of scratch writes per
+        // launch), 1-4% slower. The 256-wide kernels have the registers.
+        const int el = BN == 320 ? opaque(lane) : lane;
 #pragma unroll
         for (int i = 0; i < kRowsPerWave * kChunks / 64; ++i) {
-          const int idx = i * 64 + lane;
+          const int idx = i * 64 + el;
           const int prow = wave * kRowsPerWave + idx / kChunks;
           const int c = idx % kChunks;
           const int m = m0 + (prow / kRowsG) * TM * 16 + pass * kRowsG + prow % kRowsG;

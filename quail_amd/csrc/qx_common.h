@@ -137,6 +137,15 @@ __device__ __forceinline__ float sum_halves(float x) {
 // accesses across it.
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_barrier" ::: "memory"); }
 
+// v as an opaque value where this call stands: the compiler cannot move
+// what is computed from it out of an enclosing loop, so per-lane addresses
+// that a loop's tail uses are recomputed there instead of being kept live
+// (or spilled) across the loop's body.
+__device__ __forceinline__ int opaque(int v) {
+  asm volatile("" : "+v"(v));
+  return v;
+}
+
 // s_waitcnt with vmcnt <= n and the other counters unconstrained (gfx9
 // encoding: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt_hi[15:14]).
 template <int n>
