@@ -19,6 +19,19 @@ import torch
 from quail_amd.pages import PageArena
 
 
+class _Claim:
+    """What keeps a key's pages in the arena: queued borrowers that will
+    read them (holds), admissions reading them now (reads), and whether a
+    free was asked for meanwhile (done when the last claim goes)."""
+
+    __slots__ = ("holds", "reads", "free_asked")
+
+    def __init__(self):
+        self.holds = 0
+        self.reads = 0
+        self.free_asked = False
+
+
 class KVArena:
     def __init__(self, num_layers: int, num_pages: int, page_tokens: int, num_kv_heads: int,
                  d_head: int, dtype=torch.bfloat16, device="cuda", v_dtype=torch.float16):
@@ -51,9 +64,7 @@ class KVArena:
         # when written, and the PV product then keeps 11 bits of each
         # probability instead of 8)
         self.v = [p.view(self.v_dtype).view(rows, heads, dim) for p in parts[1::2]]
-        self._holds = {}
-        self._reading = {}
-        self._deferred = set()
+        self._claims = {}
 
     # ---- sizes -------------------------------------------------------------
 
@@ -125,7 +136,7 @@ class KVArena:
         read (held) or that an admission is reading is never a victim.
         Returns the evicted keys."""
         acct = self.accounting
-        keep = frozenset(self._holds) | frozenset(self._reading)
+        keep = frozenset(self._claims)
         keys = []
         while not satisfied():
             victim = acct.pop_retained_victim(keep=keep)
@@ -199,8 +210,9 @@ class KVArena:
         """Free a key's pages, or once its holds and reads are over (a key
         queued borrowers will read, or that an admission reads, waits for
         them). Returns the pages that went free now."""
-        if key in self._holds or key in self._reading:
-            self._deferred.add(key)
+        claim = self._claims.get(key)
+        if claim is not None:
+            claim.free_asked = True
             return 0
         return self.accounting.free_key(key)
 
@@ -216,50 +228,53 @@ class KVArena:
 
     # ---- holds and reads: keys that admitted or queued readers need -------------
 
+    def _claim(self, key) -> "_Claim":
+        claim = self._claims.get(key)
+        if claim is None:
+            claim = self._claims[key] = _Claim()
+        return claim
+
+    def _settle(self, key) -> None:
+        """Forget a key's claim once nothing keeps it; free its pages then
+        if a free was asked for while it was kept."""
+        claim = self._claims[key]
+        if claim.holds or claim.reads:
+            return
+        del self._claims[key]
+        if claim.free_asked:
+            self.accounting.free_key(key)
+
     def hold(self, key, borrowers: int) -> None:
         """Keep a key for `borrowers` documents that will read its pages."""
         if borrowers:
-            self._holds[key] = self._holds.get(key, 0) + borrowers
+            self._claim(key).holds += borrowers
 
     def release(self, key) -> None:
         """One borrower of the key was admitted, or will not come."""
-        count = self._holds.get(key)
-        if count is None:
-            return
-        if count > 1:
-            self._holds[key] = count - 1
-        else:
-            self._drop_hold(key)
-
-    def _drop_hold(self, key) -> None:
-        del self._holds[key]
-        if key in self._deferred and key not in self._reading:
-            self._deferred.discard(key)
-            self.free_key(key)
+        claim = self._claims.get(key)
+        if claim is not None and claim.holds:
+            claim.holds -= 1
+            self._settle(key)
 
     def drop_holds(self, keys=None) -> bool:
         """Release every hold on the keys (all by default): freed keys go
         free, retained ones become evictable. True when any hold went."""
-        keys = list(self._holds) if keys is None else [k for k in keys if k in self._holds]
-        for key in keys:
-            self._drop_hold(key)
-        return bool(keys)
+        pool = self._claims if keys is None else keys
+        held = [k for k in pool if k in self._claims and self._claims[k].holds]
+        for key in held:
+            self._claims[key].holds = 0
+            self._settle(key)
+        return bool(held)
 
     def read_state(self, keys) -> None:
         """Keep each key's pages until done_reading for the same keys."""
         for key in keys:
-            self._reading[key] = self._reading.get(key, 0) + 1
+            self._claim(key).reads += 1
 
     def done_reading(self, keys) -> None:
         for key in keys:
-            left = self._reading[key] - 1
-            if left:
-                self._reading[key] = left
-                continue
-            del self._reading[key]
-            if key in self._deferred and key not in self._holds:
-                self._deferred.discard(key)
-                self.free_key(key)
+            self._claims[key].reads -= 1
+            self._settle(key)
 
     def origin(self, tokens: int) -> int:
         """The first row a key's pages must hold for a borrower of `tokens`

@@ -64,31 +64,51 @@ class AnswerRows:
         return bits.int().cpu().tolist()
 
 
+class _Pending:
+    """A submitted copy: the event after it, its pinned buffer, the rows."""
+
+    __slots__ = ("done", "buf", "rows", "kind")
+
+    def __init__(self, done, buf, rows, kind):
+        self.done, self.buf, self.rows, self.kind = done, buf, rows, kind
+
+
 class _HostReadout:
+    """Device rows to pinned host buffers without stalling the stream: the
+    copy and an event go on the current stream and result() waits on that
+    event alone. Idle buffers are pooled per (dtype, row shape) and sized in
+    powers of two rows, so a stage allocates pinned memory a few times at
+    most."""
+
     trailing_rows = 1
     normalize = False
 
     def __init__(self):
-        self.available = []
+        self._idle = {}
 
     def _copy(self, values):
-        host = self.available.pop() if self.available else None
-        if host is None or host.shape[0] < values.shape[0] or host.dtype != values.dtype \
-                or host.shape[1:] != values.shape[1:]:
-            host = torch.empty((max(values.shape[0], 64),) + tuple(values.shape[1:]),
-                               dtype=values.dtype, pin_memory=True)
-        host[:values.shape[0]].copy_(values, non_blocking=True)
-        event = torch.cuda.Event()
-        event.record()
-        return event, host, values.shape[0]
+        kind = (values.dtype, tuple(values.shape[1:]))
+        rows = values.shape[0]
+        idle = self._idle.setdefault(kind, [])
+        fits = [i for i, b in enumerate(idle) if b.shape[0] >= rows]
+        if fits:
+            buf = idle.pop(fits[0])
+        else:
+            cap = max(64, 1 << max(rows - 1, 0).bit_length())
+            buf = torch.empty((cap,) + kind[1], dtype=kind[0], pin_memory=True)
+        buf[:rows].copy_(values, non_blocking=True)
+        done = torch.cuda.Event()
+        done.record()
+        return _Pending(done, buf, rows, kind)
 
     def result(self, handle, *, copy=True):
-        event, host, count = handle
-        event.synchronize()
-        values = host[:count].numpy()
+        """The handle's rows as numpy; without copy, a view of the pinned
+        buffer that the next submit may overwrite."""
+        handle.done.synchronize()
+        values = handle.buf[:handle.rows].numpy()
         if copy:
             values = values.copy()
-        self.available.append(host)
+        self._idle[handle.kind].append(handle.buf)
         return values
 
 
