@@ -45,19 +45,13 @@ __device__ __forceinline__ float round_bf16(float f) {
   return bf16_to_f32(f32_to_bf16(f));
 }
 
-// x clamped to +-448; NaN stays NaN, as torch.clamp keeps it (fminf and
-// fmaxf alone would turn it into -448)
-__device__ __forceinline__ float clamp_fp8_range(float x) {
-  return x != x ? x : fminf(fmaxf(x, -kFp8Max), kFp8Max);
-}
-
-// Four fp32 values -> four packed e4m3fn bytes (little-endian order), with
-// the clamp to +-448 applied first.
+// Four fp32 values -> four packed e4m3fn bytes (little-endian order).
+// Every caller passes values divided by their group's scale, amax / 448
+// (div_by with fp8_scale), so |x| <= 448 up to an ulp of the quotient,
+// which the conversion rounds to +-448: the reference's clamp to +-448
+// (attention.py:786-787) changes nothing there and is not repeated. NaN
+// converts to the NaN code, as the clamp would have kept it.
 __device__ __forceinline__ uint32_t pack4_fp8(float a, float b, float c, float d) {
-  a = clamp_fp8_range(a);
-  b = clamp_fp8_range(b);
-  c = clamp_fp8_range(c);
-  d = clamp_fp8_range(d);
   int v = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
   v = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, v, true);
   return static_cast<uint32_t>(v);
@@ -98,12 +92,33 @@ __device__ __forceinline__ uint4 bf16x8_to_f16(uint4 w) {
   return w;
 }
 
-// Butterfly reductions across `width` consecutive lanes of a wave64.
+// v of another lane of the same 16-lane DPP row: CTRL is a DPP control
+// (quad_perm 0x00-0xff, row_mirror 0x140, row_half_mirror 0x141); a VALU
+// operand modifier, no LDS permute.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+
+// Butterfly reductions across `width` consecutive lanes of a wave64. The
+// max over an aligned group of 16 (one DPP row) takes four DPP moves:
+// lane ^ 1 and lane ^ 2 (quad_perm [1,0,3,2], [2,3,0,1]) leave each quad's
+// max on its lanes, the mirror within the half row pairs each quad with
+// the other one, the mirror within the row each half with the other. Max
+// is order-free (fmaxf drops a NaN operand either way), so the result is
+// the permute butterfly's.
 template <int width>
 __device__ __forceinline__ float group_max(float v) {
+  if constexpr (width == 16) {
+    v = fmaxf(v, dpp_f32<0xb1>(v));
+    v = fmaxf(v, dpp_f32<0x4e>(v));
+    v = fmaxf(v, dpp_f32<0x141>(v));
+    return fmaxf(v, dpp_f32<0x140>(v));
+  } else {
 #pragma unroll
-  for (int o = width / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-  return v;
+    for (int o = width / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+  }
 }
 
 template <int width>
