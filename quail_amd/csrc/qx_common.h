@@ -40,9 +40,11 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
 }
 
 // Round an fp32 value through bf16 and back (the reference stores bf16
-// intermediates between kernels).
+// intermediates between kernels): gfx950's conversion (v_cvt_pk_bf16_f32,
+// round to nearest even, the same bits as f32_to_bf16 for every non-NaN
+// value; a NaN stays a NaN), two instructions where f32_to_bf16 takes five.
 __device__ __forceinline__ float round_bf16(float f) {
-  return bf16_to_f32(f32_to_bf16(f));
+  return bf16_to_f32(__builtin_bit_cast(uint16_t, static_cast<__bf16>(f)));
 }
 
 // Four fp32 values -> four packed e4m3fn bytes (little-endian order).
