@@ -1116,17 +1116,17 @@ __global__ __launch_bounds__(512) void gemm_fp8_promo_kernel(
                                        4, 0, 0);
     }
   };
-  auto issue = [&](int m0_, int n0_, int kb, int stage) {
-    const Blk b = block_of(m0_, n0_, kb, stage);
-#pragma unroll
-    for (int j = 0; j < kLoadOps; ++j) load_op(b, j);
-  };
-
   v4f tot[TN][TM];
   int m0 = 0, n0 = 0;
+  // the block most recently issued: within a tile the next one is its K
+  // neighbour (every address one block further on, the other stage), so
+  // block_of's full address arithmetic runs once per tile
+  Blk issued{};
   if (my_tiles > 0) {
     origin(0, m0, n0);
-    issue(m0, n0, 0, 0);
+    issued = block_of(m0, n0, 0, 0);
+#pragma unroll
+    for (int j = 0; j < kLoadOps; ++j) load_op(issued, j);
   }
   // Blocks alternate between the two stages across tiles: the block after
   // a tile's last (the next tile's first) is loaded into the other stage
@@ -1150,13 +1150,17 @@ __global__ __launch_bounds__(512) void gemm_fp8_promo_kernel(
       // first; after the workgroup's last block, the current block again
       // (into the free stage: loads with no branch around them, drained
       // before the end)
-      Blk nb;
-      {
-        const bool same = kb + 1 < KT;
-        const bool next_tile = !same && has_next;
-        nb = block_of(next_tile ? nm0 : m0, next_tile ? nn0 : n0,
-                      same ? kb + 1 : (next_tile ? 0 : kb), stage ^ 1);
+      Blk nb = issued;
+      if (kb + 1 < KT) {
+        nb.a += 128;
+        nb.w += 128;
+        nb.sa += sa_ld;
+        nb.sw += 1;
+        nb.buf = smem + (stage ^ 1) * Cfg::kStage;
+      } else {
+        nb = has_next ? block_of(nm0, nn0, 0, stage ^ 1) : block_of(m0, n0, kb, stage ^ 1);
       }
+      issued = nb;
       const uint8_t* a_lds = smem + stage * Cfg::kStage;
       const uint8_t* w_lds = a_lds + Cfg::kABytes;
       const float* sa_lds = reinterpret_cast<const float*>(w_lds + Cfg::kWBytes);
