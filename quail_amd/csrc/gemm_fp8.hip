@@ -213,10 +213,10 @@ __device__ __forceinline__ void tile_epilogue(uint8_t* smem, const v16f (&acc)[T
       const float scale = fp8_scale(amax);
       const float rs = recip(scale);
       if (m < M) {
-        const v2i o = {(int)pack4_fp8(div_by(y[0], scale, rs), div_by(y[1], scale, rs),
-                                      div_by(y[2], scale, rs), div_by(y[3], scale, rs)),
-                       (int)pack4_fp8(div_by(y[4], scale, rs), div_by(y[5], scale, rs),
-                                      div_by(y[6], scale, rs), div_by(y[7], scale, rs))};
+        const v2i o = {(int)pack4_fp8(silu_quot(y[0], rs), silu_quot(y[1], rs),
+                                      silu_quot(y[2], rs), silu_quot(y[3], rs)),
+                       (int)pack4_fp8(silu_quot(y[4], rs), silu_quot(y[5], rs),
+                                      silu_quot(y[6], rs), silu_quot(y[7], rs))};
         __builtin_nontemporal_store(o, reinterpret_cast<v2i*>(Q + (int64_t)m * q_ld + j0 + seg * 8));
         if (seg == 0) Qs[(int64_t)(j0 >> 7) * qs_ld + m] = scale;
       }
@@ -922,10 +922,10 @@ __global__ __launch_bounds__(512) void gemm_fp8_k128q_kernel(
           const float scale = fp8_scale(amax);
           const float rs = recip(scale);
           if (m < M) {
-            const v2i o = {(int)pack4_fp8(div_by(y[0], scale, rs), div_by(y[1], scale, rs),
-                                          div_by(y[2], scale, rs), div_by(y[3], scale, rs)),
-                           (int)pack4_fp8(div_by(y[4], scale, rs), div_by(y[5], scale, rs),
-                                          div_by(y[6], scale, rs), div_by(y[7], scale, rs))};
+            const v2i o = {(int)pack4_fp8(silu_quot(y[0], rs), silu_quot(y[1], rs),
+                                          silu_quot(y[2], rs), silu_quot(y[3], rs)),
+                           (int)pack4_fp8(silu_quot(y[4], rs), silu_quot(y[5], rs),
+                                          silu_quot(y[6], rs), silu_quot(y[7], rs))};
             __builtin_nontemporal_store(o, reinterpret_cast<v2i*>(Q + (int64_t)m * q_ld + j0 +
                                                                  seg * 8));
             if (seg == 0) Qs[(int64_t)(j0 >> 7) * qs_ld + m] = scale;
@@ -1290,10 +1290,10 @@ __global__ __launch_bounds__(512) void gemm_fp8_promo_kernel(
           const float scale = fp8_scale(amax);
           const float rs = recip(scale);
           if (m < M) {
-            const v2i o = {(int)pack4_fp8(div_by(y[0], scale, rs), div_by(y[1], scale, rs),
-                                          div_by(y[2], scale, rs), div_by(y[3], scale, rs)),
-                           (int)pack4_fp8(div_by(y[4], scale, rs), div_by(y[5], scale, rs),
-                                          div_by(y[6], scale, rs), div_by(y[7], scale, rs))};
+            const v2i o = {(int)pack4_fp8(silu_quot(y[0], rs), silu_quot(y[1], rs),
+                                          silu_quot(y[2], rs), silu_quot(y[3], rs)),
+                           (int)pack4_fp8(silu_quot(y[4], rs), silu_quot(y[5], rs),
+                                          silu_quot(y[6], rs), silu_quot(y[7], rs))};
             __builtin_nontemporal_store(o, reinterpret_cast<v2i*>(Q + (int64_t)m * q_ld + j0 +
                                                                  seg * 8));
             if (seg == 0) Qs[(int64_t)(j0 >> 7) * qs_ld + m] = scale;

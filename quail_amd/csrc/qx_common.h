@@ -241,14 +241,22 @@ __device__ __forceinline__ float recip(float s) {
 }
 
 // silu(g) * u in fp32 (attention.py:771-793): sigmoid(g) = 1 / (1 + e^-g),
-// e^-g = 2^(-g log2 e) on v_exp_f32; past |g| ~ 88 the exponential
-// saturates to 0 or inf and sigmoid to 1 or 0. Shared by the SiLU-quant
-// kernel and the gate_up GEMM's fused epilogue so both give the same bits.
+// e^-g = 2^(-g log2 e) on v_exp_f32 and the reciprocal on v_rcp_f32 (each
+// within an ulp, as the reference's approximate exp and division are);
+// past |g| ~ 88 the exponential saturates to 0 or inf and sigmoid to 1 or
+// 0. Shared by the SiLU-quant kernel and the gate_up GEMM's fused epilogue
+// so both give the same bits.
 __device__ __forceinline__ float silu_mul(float g, float u) {
   constexpr float kLog2e = 1.4426950408889634f;
   const float d = 1.0f + __builtin_amdgcn_exp2f(-g * kLog2e);
-  return g * recip(d) * u;
+  return g * __builtin_amdgcn_rcpf(d) * u;
 }
+
+// y / s for the SiLU-quant rows as y times the scale's reciprocal r (within
+// an ulp and a half of the quotient; the fp8 code then differs from the
+// correctly rounded quotient's for about one value in a million, as the
+// reference's approximate division may). Shared like silu_mul.
+__device__ __forceinline__ float silu_quot(float y, float r) { return y * r; }
 
 // qk-norm and neox RoPE (attention.py:833-879) in pieces shared by the
 // qk-norm-rope pass and the attention's Q load, so both give the same bits;
@@ -292,9 +300,21 @@ __device__ __forceinline__ void bf16x4_to_f32(uint2 w, float (&x)[4]) {
   x[0] = lo_bf16(w.x); x[1] = hi_bf16(w.x); x[2] = lo_bf16(w.y); x[3] = hi_bf16(w.y);
 }
 
-// Per-group FP8 scale: max(amax, 1e-10) / 448 (attention.py:780-781).
+// Per-group FP8 scale: max(amax, 1e-10) / 448 (attention.py:780-781),
+// correctly rounded as the division is, in four operations instead of the
+// division's ten: x / 448 = (x / 7) * 2^-6 exactly for these x (normal,
+// and so are the quotients), and x / 7 is x * RN(1/7) corrected by one
+// fma of the remainder, which gives the correctly rounded quotient for
+// every fp32 significand (checked exhaustively). inf stays inf (the
+// remainder of inf is NaN).
 __device__ __forceinline__ float fp8_scale(float amax) {
-  return fmaxf(amax, kScaleFloor) / kFp8Max;
+#pragma clang fp contract(off)
+  static_assert(kFp8Max == 448.0f, "448 = 7 * 2^6");
+  constexpr float kSeventh = 1.0f / 7.0f;
+  const float x = fmaxf(amax, kScaleFloor);
+  const float q0 = x * kSeventh;
+  const float q = __builtin_fmaf(__builtin_fmaf(-q0, 7.0f, x), kSeventh, q0);
+  return (q0 == __builtin_inff() ? q0 : q) * 0.015625f;
 }
 
 }  // namespace qx

@@ -362,12 +362,12 @@ __global__ __launch_bounds__(256) void group_quant_kernel(const uint16_t* __rest
   amax = group_max<16>(amax);
   const float scale = fp8_scale(amax);
   const float rs = recip(scale);
+  // the SiLU rows divide as the gate_up GEMM's fused epilogue does
+  auto quot = [&](float v) { return SILU ? silu_quot(v, rs) : div_by(v, scale, rs); };
   if (live) {
     uint2 o;
-    o.x = pack4_fp8(div_by(y[0], scale, rs), div_by(y[1], scale, rs), div_by(y[2], scale, rs),
-                    div_by(y[3], scale, rs));
-    o.y = pack4_fp8(div_by(y[4], scale, rs), div_by(y[5], scale, rs), div_by(y[6], scale, rs),
-                    div_by(y[7], scale, rs));
+    o.x = pack4_fp8(quot(y[0]), quot(y[1]), quot(y[2]), quot(y[3]));
+    o.y = pack4_fp8(quot(y[4]), quot(y[5]), quot(y[6]), quot(y[7]));
     *reinterpret_cast<uint2*>(q + (int64_t)row * q_ld + col) = o;
     if ((lane & 15) == 0) scales[(int64_t)(col >> 7) * s_ld + row] = scale;
   }
