@@ -405,6 +405,25 @@ def test_group_quant_matches_and_zero_group_floor():
     assert s[3, 2].item() == np.float32(1e-10) / np.float32(448)
 
 
+def test_group_scales_equal_the_division_bit_for_bit():
+    """The kernels form max(amax, 1e-10) / 448 without a division; over
+    groups whose maxima span the bf16 range (2^-30 .. 2^127, and the floor)
+    every scale must equal torch's fp32 division exactly, and the codes the
+    reference's."""
+    g = _gen(13)
+    rows = 64
+    x = torch.randn(rows, 1024, generator=g)
+    exps = torch.linspace(-30, 125, rows * 8).round().view(rows, 8)
+    x = (x.view(rows, 8, 128) * torch.exp2(exps)[..., None]).view(rows, 1024)
+    x[5, :128] = 0
+    x = x.to(torch.bfloat16)
+    eng = _engine()
+    q, s = eng.quant(x.to(DEV))
+    q_ref, s_ref = ofp8.group_quant(x.float())
+    assert torch.equal(s.cpu().view(torch.int32), s_ref.view(torch.int32))
+    _fp8_close(q, s, q_ref, s_ref, min_equal=1.0)
+
+
 # ---- qk norm + rope -----------------------------------------------------------------
 
 @pytest.mark.parametrize("hq,hk,d", [(4, 2, 64), (32, 8, 128), (64, 8, 128)])
