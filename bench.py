@@ -524,6 +524,10 @@ def main():
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     pipe.engine.gemm_timer = None
+    host = {k: sum(st.get(k, 0.0) for st in stats) / len(stats) * 1e3
+            for k in ("admission_s", "pack_s")}
+    log("host work per step (overlapped with the GPU after the first pack): " +
+        ", ".join(f"{k[:-2]} {v:.1f} ms" for k, v in host.items()))
 
     gemm_ms = 0.0
     gemm_flops = 0.0

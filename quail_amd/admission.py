@@ -35,6 +35,7 @@ question is answered is finished.
 
 from bisect import bisect_right
 from collections import deque
+from itertools import accumulate
 
 import numpy as np
 
@@ -84,13 +85,15 @@ class StageAdmission:
         self.tree_shared = [0] * n if tree is None else [int(s) for s in tree.shared]
         page = arena.page_tokens
         self.flen = [len(p) for p in self.prefixes]
-        self.cum = [np.concatenate(([0], np.cumsum([len(s) for s in sufs]))).astype(np.int64)
-                    for sufs in self.suffixes]
+        # per document, the questions' cumulative rows and (below) temporary
+        # pages, as plain int lists (bisected per pass; built once per stage
+        # for every document, so kept out of numpy's per-call cost)
+        self.cum = [list(accumulate((len(s) for s in sufs), initial=0)) for sufs in self.suffixes]
         # temporary pages per question: its rows past the document's last
         # partial page (admission.py:54-62)
-        self.page_cum = [np.concatenate(([0], np.cumsum(
-            [arena.pages_needed(self.flen[d] % page + len(s)) for s in self.suffixes[d]])))
-            .astype(np.int64) for d in range(n)]
+        self.page_cum = [list(accumulate((-(-(self.flen[d] % page + len(s)) // page)
+                                          for s in self.suffixes[d]), initial=0))
+                         for d in range(n)]
         # the attention kernel's page-table row: longer documents are
         # refused here, not at their first attention launch
         max_keys = _lib.count("qx_paged_attention_max_keys", page)
@@ -100,18 +103,19 @@ class StageAdmission:
         for d in range(n):
             if not self.suffixes[d]:
                 raise OversizedDocumentError(d, "no question")
-            longest = int(np.diff(self.cum[d]).max())
+            longest = max(len(s) for s in self.suffixes[d])
             if longest > self.chunk_budget:
                 raise OversizedDocumentError(
                     d, f"its {longest}-token question exceeds the {self.chunk_budget}-token "
                        f"pack")
             need = arena.pages_needed(self.flen[d] + self.extra)
-            largest = int(np.diff(self.page_cum[d]).max()) if self.temporary_pages else 0
+            pc = self.page_cum[d]
+            largest = max(b - a for a, b in zip(pc, pc[1:])) if self.temporary_pages else 0
             if need + largest > arena.num_pages:
                 raise OversizedDocumentError(
                     d, f"{need + largest} KV pages, more than the {arena.num_pages} of the "
                        f"whole arena")
-            keys = self.flen[d] + int(self.cum[d][-1])
+            keys = self.flen[d] + self.cum[d][-1]
             if keys > max_keys:
                 raise OversizedDocumentError(
                     d, f"{keys} tokens, more keys than the paged attention's {max_keys} "
@@ -120,7 +124,7 @@ class StageAdmission:
             self.page_reserve = max(self.page_reserve, largest)
             # the fewest rows it can pack fresh: past a borrow, with its
             # first question; a document longer than a pack fits any room
-            least = max(0, self.flen[d] - self.tree_shared[d]) + int(self.cum[d][1])
+            least = max(0, self.flen[d] - self.tree_shared[d]) + self.cum[d][1]
             self.min_fresh = min(self.min_fresh, 1 if least > self.chunk_budget else least)
         self.state = [QUEUED] * n
         self.next_q = [0] * n
