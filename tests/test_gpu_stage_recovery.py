@@ -60,7 +60,9 @@ def _run(model, prefixes, suffixes, num_pages, budget, retained=(), optimism=0):
     run = OptimisticRun(pipe, arena, readout, prefixes, suffixes, budget)
     results = run.run()
     torch.cuda.synchronize()
-    margins = np.array([[a[0] - a[1] for a in r] for r in results], dtype=np.float64)
+    # a document asked one question gets its answer, one asked several the list
+    margins = np.array([[a[0] - a[1] for a in (r if isinstance(r, list) else [r])]
+                        for r in results], dtype=np.float64)
     assert arena.free_pages + arena.retained_pages == arena.num_pages
     return margins, run, arena
 
@@ -102,3 +104,29 @@ def test_pieces_evictions_and_splits_give_the_same_answers():
         assert np.sum(d > TOL) <= 2
         clear = np.abs(want) > TOL
         assert np.all((got[clear, j] > 0) == (want[clear] > 0))
+
+
+@pytest.mark.parametrize("length", [36_000, 40_900])
+def test_a_document_past_32k_keys_in_pieces_equals_it_whole(length):
+    """One document longer than two packs (Qwen3-4B's layer shapes, one
+    layer, a 4096-token vocabulary), its 2-token question at positions up
+    to 40,901: prefilled in 16,384-row pieces, its last piece's rows and
+    question read 2250-2557 pages of its own (past the 2048 of a 32,768-key
+    page table), and the answer must equal bit for bit the same document
+    packed whole in one 40,960-row pass (every kernel row-local, the keys
+    read in the same 64-key tiles either way)."""
+    import dataclasses
+    cfg = dataclasses.replace(CONFIGS["qwen3-4b"], layers=1, vocab=4096)
+    model = build_synthetic(cfg, seed=3, device="cuda", gen_device="cpu", norm_init="random")
+    rng = np.random.default_rng(length)
+    doc = rng.integers(12, cfg.vocab, length + 2).astype(np.int64)
+    prefixes, suffixes = [doc[:-2]], [[doc[-2:]]]
+    pages = -(-(length + 2) // 16) + 8
+    print(f"case: one {length}-token document, 16384-row pieces, {pages}-page arena", flush=True)
+    got, run, _ = _run(model, prefixes, suffixes, pages, 16384)
+    assert run.stats["prefill_pieces"] >= 2
+    print(f"case: the same document whole, one {length + 2}-row pass", flush=True)
+    whole, wrun, _ = _run(model, prefixes, suffixes, pages, 40960)
+    assert wrun.stats["chunks"] == 1 and wrun.stats["prefill_pieces"] == 0
+    assert np.all(np.isfinite(got))
+    assert np.array_equal(got, whole)
