@@ -10,7 +10,8 @@ bit run alone as packed with the others and borrowing the shared prefix
 (every kernel is row-local, and a row's attention does not depend on the
 rows it shares a workgroup with); the tree path's AI.IF decisions equal
 the unified path's wherever the margin is clear of the tree path's extra
-roundings. Checked against the oracle: a few documents through all layers
+roundings; the Qwen3-4B stage again on the reference arena's bf16 V pages.
+Checked against the oracle: a few documents through all layers
 with the oracle run on the GPU as the checker (per-layer dequantization,
 no cached weights), in float64 (the exact value of the dequantized
 arithmetic) and in float32 (the reference torch path's own precision).
@@ -22,7 +23,8 @@ step, and 36 layers of that leave the float32 torch path itself rms 0.15-
 (margin spread ~1.0-1.5), growing with depth (rms 0.044 at one layer). So
 the bound is relative to that floor, measured in the test on the same
 documents: the engine's rms distance to the exact value at most 3x the
-float32 path's. Measured here: 1.17x (Qwen3-4B, 8 documents), 1.32x
+float32 path's. Measured here: 1.15x (Qwen3-4B, 8 documents; 1.21x on
+bf16 V pages), 1.32x
 (Qwen3-8B label logits), 0.96x (Qwen3-32B shape); on another sample of six
 Qwen3-4B documents 2.0-2.1x at every depth from 1 to 36 layers, as on the
 2-layer model (0.021 against 0.010).
@@ -82,9 +84,9 @@ def _within_floor(name, got, exact, f32, factor=3.0):
     assert dev <= factor * floor
 
 
-def _alone_equals_packed(model, wl, kind, packed, sample):
+def _alone_equals_packed(model, wl, kind, packed, sample, **kw):
     for d in sample:
-        alone, run = run_stage(model, _subset(wl, [d]), kind)
+        alone, run = run_stage(model, _subset(wl, [d]), kind, **kw)
         assert run.stats["borrowed_tokens"] == 0
         assert np.array_equal(np.asarray(alone[0]), np.asarray(packed[d])), d
 
@@ -117,6 +119,16 @@ def test_qwen3_4b_ai_if_workload():
     assert spread <= 2 * 3.0 * _rms(f32 - exact)
     clear = np.abs(m) > 3 * spread
     assert np.all((t[clear] > 0) == (m[clear] > 0))
+    # the whole stage again on the reference arena's own V pages (bf16, the
+    # PV product in bf16): the same bounds against the oracle, and packed
+    # equals alone on it too
+    b16, _ = run_stage(model, wl, "margins", v_dtype=torch.bfloat16)
+    mb = _margins(b16)
+    assert len(mb) == 512 and np.isfinite(mb).all()
+    print(f"qwen3-4b bf16 V vs fp16 V: rms {_rms(mb - m):.4f} "
+          f"decisions {np.mean((mb > 0) == (m > 0)):.4f}")
+    _within_floor("qwen3-4b margins, bf16 V pages (8 docs)", mb[few], exact, f32)
+    _alone_equals_packed(model, wl, "margins", b16, sample[:3], v_dtype=torch.bfloat16)
 
 
 def test_qwen3_8b_ai_classify_stage_at_full_depth():
