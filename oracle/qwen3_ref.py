@@ -24,9 +24,13 @@ Activations stay bf16 between kernels exactly where the reference stores
 bf16 (residual, GEMM outputs, q/k, attention output); FP8 activation
 quantization is kept, so FP8 rounding matches the GPU path.
 
-Parity unpinned here (no reference test or vector exists for Qwen3): the
-accumulation order of DeepGEMM and FlashAttention, and vLLM's rms_norm /
-per-token quant internals; they are restated as the closed forms above.
+Pinned: every function here against an independent statement of it
+(tests/test_oracle_pins.py: transformers' Qwen3 RMSNorm, rotary embedding
+and layer order, torch's scaled-dot-product attention over shuffled pages,
+a block-by-block float64 GEMM, the fp8 code table by brute force). Parity
+unpinned here (no reference test or vector exists for Qwen3, and the
+libraries are absent): the accumulation order of DeepGEMM and
+FlashAttention inside a dot product; the oracle computes the exact sums.
 """
 
 from dataclasses import dataclass, field
