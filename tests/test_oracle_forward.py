@@ -3,7 +3,6 @@ packs (borrowed prefix pages, scatter maps, block tables) and each
 document's prompt run whole. Runs on the CPU with the tiny configuration,
 so pack metadata is pinned numerically without a GPU."""
 
-import numpy as np
 import torch
 
 from oracle import qwen3_ref as ref
@@ -49,4 +48,4 @@ def test_paged_pack_forward_equals_whole_documents():
     rows = m.head[[10, 11]]
     y1, n1, _, _ = ref.answer(paged, rows, [1, 0])
     y2, n2, _, _ = ref.answer(dense, rows, [1, 0])
-    assert np.abs((y1 - n1) - (y2 - n2)).max() <= 0.05
+    assert ((y1 - n1) - (y2 - n2)).abs().max().item() <= 0.05
