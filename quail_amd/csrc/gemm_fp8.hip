@@ -1128,11 +1128,21 @@ __global__ __launch_bounds__(512) void gemm_fp8_promo_kernel(
 #pragma unroll
     for (int j = 0; j < kLoadOps; ++j) load_op(issued, j);
   }
-  // Blocks alternate between the two stages across tiles: the block after
-  // a tile's last (the next tile's first) is loaded into the other stage
-  // while the last one is consumed, and the epilogue stages the tile
-  // through the last block's stage.
+  // Blocks alternate between the two stages across tiles. The next block's
+  // fragments are read, and the block after it is loaded, while the last
+  // weight tile's MFMAs of the current block run: every wave has read its
+  // last operand of the current block by then, so one barrier there frees
+  // the block's stage for the loads and lets the next block start with its
+  // fragments in registers (a barrier and the fragment reads at each
+  // block's start left the matrix cores idle there: 1-6% slower, same
+  // bits). A tile's first block (after the epilogue, which stages the tile
+  // through the stage of its last block) starts with the barrier and its
+  // reads.
+  constexpr int kLast = (TN - 1) * TM;  // the last weight tile's first MFMA
+  constexpr int kEarly = TM - 1;        // loads issued in that tile's other slots
+  static_assert(kLoadOps > kEarly, "load split");
   int stage = 0;
+  v8i wf, wf_next, af[TM];
   for (int it = 0; it < my_tiles; ++it) {
     int nm0 = m0, nn0 = n0;
     const bool has_next = it + 1 < my_tiles;
@@ -1143,64 +1153,83 @@ __global__ __launch_bounds__(512) void gemm_fp8_promo_kernel(
     for (int a = 0; a < TN; ++a)
 #pragma unroll
       for (int b = 0; b < TM; ++b) tot[a][b] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-    for (int kb = 0; kb < KT; ++kb) {
-      // this block's operands are done: a tile's first block (but the
-      // workgroup's first) was waited for before the previous tile's
-      // epilogue stores, which drain under this block instead
-      if (kb > 0 || it == 0) wait_vmcnt<0>();
-      lds_barrier();
-      // the next block: this tile's, or after its last the next tile's
-      // first; after the workgroup's last block, the current block again
-      // (into the free stage: loads with no branch around them, drained
-      // before the end)
-      Blk nb = issued;
+    // the block after `from` (block kb of this tile) into stage `to`: its K
+    // neighbour, or after the tile's last the next tile's first; after the
+    // workgroup's last block, block kb again (into a free stage: loads with
+    // no branch around them, drained before the end)
+    auto after = [&](const Blk& from, int kb, int to) {
+      Blk b = from;
       if (kb + 1 < KT) {
-        nb.a += 128;
-        nb.w += 128;
-        nb.sa += sa_ld;
-        nb.sw += 1;
-        nb.buf = smem + (stage ^ 1) * Cfg::kStage;
+        b.a += 128;
+        b.w += 128;
+        b.sa += sa_ld;
+        b.sw += 1;
+        b.buf = smem + to * Cfg::kStage;
       } else {
-        nb = has_next ? block_of(nm0, nn0, 0, stage ^ 1) : block_of(m0, n0, kb, stage ^ 1);
+        b = has_next ? block_of(nm0, nn0, 0, to) : block_of(m0, n0, kb, to);
       }
-      issued = nb;
+      return b;
+    };
+    // block kb of the tile. pre: its fragments were read during the
+    // previous block, and its first kEarly loads issued there; fetch: the
+    // block after the next is this tile's (or the next tile's first), so
+    // its loads start during this block's last weight tile
+    // (wave-uniform flags: one copy of the block's code, whose registers
+    // the 256-VGPR budget holds)
+    for (int kb = 0; kb < KT; ++kb) {
+      const bool pre = kb > 0;
+      const bool fetch = kb + 1 < KT;
       const uint8_t* a_lds = smem + stage * Cfg::kStage;
       const uint8_t* w_lds = a_lds + Cfg::kABytes;
       const float* sa_lds = reinterpret_cast<const float*>(w_lds + Cfg::kWBytes);
-      // the block's scales (the wave's weight scale came with its token
-      // scales, in the slot past them), then the fragments in the order the
-      // first MFMAs use them: weight tile 0, the token tiles, weight tile 1
-      // (reading the weight fragments two tiles ahead hides the LDS latency
-      // that one ahead left exposed: 3-5% faster)
-      const float sw = sa_lds[wave * 64 + Cfg::kSaPerWave];
-      const float sw1 = BN == 320 ? sa_lds[wave * 64 + Cfg::kSaPerWave + 1] : 0.0f;
-      float sr[TM];
-#pragma unroll
-      for (int b = 0; b < TM; ++b) {
-        const int row = wm * TM * 16 + b * 16 + r16;
-        sr[b] = sa_lds[(row / Cfg::kSaPerWave) * 64 + row % Cfg::kSaPerWave];
-      }
-      v8i wf = read_frag16(w_lds, wn * TN * 16 + r16, q16);
-      v8i af[TM];
-#pragma unroll
-      for (int b = 0; b < TM; ++b) af[b] = read_frag16(a_lds, wm * TM * 16 + b * 16 + r16, q16);
+      const uint8_t* a_nxt = smem + (stage ^ 1) * Cfg::kStage;
+      const uint8_t* w_nxt = a_nxt + Cfg::kABytes;
       // weight fragments kAhead tiles ahead (one ahead in the 320-wide
       // kernel, whose 160 totals leave no registers for a third fragment:
       // measured 6-8% faster than two ahead there, or than a one-MFMA lag)
       constexpr int kAhead = BN == 256 ? 2 : 1;
-      v8i wf_next;
+      // the block whose loads this block issues (PRE: begun in the previous)
+      Blk nb = issued;
+      if (!pre) {
+        // this block's operands are done: a tile's first block (but the
+        // workgroup's first) was waited for before the previous tile's
+        // epilogue stores, which drain under this block instead
+        if (kb > 0 || it == 0) wait_vmcnt<0>();
+        lds_barrier();
+        nb = after(issued, kb, stage ^ 1);
+        issued = nb;
+        // its first loads here (the later ones go one per MFMA, as after a
+        // prefetched block, whose first ones the previous block issued)
+#pragma unroll
+        for (int j = 0; j < kEarly; ++j) load_op(nb, j);
+        // the fragments in the order the first MFMAs use them: weight tile
+        // 0, the token tiles, weight tile 1 (reading the weight fragments
+        // two tiles ahead hides the LDS latency that one ahead left
+        // exposed: 3-5% faster)
+        wf = read_frag16(w_lds, wn * TN * 16 + r16, q16);
+#pragma unroll
+        for (int b = 0; b < TM; ++b) af[b] = read_frag16(a_lds, wm * TM * 16 + b * 16 + r16, q16);
+      }
+      // weight tile 1 (read here after a prefetched block too: the registers
+      // that would hold it during the previous block's last tile are not free)
       if constexpr (kAhead == 2) wf_next = read_frag16(w_lds, wn * TN * 16 + 16 + r16, q16);
+      // the block's scales (the wave's weight scale came with its token
+      // scales, in the slot past them)
+      const float sw = sa_lds[wave * 64 + Cfg::kSaPerWave];
+      const float sw1 = BN == 320 ? sa_lds[wave * 64 + Cfg::kSaPerWave + 1] : 0.0f;
       float s[TM], s1[TM];
 #pragma unroll
       for (int b = 0; b < TM; ++b) {
-        s[b] = sr[b] * sw;
-        s1[b] = BN == 320 ? sr[b] * sw1 : 0.0f;
+        const int row = wm * TM * 16 + b * 16 + r16;
+        const float sr = sa_lds[(row / Cfg::kSaPerWave) * 64 + row % Cfg::kSaPerWave];
+        s[b] = sr * sw;
+        s1[b] = BN == 320 ? sr * sw1 : 0.0f;
       }
       // MFMA t (weight tile a = t / TM, token tile b = t % TM) writes
       // partial slot t % 3; each scheduling slot issues one MFMA and the
       // promotion of the partial two MFMAs older, so three partials are
       // live and the FMAs never wait on the MFMA just issued. Weight
-      // fragment a + 2 is read at the start of fragment a's MFMAs.
+      // fragment a + kAhead is read at the start of fragment a's MFMAs.
       constexpr int kLag = 2;
       v4f part[kLag + 1];
       auto promote = [&](int t) {
@@ -1212,6 +1241,11 @@ __global__ __launch_bounds__(512) void gemm_fp8_promo_kernel(
               __builtin_fmaf(sc, part[t % (kLag + 1)][e], tot[t / TM][t % TM][e]);
       };
       v8i wf_next2;
+      // the block loaded during this block's last weight tile (formed here:
+      // a branch among the slots would let the compiler move the
+      // promotions away from their MFMAs)
+      const Blk nb2 = fetch ? after(issued, kb + 1, stage) : issued;
+      issued = nb2;
 #pragma unroll
       for (int t = 0; t < TN * TM; ++t) {
         const int a = t / TM, b = t % TM;
@@ -1225,12 +1259,37 @@ __global__ __launch_bounds__(512) void gemm_fp8_promo_kernel(
         part[t % (kLag + 1)] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
             wf, af[b], v4f{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0, 0, 0, 0);
         if (t >= kLag) promote(t - kLag);
-        // the next block's loads, one per MFMA over the block's first
-        // slots: all of them issued at once after the barrier queue every
-        // wave behind the address unit while the matrix core waits
-        // (measured 7-14% slower), spread one per two or three MFMAs they
-        // land too close to the next barrier (3-8% slower)
-        if (t < kLoadOps) load_op(nb, t);
+        // the loads, one per MFMA over the block's first slots: all of them
+        // issued at once after the barrier queue every wave behind the
+        // address unit while the matrix core waits (measured 7-14% slower),
+        // spread one per two or three MFMAs they land too close to the next
+        // barrier (3-8% slower)
+        if (t + kEarly < kLoadOps) load_op(nb, t + kEarly);
+        if (t >= kLast) {
+          // the next block's reads after this slot's MFMA: the registers
+          // they fill are the ones it reads
+          __builtin_amdgcn_sched_barrier(0);
+          if (t == kLast) {
+            // this wave's loads of the next block have landed, and its
+            // reads of this block's operands are consumed (the weight
+            // fragment of this tile fed the MFMA just issued): after the
+            // barrier the next block is in LDS for every wave and this
+            // block's stage is free. In a tile's last block the next is
+            // the next tile's first, read here to no use (its first
+            // block reads it again after the epilogue, which stages the
+            // tile through this block's stage), and the loads below
+            // rewrite its first rows with the same bytes: the code of
+            // the slots has no branch, which would let the compiler move
+            // the promotions away from their MFMAs
+            wait_vmcnt<0>();
+            lds_barrier();
+            wf_next = read_frag16(w_nxt, wn * TN * 16 + r16, q16);
+          }
+          // token fragment b of the next block, into the registers of
+          // this block's, whose last MFMA was just issued
+          af[b] = read_frag16(a_nxt, wm * TM * 16 + b * 16 + r16, q16);
+          if (t > kLast) load_op(nb2, t - kLast - 1);
+        }
         __builtin_amdgcn_sched_barrier(0);
         if (b == TM - 1 && a + 1 < TN) {
           wf = wf_next;
@@ -1239,6 +1298,7 @@ __global__ __launch_bounds__(512) void gemm_fp8_promo_kernel(
       }
 #pragma unroll
       for (int t = TN * TM - kLag; t < TN * TM; ++t) promote(t);
+      wf = wf_next;
       stage ^= 1;
     }
 
