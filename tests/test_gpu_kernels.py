@@ -180,6 +180,26 @@ def test_gemm_wide_promotion_tiles_equal_config_30(m, n, k, monkeypatch):
         _bf16_close(outs[PROMOTION_WIDE_CONFIG], ref.gemm(q, s, ref.RefLinear(wq, ws)))
 
 
+@pytest.mark.parametrize("m,n,k", [(16294, 2560, 128), (16294, 2560, 256), (9000, 5120, 384)])
+def test_gemm_promotion_tile_boundaries_with_few_blocks(m, n, k, monkeypatch):
+    """Both promotion configs with one, two and three 128-K blocks per tile
+    and two or more tiles per workgroup: a tile's first block (no fragments
+    read ahead), its last (the next tile's first block read to no use, the
+    loads rewriting its first rows), and a tile whose first block is also
+    its last all meet at tile boundaries. Configs 30 and 31 bit-identical,
+    and the first and last 1500 rows (the last token tile partial) the
+    oracle's to the bf16 tolerance."""
+    q, s, wq, ws = _gemm_case(m, n, k, seed=m + n + k)
+    outs = {}
+    for config in (PROMOTION_CONFIG, PROMOTION_WIDE_CONFIG):
+        monkeypatch.setenv("QUAIL_GEMM_CONFIG", str(config))
+        outs[config] = _run_gemm(q, s, wq, ws).cpu()
+    assert torch.equal(outs[PROMOTION_CONFIG], outs[PROMOTION_WIDE_CONFIG])
+    lin = ref.RefLinear(wq, ws)
+    for rows in (slice(0, 1500), slice(m - 1500, m)):
+        _bf16_close(outs[PROMOTION_WIDE_CONFIG][rows], ref.gemm(q[rows], s[rows], lin))
+
+
 @pytest.mark.parametrize("m,n,k", [(1, 640, 256), (300, 640, 512), (700, 1920, 1152)])
 def test_gemm_wide_promotion_tiles_at_widths_only_320_divides(m, n, k, monkeypatch):
     """Widths that are multiples of 320 but not of 256 take config 31 (the
@@ -223,7 +243,9 @@ def test_gemm_configs_agree_with_zero_weight_blocks(monkeypatch):
 
 
 @pytest.mark.parametrize("m,i,k,zero_blocks", [(700, 768, 512, False), (333, 1536, 256, True),
-                                               (2000, 9728, 2560, False)])
+                                               (2000, 9728, 2560, False),
+                                               (9000, 1280, 128, False),
+                                               (9000, 1280, 256, False)])
 @pytest.mark.parametrize("config", ["10", "22", "30"])
 def test_gate_up_swiglu_quant_equals_gemm_then_activation_quant(m, i, k, zero_blocks, config,
                                                                  monkeypatch):
