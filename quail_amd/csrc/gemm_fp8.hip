@@ -1188,13 +1188,13 @@ __global__ __launch_bounds__(512) void gemm_fp8_promo_kernel(
       // kernel, whose 160 totals leave no registers for a third fragment:
       // measured 6-8% faster than two ahead there, or than a one-MFMA lag)
       constexpr int kAhead = BN == 256 ? 2 : 1;
-      // the block whose loads this block issues (PRE: begun in the previous)
+      // the block whose loads this block issues (pre: begun in the previous)
       Blk nb = issued;
       if (!pre) {
         // this block's operands are done: a tile's first block (but the
         // workgroup's first) was waited for before the previous tile's
         // epilogue stores, which drain under this block instead
-        if (kb > 0 || it == 0) wait_vmcnt<0>();
+        if (it == 0) wait_vmcnt<0>();
         lds_barrier();
         nb = after(issued, kb, stage ^ 1);
         issued = nb;
