@@ -1249,16 +1249,23 @@ __global__ __launch_bounds__(512) void gemm_fp8_promo_kernel(
 #pragma unroll
       for (int t = 0; t < TN * TM; ++t) {
         const int a = t / TM, b = t % TM;
-        if constexpr (kAhead == 2) {
-          if (b == 0 && a + 2 < TN)
-            wf_next2 = read_frag16(w_lds, wn * TN * 16 + (a + 2) * 16 + r16, q16);
-        } else {
+        if constexpr (kAhead == 1) {
           if (b == 0 && a + 1 < TN)
             wf_next = read_frag16(w_lds, wn * TN * 16 + (a + 1) * 16 + r16, q16);
         }
         part[t % (kLag + 1)] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
             wf, af[b], v4f{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0, 0, 0, 0);
         if (t >= kLag) promote(t - kLag);
+        if constexpr (kAhead == 2) {
+          // after the MFMA that takes fragment a: the compiler's wait for
+          // that fragment drains every LDS read in flight (the direct loads
+          // leave its LDS counting imprecise), so a read issued ahead of the
+          // MFMA would be waited for there too (0-2% slower)
+          if (b == 0 && a + 2 < TN) {
+            __builtin_amdgcn_sched_barrier(0);
+            wf_next2 = read_frag16(w_lds, wn * TN * 16 + (a + 2) * 16 + r16, q16);
+          }
+        }
         // the loads, one per MFMA over the block's first slots: all of them
         // issued at once after the barrier queue every wave behind the
         // address unit while the matrix core waits (measured 7-14% slower),
